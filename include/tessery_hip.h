@@ -1,0 +1,79 @@
+/* C ABI of libtessery_hip.so: tessery's native bridge, rebuilt on HIP for MI355X (gfx950).
+ *
+ * Every mi_* function keeps the name, argument list and 0/1 / NULL error convention of
+ * tessery's Objective-C++ runtime (src/metal_inference/native/runtime.mm:42-297), whose ctypes
+ * signatures are declared in src/metal_inference/metal.py:42-83. A caller that binds those
+ * signatures binds this library unchanged. Plain pointers and sizes only: no HIP, torch or
+ * Python types cross this boundary.
+ *
+ * Execution model: mi_begin opens a command, mi_dispatch validates one kernel launch and queues
+ * it, mi_finish launches the queued kernels in order on the runtime's HIP stream and waits for
+ * them (the counterpart of commit + waitUntilCompleted, runtime.mm:217-253). mi_abort discards
+ * queued, unlaunched work. Buffers are device (HBM) allocations: mi_buffer uploads, mi_read
+ * downloads, both synchronous.
+ */
+#ifndef TESSERY_HIP_H
+#define TESSERY_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Version of this ABI; bumped whenever a signature or Params meaning changes. The Python
+ * loader refuses a library whose version differs (tessery's stale-ABI check, metal.py:84-90). */
+int mi_abi_version(void);
+
+/* runtime.mm:43-59 mi_create. `source` is accepted and ignored: kernels are compiled ahead of
+ * time for gfx950. Returns NULL when no gfx950 device is visible. */
+void *mi_create(const char *source);
+/* runtime.mm:61-63 */
+void mi_destroy(void *runtime);
+
+/* runtime.mm:65-75. Device allocation of `size` bytes; `bytes` (host, may be NULL) is copied in,
+ * otherwise the buffer is zero-filled. NULL on failure or size == 0. */
+void *mi_buffer(void *runtime, const void *bytes, uint64_t size);
+/* runtime.mm:77-79 */
+void mi_free(void *buffer);
+/* runtime.mm:81-86. Copies the first `bytes` bytes of the buffer to host memory `output`. */
+int mi_read(void *buffer, void *output, uint64_t bytes);
+
+/* runtime.mm:88-107 */
+int mi_begin(void *runtime);
+/* runtime.mm:109-146. `name` selects a route (kernel), `buffers` are mi_buffer handles bound in
+ * order, `parameters` is the 64-byte Params block (kernels.metal:5-8), `threads`/`group` follow
+ * the reference thread formulas (metal.py:532-569, 416-499) and are validated against them.
+ * Shapes implied by Params/threads are checked against buffer sizes before anything launches. */
+int mi_dispatch(void *runtime, const char *name, void **buffers, uint32_t count,
+                const void *parameters, uint32_t size, uint64_t threads, uint32_t group);
+/* runtime.mm:217-253 */
+int mi_finish(void *runtime);
+/* runtime.mm:285-287. Seconds between the first and last launch of the last finished command,
+ * from HIP events on the runtime stream; negative when unavailable. */
+double mi_gpu_seconds(void *runtime);
+/* runtime.mm:289-296 */
+void mi_abort(void *runtime);
+
+/* runtime.mm:256-276. Per-dispatch HIP-event timing, at most 2048 dispatches per command. */
+int mi_profile_enable(void *runtime, int enabled);
+/* runtime.mm:278-283 */
+int mi_profile_read(void *runtime, double *seconds, uint32_t count);
+
+/* runtime.mm:148-215. Prepared plans hold route ids, Params and binding slots, never buffers. */
+void *mi_plan_create(void *runtime, void **buffers, uint32_t count);
+int mi_plan_add(void *plan, const char *name, const uint32_t *slots, uint32_t count,
+                const void *params, uint64_t threads, uint32_t group);
+uint64_t mi_plan_bytes(void *plan);
+void mi_plan_free(void *plan);
+int mi_plan_run(void *runtime, void *plan, void **buffers, uint32_t count);
+
+/* No counterpart in the reference (unified memory made it unnecessary there): copy `bytes`
+ * host bytes into an existing device buffer, synchronously. */
+int mi_write(void *buffer, const void *bytes, uint64_t size);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TESSERY_HIP_H */

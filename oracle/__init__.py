@@ -1,0 +1,21 @@
+"""CPU oracle of tessery's prefill-attention path (float64 NumPy).
+
+TEST INFRASTRUCTURE ONLY. It is imported by tests/, by __graft_entry__.smoke() and by bench.py's
+CPU-baseline leg, and only as the checker or the timed CPU baseline. The product path
+(tessery_amd) never imports, calls or falls back to it.
+
+Modules and what pins each one (the tests under tests/test_oracle_*.py run these checks):
+  attention   per-(batch, head) softmax attention with tessery's mask / padding / GQA semantics.
+              Pinned by torch.nn.functional.scaled_dot_product_attention (float64, enable_gqa,
+              explicit tril & key-padding masks), the closed-form known answers of tessery's
+              extreme-logit test (test_kernels.py:213-253) and a scalar online-softmax loop.
+  norm_rope   per-head RMSNorm and split-half RoPE. Pinned by torch.nn.functional.rms_norm,
+              transformers' Qwen3RMSNorm / apply_rotary_pos_emb, a complex-number rotation and
+              rotation invariants.
+  quant4      uint4 group-64 packing, dequantization and projection. Pinned by tessery's
+              known-answer tests (test_kernels.py:55-81, 759-776) and a scalar restatement of
+              the kernel indexing (kernels.metal:11-19).
+  qwen_block  composition QKV projection -> q/k norm + RoPE -> attention (qwen3.py:194-245),
+              pinned through the three modules above.
+No function here is "parity unpinned".
+"""

@@ -1,0 +1,42 @@
+"""float64 per-head RMSNorm and rotary position embedding.
+
+rms_norm: y = x / sqrt(mean(x^2) + eps) * w           (kernels.metal:53-63; closed form of
+                                                        test_kernels.py:109)
+rope:     split-half pairs (c, c + D/2), angle = pos * theta^(-2c/D),
+          x_c' = x_c cos - x_{c+D/2} sin, x_{c+D/2}' = x_c sin + x_{c+D/2} cos
+                                                       (kernels.metal:65-74; test_kernels.py:273-283)
+Positions are the token's index within its padded row, so padded tokens get positions too.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+from numpy.typing import NDArray
+
+
+def rms_norm(x: NDArray, weight: NDArray, eps: float) -> NDArray[np.float64]:
+    x = np.asarray(x, dtype=np.float64)
+    inv = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    return x * inv * np.asarray(weight, dtype=np.float64)
+
+
+def rope_angles(seq: int, dim: int, theta: float) -> NDArray[np.float64]:
+    """[seq, dim/2] angles pos * theta^(-2c/dim)."""
+    inv_freq = float(theta) ** (-2.0 * np.arange(dim // 2, dtype=np.float64) / dim)
+    return np.arange(seq, dtype=np.float64)[:, None] * inv_freq[None, :]
+
+
+def rope(x: NDArray, theta: float) -> NDArray[np.float64]:
+    """x [B, S, heads, D] (position = axis 1) -> rotated float64."""
+    x = np.asarray(x, dtype=np.float64)
+    seq, dim = x.shape[1], x.shape[-1]
+    half = dim // 2
+    angles = rope_angles(seq, dim, theta)[None, :, None, :]
+    cos, sin = np.cos(angles), np.sin(angles)
+    a, b = x[..., :half], x[..., half:]
+    return np.concatenate((a * cos - b * sin, a * sin + b * cos), axis=-1)
+
+
+def norm_rope(x: NDArray, weight: NDArray, eps: float, theta: float) -> NDArray[np.float64]:
+    """Qwen3 order (qwen3.py:216-237): RMSNorm over D, then RoPE."""
+    return rope(rms_norm(x, weight, eps), theta)

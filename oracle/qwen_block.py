@@ -1,0 +1,35 @@
+"""float64 composition of tessery's Qwen3 attention block (qwen3.py:194-245):
+QKV projection -> per-head q/k RMSNorm -> RoPE -> causal GQA attention.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+from numpy.typing import NDArray
+
+from . import attention as _attention
+from . import norm_rope as _norm_rope
+from . import quant4 as _quant4
+
+
+def norm_rope_attention(
+    q_pre: NDArray,
+    k_pre: NDArray,
+    v: NDArray,
+    lengths: NDArray,
+    q_norm: NDArray,
+    k_norm: NDArray,
+    *,
+    eps: float,
+    theta: float,
+    bidirectional: bool = False,
+) -> NDArray[np.float64]:
+    """q_pre [B,S,H,D], k_pre/v [B,S,KV,D]; norm weights as float values [D]."""
+    q = _norm_rope.norm_rope(q_pre, q_norm, eps, theta)
+    k = _norm_rope.norm_rope(k_pre, k_norm, eps, theta)
+    return _attention.attention(q, k, v, lengths, bidirectional=bidirectional)
+
+
+def qkv4(x: NDArray, weights: dict[str, tuple[NDArray, NDArray, NDArray]], kind: str):
+    """x [M, K]; weights name -> (packed, scales, biases) for "q", "k", "v"."""
+    return {name: _quant4.linear4(x, *weights[name], kind=kind) for name in ("q", "k", "v")}

@@ -1,0 +1,85 @@
+"""Ahead-of-time build of libtessery_hip.so for gfx950 (MI355X).
+
+Every HIP source under csrc/ is compiled with hipcc into objects under tessery_amd/_build/ and
+linked into tessery_amd/libtessery_hip.so, which the ctypes loader in runtime.py opens. The
+library always builds in-tree so that it travels with the source tree to a GPU host.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PACKAGE = Path(__file__).resolve().parent
+ROOT = PACKAGE.parent
+CSRC = PACKAGE / "csrc"
+BUILD = PACKAGE / "_build"
+LIBRARY = PACKAGE / "libtessery_hip.so"
+
+SOURCES = ("attention.hip", "norm_rope.hip", "linear4.hip", "util.hip", "runtime.cpp")
+
+# -packed-fp32-ops keeps the device compiler from emitting packed fp32 VALU instructions.
+FLAGS = (
+    "--offload-arch=gfx950",
+    "-O3",
+    "-fPIC",
+    "-std=c++17",
+    "-Wall",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+)
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(path).exists():
+        raise RuntimeError("hipcc not found; the ROCm toolchain is required to build")
+    return path
+
+
+def _compile(source: str) -> Path:
+    obj = BUILD / (source + ".o")
+    cmd = [
+        hipcc(),
+        *FLAGS,
+        "-x",
+        "hip",
+        "-I",
+        str(ROOT / "include"),
+        "-I",
+        str(CSRC),
+        "-c",
+        str(CSRC / source),
+        "-o",
+        str(obj),
+    ]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode:
+        raise RuntimeError(f"hipcc failed for {source}:\n{result.stderr}")
+    return obj
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every kernel source for gfx950 and link the shared library; returns its path."""
+    BUILD.mkdir(exist_ok=True)
+    jobs = min(len(SOURCES), max(1, (os.cpu_count() or 1)), 8)
+    with ThreadPoolExecutor(jobs) as pool:
+        objects = list(pool.map(_compile, SOURCES))
+    tmp = LIBRARY.with_suffix(".so.tmp")
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode:
+        raise RuntimeError(f"link failed:\n{result.stderr}")
+    os.replace(tmp, LIBRARY)
+    if verbose:
+        print(f"built {LIBRARY}")
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    build(verbose=True)

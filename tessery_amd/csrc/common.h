@@ -1,0 +1,42 @@
+// Shared definitions for the gfx950 prefill-attention kernels and the C-ABI runtime.
+//
+// Params mirrors tessery's 64-byte kernel argument block, `struct Params` in
+// src/metal_inference/native/kernels.metal:5-8, packed by MetalRuntime._dispatch with
+// struct format "<12I4f" (src/metal_inference/metal.py:596-614). The field order is part of
+// the drop-in boundary: callers pack the same 64 bytes and the runtime decodes them here.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tessery {
+
+struct Params {
+  uint32_t n, rows, cols, k, heads, kv_heads, seq, batch, dim, group, u0, u1;
+  float eps, theta, scale, reserved;
+};
+static_assert(sizeof(Params) == 64, "Params must stay 64 bytes");
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t uint4v __attribute__((ext_vector_type(4)));
+
+// BF16 storage word -> float (exact): tessery stores norm weights and uint4 scales/biases
+// as bfloat16 words (kernels.metal:10).
+__device__ __forceinline__ float bf16_to_float(uint16_t w) {
+  return __uint_as_float(static_cast<uint32_t>(w) << 16);
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+// log2(e) for exp2-based softmax.
+constexpr float kLog2e = 1.4426950408889634f;
+
+}  // namespace tessery

@@ -1,0 +1,74 @@
+// Host-side launch interface of the gfx950 kernels, used by the C-ABI runtime (runtime.cpp).
+// Every launcher enqueues on the given stream and returns hipGetLastError(); shapes are
+// validated by the caller before a launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.h"
+
+namespace tessery {
+
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const uint32_t* lengths;
+  void* out;
+  int B, S, H, KV, D;
+  float scale;
+  int bidi;
+  int in_f16;   // q/k/v are fp16 (else fp32)
+  int out_f16;  // out is fp16 (else fp32)
+  // Fused per-head RMSNorm + RoPE of Q (fp16 MFMA kernel only); null when unused.
+  const uint16_t* gamma_q;  // bf16 [D]
+  const float* rope_cos;    // [S, D/2]
+  const float* rope_sin;    // [S, D/2]
+  float eps;
+};
+
+hipError_t launch_attention_scalar(const AttnArgs& a, hipStream_t st);
+hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st);
+hipError_t launch_attention_f16(const AttnArgs& a, hipStream_t st);
+
+// tessery rms_norm (kernels.metal:53-63): rows x cols fp32, bf16 weight, out may alias x.
+hipError_t launch_rms_norm_f32(const float* x, const uint16_t* w, float* out, int rows, int cols,
+                               float eps, hipStream_t st);
+// tessery rope (kernels.metal:65-74): in place, split-half pairs, pos = (row / heads) % seq.
+hipError_t launch_rope_f32(float* x, const float* cos_tab, const float* sin_tab, uint32_t n,
+                           int heads, int seq, int dim, hipStream_t st);
+// Fused per-head RMSNorm + RoPE on fp16 rows [B,S,heads,D] -> fp16 rows, rows with
+// position >= lengths[b] skipped (they are padding that attention never reads).
+hipError_t launch_norm_rope_f16(const _Float16* x, _Float16* y, const uint16_t* gamma,
+                                const float* cos_tab, const float* sin_tab,
+                                const uint32_t* lengths, int B, int S, int heads, int D,
+                                float eps, hipStream_t st);
+
+// uint4 affine group-64 projection, fp32 activations, bf16 scale/bias (tessery linear4 family,
+// kernels.metal:11-19, 32-51, 489-605, 655-684, 733-773). Computes rows [row0, row1).
+hipError_t launch_linear4_f32(const float* x, const uint32_t* w, const uint16_t* scales,
+                              const uint16_t* biases, float* out, int row0, int row1, int cols,
+                              int k, hipStream_t st);
+
+// Fused uint4 QKV projection for fp16 activations: three weight sets, outputs written in the
+// attention layout. scale/bias words are fp16 (scale_bf16 = 0) or bf16 (scale_bf16 = 1).
+struct Qkv4Args {
+  const _Float16* x;  // [M, K]
+  const uint32_t* w[3];
+  const uint16_t* s[3];
+  const uint16_t* b[3];
+  _Float16* y[3];
+  int n[3];
+  int M, K;
+  int scale_bf16;
+};
+hipError_t launch_qkv4_f16(const Qkv4Args& a, hipStream_t st);
+
+// tessery add (kernels.metal:300-304): out[i] = a[i] + b[i], i < n. out may alias a or b.
+hipError_t launch_add_f32(const float* a, const float* b, float* out, uint32_t n, hipStream_t st);
+
+// Plain device copy (bytes % 16 == 0), used to calibrate HBM traffic counters.
+hipError_t launch_copy(const void* src, void* dst, uint64_t bytes, hipStream_t st);
+
+}  // namespace tessery

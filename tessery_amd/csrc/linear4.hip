@@ -1,0 +1,87 @@
+// uint4 affine group-64 projections for gfx950.
+//
+// Weight format (tessery weight4, kernels.metal:11-19): W packed u32[N, K/8]; nibble j of word
+// (n, k/8) is column 8*(k/8)+j, little-nibble first; group g = n*(K/64) + k/64;
+// w[n][k] = code * scale[g] + bias[g], scale/bias bfloat16 words [N, K/64].
+// y[t][n] = sum_k x[t][k] * w[n][k].
+//
+// linear4_f32 serves every tessery linear4 route name (linear4, linear4_tiled, linear4_tail,
+// linear4_16x32_k64, linear4_32x32_k64, linear4_small3): one kernel, one reduction order per
+// output element, so every route over the same rows produces bit-identical results.
+#include "common.h"
+#include "kernels.h"
+
+namespace tessery {
+
+// 256 threads = 4 wavefronts; tile 32 rows x 128 columns (32 columns per wavefront); the K loop
+// walks one quantization group (64) at a time. fp32 MFMA v_mfma_f32_32x32x2_f32 computes
+// Y = X * W^T with lane (column n = l%32, k-slot h = l/32); k-step t pairs k = 32h + t, so each
+// lane decodes 32 consecutive codes (four words) of its weight row per group.
+__global__ __launch_bounds__(256) void linear4_f32(const float* __restrict__ x,
+                                                   const uint32_t* __restrict__ w,
+                                                   const uint16_t* __restrict__ scales,
+                                                   const uint16_t* __restrict__ biases,
+                                                   float* __restrict__ out, int row0, int row1,
+                                                   int cols, int k) {
+  constexpr int XROW = 64 + 4;
+  __shared__ __attribute__((aligned(16))) float xs[32 * XROW];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int rbase = row0 + blockIdx.x * 32;
+  const int n = blockIdx.y * 128 + wave * 32 + l32;
+  const bool nvalid = n < cols;
+  const int groups = k / 64;
+  floatx16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+  for (int gi = 0; gi < groups; ++gi) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + 256 * i;  // 512 float4 chunks = 32 rows x 16
+      const int r = c / 16, ck = c % 16;
+      floatx4 t = {0.f, 0.f, 0.f, 0.f};
+      if (rbase + r < row1)
+        t = *reinterpret_cast<const floatx4*>(x + static_cast<size_t>(rbase + r) * k + gi * 64 + 4 * ck);
+      *reinterpret_cast<floatx4*>(&xs[r * XROW + 4 * ck]) = t;
+    }
+    __syncthreads();
+    float wv[32];
+    if (nvalid) {
+      const uint4v words =
+          *reinterpret_cast<const uint4v*>(w + static_cast<size_t>(n) * (k / 8) + gi * 8 + 4 * hh);
+      const size_t gidx = static_cast<size_t>(n) * groups + gi;
+      const float sc = bf16_to_float(scales[gidx]), bi = bf16_to_float(biases[gidx]);
+#pragma unroll
+      for (int t = 0; t < 32; ++t)
+        wv[t] = static_cast<float>((words[t >> 3] >> (4 * (t & 7))) & 15u) * sc + bi;
+    } else {
+#pragma unroll
+      for (int t = 0; t < 32; ++t) wv[t] = 0.0f;
+    }
+#pragma unroll
+    for (int c4 = 0; c4 < 8; ++c4) {
+      const floatx4 xa = *reinterpret_cast<const floatx4*>(&xs[l32 * XROW + 32 * hh + 4 * c4]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[t], wv[4 * c4 + t], acc, 0, 0, 0);
+    }
+  }
+  if (!nvalid) return;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int r = rbase + 8 * (e >> 2) + 4 * hh + (e & 3);
+    if (r < row1) out[static_cast<size_t>(r) * cols + n] = acc[e];
+  }
+}
+
+hipError_t launch_linear4_f32(const float* x, const uint32_t* w, const uint16_t* scales,
+                              const uint16_t* biases, float* out, int row0, int row1, int cols,
+                              int k, hipStream_t st) {
+  if (row1 <= row0 || cols <= 0) return hipSuccess;
+  if (k % 64) return hipErrorInvalidValue;
+  dim3 grid((row1 - row0 + 31) / 32, (cols + 127) / 128);
+  linear4_f32<<<grid, 256, 0, st>>>(x, w, scales, biases, out, row0, row1, cols, k);
+  return hipGetLastError();
+}
+
+}  // namespace tessery

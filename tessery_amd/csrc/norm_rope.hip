@@ -1,0 +1,147 @@
+// Per-head q/k RMSNorm and RoPE for gfx950.
+//
+//   rms_norm   y = x * rsqrt(mean(x^2) + eps) * bf16(w)        kernels.metal:53-63
+//   rope       split-half (NeoX) pairs (c, c + D/2), pos = (row / heads) % seq,
+//              angle = pos * theta^(-2c/D)                       kernels.metal:65-74
+// The Qwen3 attention block applies both, in place, to q ([tokens*H, D] rows) and to k
+// ([tokens*KV, D] rows) before attention (src/metal_inference/qwen3.py:216-237).
+//
+// cos/sin come from a [seq, D/2] table that the runtime computes once per (seq, D, theta) in
+// float64 on the host and rounds to float32, so the rotation is as accurate as a float64 angle.
+#include "common.h"
+#include "kernels.h"
+
+namespace tessery {
+
+// One wavefront per row, 4 rows per 256-thread workgroup. out may alias x.
+__global__ __launch_bounds__(256) void rms_norm_f32(const float* x, const uint16_t* __restrict__ w,
+                                                    float* out, int rows, int cols, float eps) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;  // row-uniform: the whole wavefront leaves together
+  const float* xr = x + static_cast<size_t>(row) * cols;
+  float squares = 0.0f;
+  for (int c = lane; c < cols; c += 64) {
+    const float val = xr[c];
+    squares += val * val;
+  }
+  const float inv = 1.0f / sqrtf(wave_sum(squares) / static_cast<float>(cols) + eps);
+  float* yr = out + static_cast<size_t>(row) * cols;
+  for (int c = lane; c < cols; c += 64) yr[c] = xr[c] * inv * bf16_to_float(w[c]);
+}
+
+__global__ __launch_bounds__(256) void rope_f32(float* x, const float* __restrict__ cos_tab,
+                                                const float* __restrict__ sin_tab, uint32_t n,
+                                                int heads, int seq, int dim) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t halfdim = static_cast<uint32_t>(dim) / 2;
+  const uint32_t row = i / halfdim, c = i % halfdim;
+  const uint32_t pos = (row / static_cast<uint32_t>(heads)) % static_cast<uint32_t>(seq);
+  const float cv = cos_tab[pos * halfdim + c], sv = sin_tab[pos * halfdim + c];
+  float* r = x + static_cast<size_t>(row) * dim;
+  const float a = r[c], b = r[c + halfdim];
+  r[c] = a * cv - b * sv;
+  r[c + halfdim] = a * sv + b * cv;
+}
+
+// fp16 rows [B,S,heads,D]; T = D/16 lanes per row, lane j owns channels 8j..8j+7 and their
+// RoPE partners D/2+8j..D/2+8j+7, so the rotation never leaves the lane. fp32 math.
+template <int D>
+__global__ __launch_bounds__(256) void norm_rope_f16(const _Float16* __restrict__ x,
+                                                     _Float16* __restrict__ y,
+                                                     const uint16_t* __restrict__ gamma,
+                                                     const float* __restrict__ cos_tab,
+                                                     const float* __restrict__ sin_tab,
+                                                     const uint32_t* __restrict__ lengths, int B,
+                                                     int S, int heads, float eps) {
+  constexpr int T = D / 16;
+  constexpr int HALF = D / 2;
+  const int tid = threadIdx.x;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / T) + tid / T;
+  const int j = tid % T;
+  const int64_t rows = static_cast<int64_t>(B) * S * heads;
+  bool valid = row < rows;
+  int pos = 0;
+  if (valid) {
+    const int64_t token = row / heads;
+    const int b = static_cast<int>(token / S);
+    pos = static_cast<int>(token % S);
+    valid = pos < static_cast<int>(min(lengths[b], static_cast<uint32_t>(S)));
+  }
+  half8 lo = {}, hi = {};
+  const size_t base = static_cast<size_t>(row) * D;
+  if (valid) {
+    lo = *reinterpret_cast<const half8*>(x + base + 8 * j);
+    hi = *reinterpret_cast<const half8*>(x + base + HALF + 8 * j);
+  }
+  float a[8], c[8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    a[m] = static_cast<float>(lo[m]);
+    c[m] = static_cast<float>(hi[m]);
+    ss += a[m] * a[m] + c[m] * c[m];
+  }
+#pragma unroll
+  for (int off = T / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  if (!valid) return;
+  const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+  const uint4v glo = *reinterpret_cast<const uint4v*>(gamma + 8 * j);
+  const uint4v ghi = *reinterpret_cast<const uint4v*>(gamma + HALF + 8 * j);
+  const float* cs = cos_tab + static_cast<size_t>(pos) * HALF + 8 * j;
+  const float* sn = sin_tab + static_cast<size_t>(pos) * HALF + 8 * j;
+  half8 olo, ohi;
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const int sh = 16 * (m & 1);
+    const float wl = bf16_to_float(static_cast<uint16_t>((glo[m >> 1] >> sh) & 0xffffu));
+    const float wh = bf16_to_float(static_cast<uint16_t>((ghi[m >> 1] >> sh) & 0xffffu));
+    const float p = a[m] * inv * wl, q = c[m] * inv * wh;
+    const float cv = cs[m], sv = sn[m];
+    olo[m] = static_cast<_Float16>(p * cv - q * sv);
+    ohi[m] = static_cast<_Float16>(p * sv + q * cv);
+  }
+  *reinterpret_cast<half8*>(y + base + 8 * j) = olo;
+  *reinterpret_cast<half8*>(y + base + HALF + 8 * j) = ohi;
+}
+
+hipError_t launch_rms_norm_f32(const float* x, const uint16_t* w, float* out, int rows, int cols,
+                               float eps, hipStream_t st) {
+  if (rows <= 0) return hipSuccess;
+  rms_norm_f32<<<(rows + 3) / 4, 256, 0, st>>>(x, w, out, rows, cols, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_f32(float* x, const float* cos_tab, const float* sin_tab, uint32_t n,
+                           int heads, int seq, int dim, hipStream_t st) {
+  if (!n) return hipSuccess;
+  rope_f32<<<(n + 255) / 256, 256, 0, st>>>(x, cos_tab, sin_tab, n, heads, seq, dim);
+  return hipGetLastError();
+}
+
+hipError_t launch_norm_rope_f16(const _Float16* x, _Float16* y, const uint16_t* gamma,
+                                const float* cos_tab, const float* sin_tab,
+                                const uint32_t* lengths, int B, int S, int heads, int D,
+                                float eps, hipStream_t st) {
+  const int64_t rows = static_cast<int64_t>(B) * S * heads;
+  if (!rows) return hipSuccess;
+  const int per_block = 256 / (D / 16);
+  const unsigned grid = static_cast<unsigned>((rows + per_block - 1) / per_block);
+  switch (D) {
+    case 32:
+      norm_rope_f16<32><<<grid, 256, 0, st>>>(x, y, gamma, cos_tab, sin_tab, lengths, B, S, heads, eps);
+      break;
+    case 64:
+      norm_rope_f16<64><<<grid, 256, 0, st>>>(x, y, gamma, cos_tab, sin_tab, lengths, B, S, heads, eps);
+      break;
+    case 128:
+      norm_rope_f16<128><<<grid, 256, 0, st>>>(x, y, gamma, cos_tab, sin_tab, lengths, B, S, heads, eps);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace tessery

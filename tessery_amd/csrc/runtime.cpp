@@ -1,0 +1,761 @@
+// C-ABI runtime of libtessery_hip.so: the HIP counterpart of tessery's Metal bridge
+// (src/metal_inference/native/runtime.mm). See include/tessery_hip.h for the contract of every
+// exported function.
+//
+// Design (MI355X): one HIP stream per runtime at default priority, device-resident buffers,
+// commands recorded on the host and launched back to back at mi_finish (so an aborted command
+// launches nothing), HIP events for command and per-dispatch timing. Routes are selected by
+// tessery's kernel names; each route decodes the 64-byte Params block, derives its batch size
+// from the reference thread formula and checks every buffer size before it may be queued.
+#include <hip/hip_runtime.h>
+
+#include <array>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <tuple>
+#include <utility>
+#include <vector>
+
+#include "kernels.h"
+#include "tessery_hip.h"
+
+using tessery::Params;
+
+namespace {
+
+constexpr int kAbiVersion = 1;
+constexpr uint32_t kMaxBuffers = 8;
+constexpr size_t kMaxProfiled = 2048;  // runtime.mm:118 (4096 timestamp samples, 2 per dispatch)
+constexpr size_t kMaxPlanOps = 2048;   // runtime.mm:166
+
+enum Route : int {
+  R_ATTENTION,
+  R_ATTENTION_TILED,
+  R_ATTENTION_TAIL_32,
+  R_ATTENTION_TAIL_128,
+  R_ATTENTION_F16,
+  R_ATTENTION_F16_SCALAR,
+  R_ATTENTION_F16_NORM_ROPE,
+  R_NORM_ROPE_F16,
+  R_RMS_NORM,
+  R_ROPE,
+  R_LINEAR4,
+  R_LINEAR4_TILED,
+  R_LINEAR4_TAIL,
+  R_LINEAR4_16X32,
+  R_LINEAR4_32X32,
+  R_LINEAR4_SMALL3,
+  R_QKV4_F16,
+  R_ADD,
+  R_COPY,
+  R_NONE
+};
+
+struct RouteName {
+  const char* name;
+  Route route;
+  uint32_t buffers;
+};
+
+const RouteName kRoutes[] = {
+    {"attention", R_ATTENTION, 5},
+    {"attention_tiled", R_ATTENTION_TILED, 5},
+    {"attention_tail_32", R_ATTENTION_TAIL_32, 5},
+    {"attention_tail_128", R_ATTENTION_TAIL_128, 5},
+    {"attention_f16", R_ATTENTION_F16, 5},
+    {"attention_f16_scalar", R_ATTENTION_F16_SCALAR, 5},
+    {"attention_f16_norm_rope", R_ATTENTION_F16_NORM_ROPE, 6},
+    {"norm_rope_f16", R_NORM_ROPE_F16, 4},
+    {"rms_norm", R_RMS_NORM, 3},
+    {"rope", R_ROPE, 1},
+    {"linear4", R_LINEAR4, 5},
+    {"linear4_tiled", R_LINEAR4_TILED, 5},
+    {"linear4_tail", R_LINEAR4_TAIL, 5},
+    {"linear4_16x32_k64", R_LINEAR4_16X32, 5},
+    {"linear4_32x32_k64", R_LINEAR4_32X32, 5},
+    {"linear4_small3", R_LINEAR4_SMALL3, 5},
+    {"qkv4_f16", R_QKV4_F16, 8},
+    {"add", R_ADD, 3},
+    {"copy", R_COPY, 2},
+};
+
+Route find_route(const char* name, uint32_t* nbuf) {
+  if (!name) return R_NONE;
+  for (const auto& r : kRoutes)
+    if (std::strcmp(r.name, name) == 0) {
+      *nbuf = r.buffers;
+      return r.route;
+    }
+  return R_NONE;
+}
+
+struct Runtime;
+
+struct Buffer {
+  void* ptr;
+  uint64_t size;
+  Runtime* owner;
+};
+
+struct Op {
+  Route route;
+  Params p;
+  uint64_t threads;
+  uint32_t group;
+  uint32_t count;
+  std::array<void*, kMaxBuffers> ptr;
+  std::array<uint64_t, kMaxBuffers> size;
+};
+
+struct RopeTable {
+  float* cos;
+  float* sin;
+};
+
+struct Runtime {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev_start = nullptr, ev_end = nullptr;
+  bool recording = false;
+  std::vector<Op> ops;
+  double last_gpu = -1.0;
+  bool profiling = false;
+  std::vector<hipEvent_t> prof_events;
+  std::vector<double> profile_seconds;
+  std::map<std::tuple<uint32_t, uint32_t, uint32_t>, RopeTable> rope;
+};
+
+struct PlanOp {
+  Route route;
+  Params p;
+  uint64_t threads;
+  uint32_t group;
+  uint32_t count;
+  std::array<uint32_t, kMaxBuffers> slots;
+};
+
+struct Plan {
+  Runtime* owner;
+  std::vector<uint64_t> sizes;
+  std::vector<PlanOp> ops;
+};
+
+inline uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+
+// ---- shape derivation -------------------------------------------------------------------------
+
+struct AttnShape {
+  uint64_t B, S, H, KV, D;
+  int in_f16, out_f16;
+};
+
+constexpr uint64_t kMaxTokens = 1ull << 31;
+
+bool attn_shape(Route r, const Params& p, uint64_t threads, uint32_t group, AttnShape* s) {
+  const uint64_t H = p.heads, KV = p.kv_heads, S = p.seq, D = p.dim;
+  if (!H || !KV || H % KV || !S || !D || H > 1024 || D > 1024 || S > (1u << 20)) return false;
+  uint64_t tokens = 0;
+  s->in_f16 = 0;
+  s->out_f16 = 0;
+  switch (r) {
+    case R_ATTENTION:  // metal.py:560-569, scalar: tokens*heads*32 threads, groups of 32
+      if (group != 32 || threads % (H * 32) || D > 256) return false;
+      tokens = threads / (H * 32);
+      break;
+    case R_ATTENTION_TILED:  // (tokens/8)*heads*128 threads, groups of 128
+      if (group != 128 || threads % (H * 128) || S % 8 || (D != 32 && D != 64 && D != 128))
+        return false;
+      tokens = threads / (H * 128) * 8;
+      break;
+    case R_ATTENTION_TAIL_32:
+    case R_ATTENTION_TAIL_128: {  // metal.py:544-555: B*ceil(S/8)*heads*128 threads
+      const uint64_t want = r == R_ATTENTION_TAIL_32 ? 32 : 128;
+      const uint64_t per = ceil_div(S, 8) * H * 128;
+      if (group != 128 || D != want || threads % per) return false;
+      tokens = threads / per * S;
+      break;
+    }
+    case R_ATTENTION_F16:
+    case R_ATTENTION_F16_NORM_ROPE:
+      if (group != 256 || (D != 32 && D != 64 && D != 128)) return false;
+      tokens = threads;
+      s->in_f16 = 1;
+      s->out_f16 = p.u1 & 1u;
+      break;
+    case R_ATTENTION_F16_SCALAR:
+      if (group != 64 || D > 256) return false;
+      tokens = threads;
+      s->in_f16 = 1;
+      s->out_f16 = p.u1 & 1u;
+      break;
+    default:
+      return false;
+  }
+  if (!tokens || tokens % S || tokens > kMaxTokens) return false;
+  s->B = tokens / S;
+  s->S = S;
+  s->H = H;
+  s->KV = KV;
+  s->D = D;
+  return true;
+}
+
+bool attn_sizes(const AttnShape& s, const uint64_t* sz) {
+  const uint64_t ein = s.in_f16 ? 2 : 4, eout = s.out_f16 ? 2 : 4;
+  const uint64_t qn = s.B * s.S * s.H * s.D, kn = s.B * s.S * s.KV * s.D;
+  return qn * ein <= sz[0] && kn * ein <= sz[1] && kn * ein <= sz[2] && s.B * 4 <= sz[3] &&
+         qn * eout <= sz[4];
+}
+
+struct RowRange {
+  uint64_t r0, r1;
+};
+
+bool linear4_range(Route r, const Params& p, uint64_t threads, uint32_t group, RowRange* out) {
+  const uint64_t rows = p.rows, cols = p.cols, k = p.k, n = p.n;
+  if (!rows || !cols || !k || k % 64 || rows > kMaxTokens || cols > 65536 || k > 65536)
+    return false;
+  switch (r) {
+    case R_LINEAR4: {  // kernels.metal:32-51: rows n + 4*(threadgroup / cols) + t
+      if (group != 32 || threads % (cols * 32)) return false;
+      const uint64_t blocks = threads / (cols * 32);
+      out->r0 = n;
+      out->r1 = std::min(n + 4 * blocks, rows);
+      break;
+    }
+    case R_LINEAR4_TILED: {  // kernels.metal:489-520: 8-row tiles from row n
+      const uint64_t per = (cols / 32) * 128;
+      if (group != 128 || cols % 32 || threads % per) return false;
+      out->r0 = n;
+      out->r1 = n + 8 * (threads / per);
+      if (out->r1 > rows) return false;
+      break;
+    }
+    case R_LINEAR4_TAIL:  // kernels.metal:560-605: one partial 8-row tile from row n
+      if (group != 128 || cols % 32 || threads != (cols / 32) * 128) return false;
+      out->r0 = n;
+      out->r1 = std::min(n + 8, rows);
+      break;
+    case R_LINEAR4_16X32:  // kernels.metal:522-558: 16-row tiles from row 0
+    case R_LINEAR4_32X32: {  // kernels.metal:733-773: 32-row tiles from row 0
+      const uint64_t tile = r == R_LINEAR4_16X32 ? 16 : 32;
+      const uint64_t per = (cols / 32) * 256;
+      if (group != 256 || cols % 32 || threads % per) return false;
+      out->r0 = 0;
+      out->r1 = tile * (threads / per);
+      if (out->r1 > rows) return false;
+      break;
+    }
+    case R_LINEAR4_SMALL3:  // kernels.metal:655-684: exactly three rows
+      if (group != 32 || threads != cols * 32 || rows != 3) return false;
+      out->r0 = 0;
+      out->r1 = 3;
+      break;
+    default:
+      return false;
+  }
+  return out->r0 < out->r1;
+}
+
+// Validates one launch against the buffer sizes it would touch. Pure: no allocation.
+bool validate(Route r, const Params& p, uint64_t threads, uint32_t group, const uint64_t* sz,
+              uint32_t count, uint32_t nbuf) {
+  if (count != nbuf || !threads || !group) return false;
+  switch (r) {
+    case R_ATTENTION:
+    case R_ATTENTION_TILED:
+    case R_ATTENTION_TAIL_32:
+    case R_ATTENTION_TAIL_128:
+    case R_ATTENTION_F16:
+    case R_ATTENTION_F16_SCALAR:
+    case R_ATTENTION_F16_NORM_ROPE: {
+      AttnShape s;
+      if (!attn_shape(r, p, threads, group, &s) || !attn_sizes(s, sz)) return false;
+      if (r == R_ATTENTION_F16_NORM_ROPE)
+        return sz[5] >= s.D * 2 && p.theta > 0.0f && p.eps >= 0.0f && std::isfinite(p.theta);
+      return true;
+    }
+    case R_NORM_ROPE_F16: {  // buffers: x, gamma, lengths, y
+      const uint64_t heads = p.heads, S = p.seq, D = p.dim, tokens = threads;
+      if (group != 256 || !heads || heads > 1024 || !S || tokens % S || tokens > kMaxTokens ||
+          (D != 32 && D != 64 && D != 128) || !(p.theta > 0.0f) || !std::isfinite(p.theta))
+        return false;
+      const uint64_t bytes = tokens * heads * D * 2;
+      return sz[0] >= bytes && sz[1] >= D * 2 && sz[2] >= tokens / S * 4 && sz[3] >= bytes;
+    }
+    case R_RMS_NORM: {  // kernels.metal:53-63: rows*32 threads, groups of 32
+      const uint64_t cols = p.cols;
+      if (group != 32 || threads % 32 || !cols || cols > 65536) return false;
+      const uint64_t rows = threads / 32;
+      if (rows > kMaxTokens * 16) return false;
+      return sz[0] >= rows * cols * 4 && sz[1] >= cols * 2 && sz[2] >= rows * cols * 4;
+    }
+    case R_ROPE: {  // kernels.metal:65-74: n threads, n = tokens*heads*dim/2
+      const uint64_t n = p.n, D = p.dim;
+      if (!n || !D || D % 2 || D > 1024 || !p.heads || !p.seq || n % (D / 2) ||
+          !(p.theta > 0.0f) || !std::isfinite(p.theta))
+        return false;
+      return sz[0] >= n * 2 * 4;
+    }
+    case R_LINEAR4:
+    case R_LINEAR4_TILED:
+    case R_LINEAR4_TAIL:
+    case R_LINEAR4_16X32:
+    case R_LINEAR4_32X32:
+    case R_LINEAR4_SMALL3: {
+      RowRange rr;
+      if (!linear4_range(r, p, threads, group, &rr)) return false;
+      const uint64_t cols = p.cols, k = p.k;
+      return sz[0] >= rr.r1 * k * 4 && sz[1] >= cols * (k / 8) * 4 &&
+             sz[2] >= cols * (k / 64) * 2 && sz[3] >= cols * (k / 64) * 2 &&
+             sz[4] >= rr.r1 * cols * 4;
+    }
+    case R_ADD: {  // kernels.metal:300-304
+      const uint64_t n = p.n;
+      return n && sz[0] >= n * 4 && sz[1] >= n * 4 && sz[2] >= n * 4;
+    }
+    case R_COPY:
+      return threads % 16 == 0 && sz[0] >= threads && sz[1] >= threads;
+    default:
+      return false;
+  }
+}
+
+// ---- RoPE tables ------------------------------------------------------------------------------
+
+uint32_t float_bits(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, sizeof u);
+  return u;
+}
+
+// cos/sin[pos][c] = cos/sin(pos * theta^(-2c/D)), evaluated in float64 and rounded once.
+bool ensure_rope(Runtime* rt, uint32_t seq, uint32_t dim, float theta) {
+  const auto key = std::make_tuple(seq, dim, float_bits(theta));
+  if (rt->rope.count(key)) return true;
+  const uint32_t half = dim / 2;
+  std::vector<float> c(static_cast<size_t>(seq) * half), s(c.size());
+  for (uint32_t pos = 0; pos < seq; ++pos)
+    for (uint32_t j = 0; j < half; ++j) {
+      const double angle =
+          static_cast<double>(pos) * std::pow(static_cast<double>(theta), -2.0 * j / dim);
+      c[static_cast<size_t>(pos) * half + j] = static_cast<float>(std::cos(angle));
+      s[static_cast<size_t>(pos) * half + j] = static_cast<float>(std::sin(angle));
+    }
+  RopeTable t{nullptr, nullptr};
+  const size_t bytes = c.size() * sizeof(float);
+  if (hipMalloc(&t.cos, bytes) != hipSuccess) return false;
+  if (hipMalloc(&t.sin, bytes) != hipSuccess) {
+    (void)hipFree(t.cos);
+    return false;
+  }
+  if (hipMemcpy(t.cos, c.data(), bytes, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(t.sin, s.data(), bytes, hipMemcpyHostToDevice) != hipSuccess) {
+    (void)hipFree(t.cos);
+    (void)hipFree(t.sin);
+    return false;
+  }
+  rt->rope[key] = t;
+  return true;
+}
+
+bool prepare(Runtime* rt, Route r, const Params& p) {
+  switch (r) {
+    case R_ATTENTION_F16_NORM_ROPE:
+    case R_NORM_ROPE_F16:
+    case R_ROPE:
+      return ensure_rope(rt, p.seq, p.dim, p.theta);
+    default:
+      return true;
+  }
+}
+
+const RopeTable* rope_of(Runtime* rt, const Params& p) {
+  auto it = rt->rope.find(std::make_tuple(p.seq, p.dim, float_bits(p.theta)));
+  return it == rt->rope.end() ? nullptr : &it->second;
+}
+
+// ---- launch -----------------------------------------------------------------------------------
+
+hipError_t launch(Runtime* rt, const Op& op) {
+  hipStream_t st = rt->stream;
+  const Params& p = op.p;
+  switch (op.route) {
+    case R_ATTENTION:
+    case R_ATTENTION_TILED:
+    case R_ATTENTION_TAIL_32:
+    case R_ATTENTION_TAIL_128:
+    case R_ATTENTION_F16:
+    case R_ATTENTION_F16_SCALAR:
+    case R_ATTENTION_F16_NORM_ROPE: {
+      AttnShape s;
+      if (!attn_shape(op.route, p, op.threads, op.group, &s)) return hipErrorInvalidValue;
+      tessery::AttnArgs a{};
+      a.q = op.ptr[0];
+      a.k = op.ptr[1];
+      a.v = op.ptr[2];
+      a.lengths = static_cast<const uint32_t*>(op.ptr[3]);
+      a.out = op.ptr[4];
+      a.B = static_cast<int>(s.B);
+      a.S = static_cast<int>(s.S);
+      a.H = static_cast<int>(s.H);
+      a.KV = static_cast<int>(s.KV);
+      a.D = static_cast<int>(s.D);
+      a.scale = p.scale;
+      a.bidi = p.u0 ? 1 : 0;
+      a.in_f16 = s.in_f16;
+      a.out_f16 = s.out_f16;
+      a.eps = p.eps;
+      if (op.route == R_ATTENTION_F16_NORM_ROPE) {
+        const RopeTable* t = rope_of(rt, p);
+        if (!t) return hipErrorInvalidValue;
+        a.gamma_q = static_cast<const uint16_t*>(op.ptr[5]);
+        a.rope_cos = t->cos;
+        a.rope_sin = t->sin;
+      }
+      if (op.route == R_ATTENTION || op.route == R_ATTENTION_F16_SCALAR)
+        return tessery::launch_attention_scalar(a, st);
+      if (op.route == R_ATTENTION_F16 || op.route == R_ATTENTION_F16_NORM_ROPE)
+        return tessery::launch_attention_f16(a, st);
+      return tessery::launch_attention_f32(a, st);
+    }
+    case R_NORM_ROPE_F16: {
+      const RopeTable* t = rope_of(rt, p);
+      if (!t) return hipErrorInvalidValue;
+      return tessery::launch_norm_rope_f16(
+          static_cast<const _Float16*>(op.ptr[0]), static_cast<_Float16*>(op.ptr[3]),
+          static_cast<const uint16_t*>(op.ptr[1]), t->cos, t->sin,
+          static_cast<const uint32_t*>(op.ptr[2]), static_cast<int>(op.threads / p.seq),
+          static_cast<int>(p.seq), static_cast<int>(p.heads), static_cast<int>(p.dim), p.eps, st);
+    }
+    case R_RMS_NORM:
+      return tessery::launch_rms_norm_f32(
+          static_cast<const float*>(op.ptr[0]), static_cast<const uint16_t*>(op.ptr[1]),
+          static_cast<float*>(op.ptr[2]), static_cast<int>(op.threads / 32),
+          static_cast<int>(p.cols), p.eps, st);
+    case R_ROPE: {
+      const RopeTable* t = rope_of(rt, p);
+      if (!t) return hipErrorInvalidValue;
+      return tessery::launch_rope_f32(static_cast<float*>(op.ptr[0]), t->cos, t->sin, p.n,
+                                      static_cast<int>(p.heads), static_cast<int>(p.seq),
+                                      static_cast<int>(p.dim), st);
+    }
+    case R_LINEAR4:
+    case R_LINEAR4_TILED:
+    case R_LINEAR4_TAIL:
+    case R_LINEAR4_16X32:
+    case R_LINEAR4_32X32:
+    case R_LINEAR4_SMALL3: {
+      RowRange rr;
+      if (!linear4_range(op.route, p, op.threads, op.group, &rr)) return hipErrorInvalidValue;
+      return tessery::launch_linear4_f32(
+          static_cast<const float*>(op.ptr[0]), static_cast<const uint32_t*>(op.ptr[1]),
+          static_cast<const uint16_t*>(op.ptr[2]), static_cast<const uint16_t*>(op.ptr[3]),
+          static_cast<float*>(op.ptr[4]), static_cast<int>(rr.r0), static_cast<int>(rr.r1),
+          static_cast<int>(p.cols), static_cast<int>(p.k), st);
+    }
+    case R_ADD:
+      return tessery::launch_add_f32(static_cast<const float*>(op.ptr[0]),
+                                     static_cast<const float*>(op.ptr[1]),
+                                     static_cast<float*>(op.ptr[2]), p.n, st);
+    case R_COPY:
+      return tessery::launch_copy(op.ptr[0], op.ptr[1], op.threads, st);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+bool make_op(Route r, const Params& p, uint64_t threads, uint32_t group, void* const* ptrs,
+             const uint64_t* sizes, uint32_t count, Op* op) {
+  op->route = r;
+  op->p = p;
+  op->threads = threads;
+  op->group = group;
+  op->count = count;
+  for (uint32_t i = 0; i < kMaxBuffers; ++i) {
+    op->ptr[i] = i < count ? ptrs[i] : nullptr;
+    op->size[i] = i < count ? sizes[i] : 0;
+  }
+  return true;
+}
+
+bool queue_op(Runtime* rt, const Op& op) {
+  if (rt->profiling && rt->ops.size() >= kMaxProfiled) return false;
+  rt->ops.push_back(op);
+  return true;
+}
+
+void release_profile_events(Runtime* rt) {
+  for (hipEvent_t e : rt->prof_events) (void)hipEventDestroy(e);
+  rt->prof_events.clear();
+}
+
+}  // namespace
+
+extern "C" {
+
+int mi_abi_version(void) { return kAbiVersion; }
+
+void* mi_create(const char* /*source*/) {
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) return nullptr;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return nullptr;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return nullptr;
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return nullptr;
+  auto rt = new Runtime();
+  rt->device = device;
+  if (hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreate(&rt->ev_start) != hipSuccess || hipEventCreate(&rt->ev_end) != hipSuccess) {
+    mi_destroy(rt);
+    return nullptr;
+  }
+  return rt;
+}
+
+void mi_destroy(void* runtime) {
+  auto rt = static_cast<Runtime*>(runtime);
+  if (!rt) return;
+  (void)hipSetDevice(rt->device);
+  if (rt->stream) (void)hipStreamSynchronize(rt->stream);
+  for (auto& kv : rt->rope) {
+    (void)hipFree(kv.second.cos);
+    (void)hipFree(kv.second.sin);
+  }
+  release_profile_events(rt);
+  if (rt->ev_start) (void)hipEventDestroy(rt->ev_start);
+  if (rt->ev_end) (void)hipEventDestroy(rt->ev_end);
+  if (rt->stream) (void)hipStreamDestroy(rt->stream);
+  delete rt;
+}
+
+void* mi_buffer(void* runtime, const void* bytes, uint64_t size) {
+  auto rt = static_cast<Runtime*>(runtime);
+  if (!rt || !size) return nullptr;
+  if (hipSetDevice(rt->device) != hipSuccess) return nullptr;
+  void* ptr = nullptr;
+  if (hipMalloc(&ptr, size) != hipSuccess) return nullptr;
+  const hipError_t e = bytes ? hipMemcpy(ptr, bytes, size, hipMemcpyHostToDevice)
+                             : hipMemset(ptr, 0, size);
+  if (e != hipSuccess) {
+    (void)hipFree(ptr);
+    return nullptr;
+  }
+  return new Buffer{ptr, size, rt};
+}
+
+void mi_free(void* buffer) {
+  auto b = static_cast<Buffer*>(buffer);
+  if (!b) return;
+  (void)hipSetDevice(b->owner->device);
+  (void)hipStreamSynchronize(b->owner->stream);
+  (void)hipFree(b->ptr);
+  delete b;
+}
+
+int mi_read(void* buffer, void* output, uint64_t bytes) {
+  auto b = static_cast<Buffer*>(buffer);
+  if (!b || !output || bytes > b->size) return 1;
+  if (hipSetDevice(b->owner->device) != hipSuccess) return 1;
+  if (hipStreamSynchronize(b->owner->stream) != hipSuccess) return 1;
+  return hipMemcpy(output, b->ptr, bytes, hipMemcpyDeviceToHost) == hipSuccess ? 0 : 1;
+}
+
+int mi_write(void* buffer, const void* bytes, uint64_t size) {
+  auto b = static_cast<Buffer*>(buffer);
+  if (!b || !bytes || size > b->size) return 1;
+  if (hipSetDevice(b->owner->device) != hipSuccess) return 1;
+  if (hipStreamSynchronize(b->owner->stream) != hipSuccess) return 1;
+  return hipMemcpy(b->ptr, bytes, size, hipMemcpyHostToDevice) == hipSuccess ? 0 : 1;
+}
+
+int mi_begin(void* runtime) {
+  auto rt = static_cast<Runtime*>(runtime);
+  if (!rt || rt->recording) return 1;
+  rt->recording = true;
+  rt->ops.clear();
+  rt->profile_seconds.clear();
+  return 0;
+}
+
+int mi_dispatch(void* runtime, const char* name, void** buffers, uint32_t count,
+                const void* parameters, uint32_t size, uint64_t threads, uint32_t group) {
+  auto rt = static_cast<Runtime*>(runtime);
+  if (!rt || !rt->recording || count > kMaxBuffers || size != sizeof(Params) || !parameters ||
+      !threads || !group)
+    return 1;
+  uint32_t nbuf = 0;
+  const Route r = find_route(name, &nbuf);
+  if (r == R_NONE) return 1;
+  Params p;
+  std::memcpy(&p, parameters, sizeof p);
+  void* ptrs[kMaxBuffers] = {};
+  uint64_t sizes[kMaxBuffers] = {};
+  for (uint32_t i = 0; i < count; ++i) {
+    auto b = static_cast<Buffer*>(buffers ? buffers[i] : nullptr);
+    if (!b || b->owner != rt) return 1;
+    ptrs[i] = b->ptr;
+    sizes[i] = b->size;
+  }
+  if (!validate(r, p, threads, group, sizes, count, nbuf)) return 1;
+  if (hipSetDevice(rt->device) != hipSuccess || !prepare(rt, r, p)) return 1;
+  Op op;
+  make_op(r, p, threads, group, ptrs, sizes, count, &op);
+  return queue_op(rt, op) ? 0 : 1;
+}
+
+int mi_finish(void* runtime) {
+  auto rt = static_cast<Runtime*>(runtime);
+  if (!rt || !rt->recording) return 1;
+  if (hipSetDevice(rt->device) != hipSuccess) return 1;
+  int failed = 0;
+  const size_t n = rt->ops.size();
+  if (rt->profiling) {
+    while (rt->prof_events.size() < 2 * n) {
+      hipEvent_t e;
+      if (hipEventCreate(&e) != hipSuccess) return 1;
+      rt->prof_events.push_back(e);
+    }
+  }
+  if (hipEventRecord(rt->ev_start, rt->stream) != hipSuccess) failed = 1;
+  for (size_t i = 0; i < n && !failed; ++i) {
+    if (rt->profiling && hipEventRecord(rt->prof_events[2 * i], rt->stream) != hipSuccess) failed = 1;
+    if (!failed && launch(rt, rt->ops[i]) != hipSuccess) failed = 1;
+    if (!failed && rt->profiling &&
+        hipEventRecord(rt->prof_events[2 * i + 1], rt->stream) != hipSuccess)
+      failed = 1;
+  }
+  if (hipEventRecord(rt->ev_end, rt->stream) != hipSuccess) failed = 1;
+  if (hipStreamSynchronize(rt->stream) != hipSuccess) failed = 1;
+  rt->last_gpu = -1.0;
+  float ms = 0.0f;
+  if (!failed && hipEventElapsedTime(&ms, rt->ev_start, rt->ev_end) == hipSuccess)
+    rt->last_gpu = ms * 1e-3;
+  rt->profile_seconds.clear();
+  if (!failed && rt->profiling) {
+    for (size_t i = 0; i < n; ++i) {
+      float t = 0.0f;
+      if (hipEventElapsedTime(&t, rt->prof_events[2 * i], rt->prof_events[2 * i + 1]) !=
+          hipSuccess) {
+        failed = 1;
+        break;
+      }
+      rt->profile_seconds.push_back(t * 1e-3);
+    }
+    if (failed) rt->profile_seconds.clear();
+  }
+  rt->ops.clear();
+  rt->recording = false;
+  return failed;
+}
+
+double mi_gpu_seconds(void* runtime) {
+  auto rt = static_cast<Runtime*>(runtime);
+  return rt ? rt->last_gpu : -1.0;
+}
+
+void mi_abort(void* runtime) {
+  auto rt = static_cast<Runtime*>(runtime);
+  if (!rt) return;
+  rt->ops.clear();  // queued work was never launched
+  rt->recording = false;
+}
+
+int mi_profile_enable(void* runtime, int enabled) {
+  auto rt = static_cast<Runtime*>(runtime);
+  if (!rt || rt->recording) return 1;
+  rt->profile_seconds.clear();
+  rt->profiling = enabled != 0;
+  if (!rt->profiling) release_profile_events(rt);
+  return 0;
+}
+
+int mi_profile_read(void* runtime, double* seconds, uint32_t count) {
+  auto rt = static_cast<Runtime*>(runtime);
+  if (!rt || rt->recording || count != rt->profile_seconds.size()) return 1;
+  if (count) std::memcpy(seconds, rt->profile_seconds.data(), count * sizeof(double));
+  return 0;
+}
+
+void* mi_plan_create(void* runtime, void** buffers, uint32_t count) {
+  auto rt = static_cast<Runtime*>(runtime);
+  if (!rt || !rt->recording || rt->profiling || !count || count > 2048 || !buffers) return nullptr;
+  auto plan = new Plan{rt, {}, {}};
+  for (uint32_t i = 0; i < count; ++i) {
+    auto b = static_cast<Buffer*>(buffers[i]);
+    if (!b || b->owner != rt) {
+      delete plan;
+      return nullptr;
+    }
+    plan->sizes.push_back(b->size);
+  }
+  return plan;
+}
+
+int mi_plan_add(void* plan, const char* name, const uint32_t* slots, uint32_t count,
+                const void* params, uint64_t threads, uint32_t group) {
+  auto pl = static_cast<Plan*>(plan);
+  if (!pl || !pl->owner->recording || pl->owner->profiling || !count || count > kMaxBuffers ||
+      !threads || !group || !params || !slots || pl->ops.size() >= kMaxPlanOps)
+    return 1;
+  uint32_t nbuf = 0;
+  const Route r = find_route(name, &nbuf);
+  if (r == R_NONE) return 1;
+  PlanOp op{};
+  std::memcpy(&op.p, params, sizeof(Params));
+  uint64_t sizes[kMaxBuffers] = {};
+  for (uint32_t i = 0; i < count; ++i) {
+    if (slots[i] >= pl->sizes.size()) return 1;
+    op.slots[i] = slots[i];
+    sizes[i] = pl->sizes[slots[i]];
+  }
+  if (!validate(r, op.p, threads, group, sizes, count, nbuf)) return 1;
+  op.route = r;
+  op.threads = threads;
+  op.group = group;
+  op.count = count;
+  pl->ops.push_back(op);
+  return 0;
+}
+
+uint64_t mi_plan_bytes(void* plan) {
+  auto pl = static_cast<Plan*>(plan);
+  if (!pl) return 0;
+  return sizeof(Plan) + pl->sizes.capacity() * sizeof(uint64_t) +
+         pl->ops.capacity() * sizeof(PlanOp);
+}
+
+void mi_plan_free(void* plan) { delete static_cast<Plan*>(plan); }
+
+int mi_plan_run(void* runtime, void* plan, void** buffers, uint32_t count) {
+  auto rt = static_cast<Runtime*>(runtime);
+  auto pl = static_cast<Plan*>(plan);
+  if (!rt || !pl || pl->owner != rt || !rt->recording || rt->profiling ||
+      count != pl->sizes.size() || pl->ops.empty() || !buffers)
+    return 1;
+  // Validate every slot before queueing any work (runtime.mm:198-202).
+  for (uint32_t i = 0; i < count; ++i) {
+    auto b = static_cast<Buffer*>(buffers[i]);
+    if (!b || b->owner != rt || b->size != pl->sizes[i]) return 1;
+  }
+  if (hipSetDevice(rt->device) != hipSuccess) return 1;
+  for (const auto& po : pl->ops)
+    if (!prepare(rt, po.route, po.p)) return 1;
+  for (const auto& po : pl->ops) {
+    void* ptrs[kMaxBuffers] = {};
+    uint64_t sizes[kMaxBuffers] = {};
+    for (uint32_t i = 0; i < po.count; ++i) {
+      auto b = static_cast<Buffer*>(buffers[po.slots[i]]);
+      ptrs[i] = b->ptr;
+      sizes[i] = b->size;
+    }
+    Op op;
+    make_op(po.route, po.p, po.threads, po.group, ptrs, sizes, po.count, &op);
+    rt->ops.push_back(op);
+  }
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,151 @@
+"""Seeded synthetic workloads of the prefill-attention path and their algorithmic work.
+
+Five workloads, each named by what it is:
+  bge_small_c1     BGE-small attention layer, B=2 S=16 H=12 D=32 fp32, lengths [16, 9], bidirectional
+  bge_small_32x512 BGE-small encoder attention, B=32 S=512 H=12 D=32 fp32, 12 layers, L ~ U{2..512}
+  qwen3_8x512      Qwen3-0.6B causal GQA, B=8 S=512 16q/8kv D=128 fp16, L ~ U{64..512}, q/k norm+RoPE
+  qwen3_32x512     Qwen3 causal GQA at maximum batch, B=32, L log-uniform in [1,512], execution width
+                   16*ceil(max L/16), 28 layers, q/k norm+RoPE
+  qwen3_qkv4       uint4 group-64 QKV projection of x[16,256,1024] fp16 feeding causal GQA, L ~ U{1..256}
+
+Convention: lengths come first from numpy.random.default_rng(seed); layer l's tensors come from
+default_rng((seed, l)). Activations are N(0,1); RMSNorm weights U(0.5,1.5) stored as bfloat16
+words (truncated, the encoding tessery's own tests use, test_kernels.py:22-23).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+from numpy.typing import NDArray
+
+EPS = 1e-6
+THETA = 1e6
+
+
+@dataclass(frozen=True)
+class Shape:
+    batch: int
+    seq: int
+    heads: int
+    kv_heads: int
+    dim: int
+    causal: bool
+
+    @property
+    def tokens(self) -> int:
+        return self.batch * self.seq
+
+
+def bf16_words(values: NDArray[np.floating]) -> NDArray[np.uint16]:
+    """float32 -> bfloat16 storage words by truncation."""
+    return (np.asarray(values, dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def bf16_values(words: NDArray[np.uint16]) -> NDArray[np.float32]:
+    return (np.asarray(words, dtype=np.uint32) << 16).view(np.float32)
+
+
+def normal(rng: np.random.Generator, shape: tuple[int, ...], dtype: type) -> NDArray:
+    return rng.standard_normal(shape, dtype=np.float32).astype(dtype, copy=False)
+
+
+# ---- lengths -------------------------------------------------------------------------------
+
+
+def lengths_uniform(seed: int, batch: int, low: int, high: int) -> NDArray[np.uint32]:
+    return np.random.default_rng(seed).integers(low, high + 1, batch).astype(np.uint32)
+
+
+def lengths_loguniform(seed: int, batch: int, high: int = 512) -> NDArray[np.uint32]:
+    draw = np.random.default_rng(seed).uniform(0.0, math.log(high + 1), batch)
+    return np.clip(np.floor(np.exp(draw)), 1, high).astype(np.uint32)
+
+
+def execution_width(lengths: NDArray[np.uint32], align: int = 16) -> int:
+    return align * int(math.ceil(int(lengths.max()) / align))
+
+
+# ---- workloads -----------------------------------------------------------------------------
+
+
+def bge_small_c1() -> tuple[Shape, NDArray[np.uint32], dict[str, NDArray]]:
+    shape = Shape(2, 16, 12, 12, 32, causal=False)
+    lengths = np.array([16, 9], np.uint32)
+    rng = np.random.default_rng((1, 0))
+    q, k, v = (normal(rng, (2, 16, 12, 32), np.float32) for _ in range(3))
+    return shape, lengths, {"q": q, "k": k, "v": v}
+
+
+def bge_small_32x512() -> tuple[Shape, NDArray[np.uint32]]:
+    return Shape(32, 512, 12, 12, 32, causal=False), lengths_uniform(2, 32, 2, 512)
+
+
+def bge_layer(shape: Shape, layer: int, seed: int = 2) -> dict[str, NDArray]:
+    rng = np.random.default_rng((seed, layer))
+    q = normal(rng, (shape.batch, shape.seq, shape.heads, shape.dim), np.float32)
+    k = normal(rng, (shape.batch, shape.seq, shape.kv_heads, shape.dim), np.float32)
+    v = normal(rng, (shape.batch, shape.seq, shape.kv_heads, shape.dim), np.float32)
+    return {"q": q, "k": k, "v": v}
+
+
+def qwen3_8x512() -> tuple[Shape, NDArray[np.uint32]]:
+    return Shape(8, 512, 16, 8, 128, causal=True), lengths_uniform(3, 8, 64, 512)
+
+
+def qwen3_32x512() -> tuple[Shape, NDArray[np.uint32]]:
+    lengths = lengths_loguniform(4, 32)
+    return Shape(32, execution_width(lengths), 16, 8, 128, causal=True), lengths
+
+
+def qwen_layer(shape: Shape, layer: int, seed: int) -> dict[str, NDArray]:
+    """Pre-norm q/k and v in fp16 plus bf16 q/k norm weights for one layer."""
+    rng = np.random.default_rng((seed, layer))
+    b, s, h, kv, d = shape.batch, shape.seq, shape.heads, shape.kv_heads, shape.dim
+    q = normal(rng, (b, s, h, d), np.float16)
+    k = normal(rng, (b, s, kv, d), np.float16)
+    v = normal(rng, (b, s, kv, d), np.float16)
+    gq = bf16_words(rng.uniform(0.5, 1.5, d))
+    gk = bf16_words(rng.uniform(0.5, 1.5, d))
+    return {"q": q, "k": k, "v": v, "q_norm": gq, "k_norm": gk}
+
+
+# ---- algorithmic work (per layer) ----------------------------------------------------------
+
+
+def pairs(shape: Shape, lengths: NDArray[np.uint32]) -> int:
+    """Sum over rows and query positions of attended keys: causal n(p) = min(p+1, L),
+    bidirectional n(p) = L; padded query rows count (they are outputs)."""
+    total = 0
+    for length in lengths.astype(np.int64).tolist():
+        length = min(length, shape.seq)
+        if shape.causal:
+            total += length * (length + 1) // 2 + (shape.seq - length) * length
+        else:
+            total += shape.seq * length
+    return total
+
+
+def attention_flop(shape: Shape, lengths: NDArray[np.uint32]) -> int:
+    """QK^T plus PV multiply-adds over attended pairs: 4 * D * H * pairs."""
+    return 4 * shape.dim * shape.heads * pairs(shape, lengths)
+
+
+def dense_flop(shape: Shape) -> int:
+    """Dense convention 4*D*H*B*S^2, halved when causal (not mask-exact)."""
+    full = 4 * shape.dim * shape.heads * shape.batch * shape.seq * shape.seq
+    return full // 2 if shape.causal else full
+
+
+def attention_bytes(
+    shape: Shape, lengths: NDArray[np.uint32], in_bytes: int, out_bytes: int
+) -> int:
+    """Compulsory HBM traffic of one attention launch: every query row in, valid K/V rows in,
+    every output row out, the lengths vector."""
+    valid = int(np.minimum(lengths.astype(np.int64), shape.seq).sum())
+    q = shape.batch * shape.seq * shape.heads * shape.dim * in_bytes
+    kv = 2 * valid * shape.kv_heads * shape.dim * in_bytes
+    o = shape.batch * shape.seq * shape.heads * shape.dim * out_bytes
+    return q + kv + o + 4 * shape.batch

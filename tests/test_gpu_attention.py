@@ -1,0 +1,278 @@
+"""Attention parity on the GPU through the C ABI (HipRuntime -> mi_dispatch), against the float64
+oracle on identical seeded inputs.
+
+fp32 routes use tessery's own tolerance (atol 2e-6, rtol 2e-5, test_kernels.py:157) and must
+also stay within max-abs 1e-4. fp16-operand routes (fp32 accumulation) use max-abs 2e-3 against
+the oracle evaluated in float64 on the same fp16 inputs; masked / padded / GQA index mapping is
+exercised by ragged lengths, padded query rows, head groups of 1, 2 and 4, and sentinel bytes
+around the output."""
+
+import numpy as np
+import pytest
+
+from oracle import attention as ref
+from oracle import norm_rope
+from tessery_amd import workloads
+from tests.conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+F32_ATOL, F32_RTOL, F32_MAX = 2e-6, 2e-5, 1e-4
+F16_MAX = 2e-3
+
+
+def run(engine, kernel, inputs, shape, out_dtype=np.float32, **params):
+    """Upload inputs, dispatch one route by name, read the output (test_kernels.py:26-39)."""
+    buffers = []
+    try:
+        for array in inputs:
+            buffers.append(engine.upload(array))
+        out = engine.buffer(int(np.prod(shape)) * np.dtype(out_dtype).itemsize)
+        buffers.append(out)
+        with engine.command():
+            engine._dispatch(kernel, buffers, **params)
+        return engine.read(out, shape, out_dtype)
+    finally:
+        for b in buffers:
+            b.close()
+
+
+def attend(engine, q, k, v, lengths, *, bidirectional, precision="f32", out_dtype=None):
+    b, s, h, d = q.shape
+    buffers = [engine.upload(a) for a in (q, k, v, lengths.astype(np.uint32))]
+    odt = np.float16 if out_dtype == "f16" else np.float32
+    buffers.append(engine.buffer(q.size * np.dtype(odt).itemsize))
+    try:
+        with engine.command():
+            engine._attention(buffers, tokens=b * s, seq=s, heads=h, kv_heads=k.shape[2], dim=d,
+                              bidirectional=int(bidirectional), precision=precision,
+                              out_dtype=out_dtype)
+        return engine.read(buffers[-1], q.shape, odt)
+    finally:
+        for x in buffers:
+            x.close()
+
+
+def check_f32(got, expected):
+    np.testing.assert_allclose(got, expected, atol=F32_ATOL, rtol=F32_RTOL)
+    assert np.max(np.abs(got - expected)) <= F32_MAX
+
+
+# ---- fp32: tessery's own cases ---------------------------------------------------------------
+
+
+def test_scalar_causal_gqa_seed17(runtime):
+    f = np.load(GOLDEN / "attention_cases.npz")
+    q = f["s17_q"]
+    got = run(runtime, "attention", [q, f["s17_k"], f["s17_v"], f["s17_lengths"]], q.shape,
+              threads=2 * 5 * 4 * 32, group_size=32, seq=5, heads=4, kv_heads=2, dim=64,
+              scale=64**-0.5)
+    check_f32(got, f["s17_expected"])
+
+
+def test_scalar_bidirectional_seed83(runtime):
+    f = np.load(GOLDEN / "attention_cases.npz")
+    q = f["s83_q"]
+    got = run(runtime, "attention", [q, f["s83_k"], f["s83_v"], f["s83_lengths"]], q.shape,
+              threads=2 * 5 * 3 * 32, group_size=32, seq=5, heads=3, kv_heads=3, dim=8,
+              scale=8**-0.5, bidirectional=True)
+    check_f32(got, f["s83_expected"])
+
+
+def test_bge_small_c1_through_route(runtime):
+    f = np.load(GOLDEN / "attention_cases.npz")
+    got = attend(runtime, f["c1_q"], f["c1_k"], f["c1_v"], f["c1_lengths"], bidirectional=True)
+    check_f32(got, f["c1_expected"])
+    assert runtime.diagnostics()["dispatches"] == {"attention": 1}
+    assert got.reshape(2, 16, 384).shape == (2, 16, 384)
+
+
+@pytest.mark.parametrize("dim", [32, 128])
+@pytest.mark.parametrize("bidirectional", [False, True])
+@pytest.mark.parametrize(
+    "seq,length_pair",
+    [(64, (1, 33)), (65, (1, 65)), (71, (33, 71)), (95, (65, 95)), (127, (1, 127)),
+     (128, (31, 32)), (129, (65, 129)), (136, (129, 136)), (255, (254, 255)), (511, (1, 511)),
+     (512, (511, 512))],
+)
+def test_tiled_attention_ragged_f64(runtime, dim, bidirectional, seq, length_pair):
+    """tessery test_kernels.py:160-210, same seed, shapes and kernel names."""
+    rng = np.random.default_rng(393)
+    heads, kv = 4, 2
+    q = rng.normal(size=(2, seq, heads, dim)).astype(np.float32)
+    k, v = [rng.normal(size=(2, seq, kv, dim)).astype(np.float32) for _ in range(2)]
+    lengths = np.array(length_pair, np.uint32)
+    got = run(runtime, f"attention_tail_{dim}" if seq % 32 else "attention_tiled",
+              [q, k, v, lengths], q.shape, threads=2 * ((seq + 7) // 8) * heads * 128,
+              group_size=128, seq=seq, heads=heads, kv_heads=kv, dim=dim, scale=dim**-0.5,
+              bidirectional=bidirectional)
+    check_f32(got, ref.attention(q, k, v, lengths, bidirectional=bidirectional))
+
+
+@pytest.mark.parametrize("bidirectional", [False, True])
+@pytest.mark.parametrize("pattern", ["alternating", "later_maximum", "uniform"])
+@pytest.mark.parametrize("seq", [65, 128, 129, 511])
+def test_extreme_logits_and_masked_blocks(runtime, bidirectional, pattern, seq):
+    """tessery test_kernels.py:213-253: logits near +-1131, late maxima, V = 1e10 when masked."""
+    rng = np.random.default_rng(718)
+    heads, dim = 2, 128
+    q = np.full((1, seq, heads, dim), 10, np.float32)
+    k = q.copy()
+    k[:, 1::2] *= -1
+    if pattern == "later_maximum":
+        k[:] = -10
+        k[:, 32:64] = 10
+    elif pattern == "uniform":
+        k[:] = 0
+    v = rng.normal(size=q.shape).astype(np.float32)
+    length = 65 if pattern == "later_maximum" else 33
+    v[:, length:] = 1e10
+    got = run(runtime, f"attention_tail_{dim}" if seq % 32 else "attention_tiled",
+              [q, k, v, np.array([length], np.uint32)], q.shape,
+              threads=((seq + 7) // 8) * heads * 128, group_size=128, seq=seq, heads=heads,
+              kv_heads=heads, dim=dim, scale=dim**-0.5, bidirectional=bidirectional)
+    expected = np.empty(q.shape)
+    for pos in range(seq):
+        end = length if bidirectional else min(pos + 1, length)
+        if pattern == "later_maximum":
+            chosen = v[0, 32 : min(end, 64)] if end > 32 else v[0, :end]
+        else:
+            chosen = v[0, :end:2] if pattern == "alternating" else v[0, :end]
+        expected[0, pos] = chosen.astype(np.float64).mean(axis=0)
+    check_f32(got, expected)
+
+
+@pytest.mark.parametrize("seq,name", [(16, "attention"), (64, "attention_tiled"),
+                                      (100, "attention_tail_32"), (512, "attention_tiled")])
+def test_route_dispatch_counts_and_output_guard(runtime, seq, name):
+    """One dispatch of the expected route; nothing written past the output."""
+    rng = np.random.default_rng(seq)
+    b, h, d = 3, 6, 32
+    q = rng.normal(size=(b, seq, h, d)).astype(np.float32)
+    k, v = [rng.normal(size=(b, seq, h, d)).astype(np.float32) for _ in range(2)]
+    lengths = np.array([seq, max(1, seq // 3), 1], np.uint32)
+    bufs = [runtime.upload(a) for a in (q, k, v, lengths)]
+    sentinel = np.full(q.size + 4096, np.nan, np.float32)
+    bufs.append(runtime.upload(sentinel))
+    try:
+        # output buffer larger than needed: route validation uses sizes as lower bounds
+        with runtime.command():
+            runtime._attention(bufs, tokens=b * seq, seq=seq, heads=h, kv_heads=h, dim=d,
+                               bidirectional=1)
+        out = runtime.read(bufs[-1], sentinel.shape)
+    finally:
+        for x in bufs:
+            x.close()
+    assert runtime.diagnostics()["dispatches"] == {name: 1}
+    assert np.isnan(out[q.size:]).all()
+    check_f32(out[: q.size].reshape(q.shape), ref.attention(q, k, v, lengths, bidirectional=True))
+
+
+def test_bge_small_32x512_layer0(runtime):
+    shape, lengths = workloads.bge_small_32x512()
+    t = workloads.bge_layer(shape, 0)
+    got = attend(runtime, t["q"], t["k"], t["v"], lengths, bidirectional=True)
+    check_f32(got, ref.attention(t["q"], t["k"], t["v"], lengths, bidirectional=True))
+
+
+# ---- fp16 operands, fp32 accumulation ---------------------------------------------------------
+
+
+def f16_inputs(seed, b, s, h, kv, d):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((b, s, h, d), dtype=np.float32).astype(np.float16)
+    k = rng.standard_normal((b, s, kv, d), dtype=np.float32).astype(np.float16)
+    v = rng.standard_normal((b, s, kv, d), dtype=np.float32).astype(np.float16)
+    return q, k, v
+
+
+@pytest.mark.parametrize("out_dtype", ["f32", "f16"])
+@pytest.mark.parametrize("bidirectional", [False, True])
+@pytest.mark.parametrize(
+    "b,s,h,kv,d,lengths",
+    [
+        (2, 1, 4, 2, 128, (1, 1)),
+        (2, 7, 4, 2, 128, (7, 3)),
+        (2, 33, 8, 2, 64, (33, 1)),
+        (3, 64, 4, 4, 32, (64, 63, 2)),
+        (2, 100, 16, 8, 128, (100, 37)),
+        (2, 129, 2, 1, 128, (129, 65)),
+        (4, 464, 16, 8, 128, (464, 1, 230, 63)),
+        (2, 512, 16, 8, 128, (512, 511)),
+    ],
+)
+def test_f16_attention(runtime, b, s, h, kv, d, lengths, bidirectional, out_dtype):
+    q, k, v = f16_inputs(b * 1000 + s, b, s, h, kv, d)
+    lengths = np.array(lengths, np.uint32)
+    got = attend(runtime, q, k, v, lengths, bidirectional=bidirectional, precision="f16",
+                 out_dtype=out_dtype)
+    expected = ref.attention(q, k, v, lengths, bidirectional=bidirectional)
+    err = np.max(np.abs(got.astype(np.float64) - expected))
+    assert err <= F16_MAX, err
+
+
+@pytest.mark.parametrize("d", [8, 96])
+def test_f16_scalar_route(runtime, d):
+    q, k, v = f16_inputs(d, 2, 19, 4, 2, d)
+    lengths = np.array([19, 5], np.uint32)
+    got = attend(runtime, q, k, v, lengths, bidirectional=False, precision="f16", out_dtype="f32")
+    assert runtime.diagnostics()["dispatches"] == {"attention_f16_scalar": 1}
+    assert np.max(np.abs(got - ref.attention(q, k, v, lengths, bidirectional=False))) <= F16_MAX
+
+
+def norm_rope_attend(engine, t, lengths, shape, out_dtype="f16"):
+    b, s, h, kv, d = shape.batch, shape.seq, shape.heads, shape.kv_heads, shape.dim
+    arrays = [t["q"], t["k"], t["v"], lengths.astype(np.uint32)]
+    bufs = [engine.upload(a) for a in arrays]
+    odt = np.float16 if out_dtype == "f16" else np.float32
+    bufs.append(engine.buffer(t["q"].size * np.dtype(odt).itemsize))
+    bufs += [engine.upload(t["q_norm"]), engine.upload(t["k_norm"]), engine.buffer(t["k"].nbytes)]
+    try:
+        with engine.command():
+            engine._attention_norm_rope(bufs, tokens=b * s, seq=s, heads=h, kv_heads=kv, dim=d,
+                                        eps=workloads.EPS, theta=workloads.THETA,
+                                        out_dtype=out_dtype)
+        return engine.read(bufs[4], t["q"].shape, odt), engine.read(bufs[7], t["k"].shape, np.float16)
+    finally:
+        for x in bufs:
+            x.close()
+
+
+def oracle_norm_rope(t, lengths):
+    qn = workloads.bf16_values(t["q_norm"]).astype(np.float64)
+    kn = workloads.bf16_values(t["k_norm"]).astype(np.float64)
+    q = norm_rope.norm_rope(t["q"], qn, workloads.EPS, workloads.THETA)
+    k = norm_rope.norm_rope(t["k"], kn, workloads.EPS, workloads.THETA)
+    return k, ref.attention(q, k, t["v"], lengths, bidirectional=False)
+
+
+def test_qwen_norm_rope_fixture(runtime):
+    f = np.load(GOLDEN / "qwen_small.npz")
+    t = {name: f[name] for name in ("q", "k", "v", "q_norm", "k_norm")}
+    shape = workloads.Shape(2, 40, 4, 2, 128, causal=True)
+    out, k_work = norm_rope_attend(runtime, t, f["lengths"], shape)
+    assert np.max(np.abs(out.astype(np.float64) - f["expected"])) <= F16_MAX
+    # the k prologue writes valid rows only, each within fp16 rounding of the float64 value
+    for bi, length in enumerate(f["lengths"]):
+        exp = f["k_normed"][bi, :length]
+        assert np.all(np.abs(k_work[bi, :length] - exp) <= 2.0**-10 * np.abs(exp) + 1e-6)
+
+
+@pytest.mark.parametrize("out_dtype", ["f16", "f32"])
+def test_qwen3_8x512(runtime, out_dtype):
+    shape, lengths = workloads.qwen3_8x512()
+    t = workloads.qwen_layer(shape, 0, seed=3)
+    out, _ = norm_rope_attend(runtime, t, lengths, shape, out_dtype)
+    _, expected = oracle_norm_rope(t, lengths)
+    err = np.max(np.abs(out.astype(np.float64) - expected))
+    assert err <= F16_MAX, err
+
+
+def test_qwen3_32x512_layer0(runtime):
+    """The benchmark workload itself (log-uniform lengths, execution width 464), layer 0."""
+    shape, lengths = workloads.qwen3_32x512()
+    t = workloads.qwen_layer(shape, 0, seed=4)
+    out, _ = norm_rope_attend(runtime, t, lengths, shape, "f16")
+    _, expected = oracle_norm_rope(t, lengths)
+    err = np.max(np.abs(out.astype(np.float64) - expected))
+    assert err <= F16_MAX, err

@@ -1,0 +1,80 @@
+"""Route selection without a GPU: HipRuntime methods called unbound on a recorder, the pattern of
+tessery's tests/unit/test_runtime_loading.py:9-106."""
+
+import json
+from types import SimpleNamespace
+
+import pytest
+
+from tessery_amd.runtime import HipRuntime
+from tests.conftest import GOLDEN
+
+ROUTES = json.loads((GOLDEN / "routes.json").read_text())
+
+
+def recorder():
+    calls = []
+    return calls, SimpleNamespace(_dispatch=lambda *a, **kw: calls.append((a, kw)))
+
+
+@pytest.mark.parametrize("case", ROUTES["attention"], ids=lambda c: f"s{c['seq']}d{c['dim']}")
+def test_attention_route_table(case):
+    calls, fake = recorder()
+    seq, dim = case["seq"], case["dim"]
+    HipRuntime._attention(fake, [], tokens=2 * seq, seq=seq, heads=4, kv_heads=2, dim=dim)
+    (args, kwargs), = calls
+    assert args[0] == case["name"]
+    assert kwargs["group_size"] == case["group_size"]
+    assert kwargs["threads"] == case["threads"]
+    assert kwargs["scale"] == dim**-0.5
+
+
+@pytest.mark.parametrize("dim,name,group", [(32, "attention_f16", 256), (64, "attention_f16", 256),
+                                            (128, "attention_f16", 256), (8, "attention_f16_scalar", 64),
+                                            (96, "attention_f16_scalar", 64)])
+@pytest.mark.parametrize("out_dtype,flag", [(None, 0), ("f32", 0), ("f16", 1)])
+def test_f16_route(dim, name, group, out_dtype, flag):
+    calls, fake = recorder()
+    HipRuntime._attention(fake, [], tokens=3 * 77, seq=77, heads=16, kv_heads=8, dim=dim,
+                          precision="f16", out_dtype=out_dtype)
+    (args, kwargs), = calls
+    assert args[0] == name and kwargs["group_size"] == group and kwargs["threads"] == 231
+    assert kwargs["out_f16"] == flag
+
+
+def test_norm_rope_route_sequence():
+    calls, fake = recorder()
+    bufs = list("abcdefgh")
+    HipRuntime._attention_norm_rope(fake, bufs, tokens=1024, seq=512, heads=16, kv_heads=8,
+                                    dim=128, eps=1e-6, theta=1e6)
+    assert [a[0] for a, _ in calls] == ["norm_rope_f16", "attention_f16_norm_rope"]
+    assert calls[0][0][1] == ["b", "g", "d", "h"]
+    assert calls[0][1]["heads"] == 8
+    assert calls[1][0][1] == ["a", "h", "c", "d", "e", "f"]
+    assert calls[1][1]["heads"] == 16 and calls[1][1]["kv_heads"] == 8 and calls[1][1]["out_f16"] == 1
+
+
+@pytest.mark.parametrize("rows,cols,k,selected", ROUTES["linear4"]["small3"])
+def test_three_row_projection_guard(rows, cols, k, selected):
+    calls, fake = recorder()
+    HipRuntime._linear4(fake, [], rows=rows, cols=cols, k=k)
+    assert any(a[0] == "linear4_small3" for a, _ in calls) == selected
+    if selected:
+        assert len(calls) == 1
+        assert calls[0][1] == dict(threads=cols * 32, group_size=32, rows=3, cols=cols, k=k)
+
+
+@pytest.mark.parametrize("rows,cols,k,selected", ROUTES["linear4"]["large"])
+def test_large_tile_partition(rows, cols, k, selected):
+    calls, fake = recorder()
+    HipRuntime._linear4(fake, [], rows=rows, cols=cols, k=k)
+    assert (calls[0][0][0] in ("linear4_16x32_k64", "linear4_32x32_k64")) == selected
+    if selected and calls[0][0][0] == "linear4_16x32_k64":
+        assert len(calls) == 1 + bool(rows % 16 >= 8) + bool(rows % 8)
+        regions = [(0, rows // 16 * 16)]
+        for args, kwargs in calls[1:]:
+            start = kwargs["n"]
+            end = start + 8 if args[0] == "linear4_tiled" else rows
+            regions.append((start, end))
+        assert regions[0][0] == 0 and regions[-1][1] == rows
+        assert all(a[1] == b[0] for a, b in zip(regions[:-1], regions[1:]))
