@@ -19,7 +19,7 @@ CSRC = PACKAGE / "csrc"
 BUILD = PACKAGE / "_build"
 LIBRARY = PACKAGE / "libtessery_hip.so"
 
-SOURCES = ("attention.hip", "norm_rope.hip", "linear4.hip", "util.hip", "runtime.cpp")
+SOURCES = ("attention.hip", "norm_rope.hip", "linear4.hip", "qkv4.hip", "util.hip", "runtime.cpp")
 
 # -packed-fp32-ops keeps the device compiler from emitting packed fp32 VALU instructions.
 FLAGS = (

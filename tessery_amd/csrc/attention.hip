@@ -280,89 +280,151 @@ __global__ __launch_bounds__(256, 2) void attn_f32_mfma(const float* __restrict_
 //   accumulator element e = 4a+c of lane half h holds key 16(a>>1) + 8h + 4(a&1) + c. For PV
 //   k-step t the lane's own elements 8t..8t+7 are then the 8 CONSECUTIVE keys 16t+8h..16t+8h+7,
 //   matching a single 16-byte read of the transposed V tile (V^T: [channel][key] in LDS).
-// Key tile 64 (two sub-tiles), one softmax update per tile; l accumulates the fp16-rounded
-// probabilities that PV actually uses, so the output is an exact weighted mean of V rows.
+// One softmax update per key tile of KT keys; l accumulates the fp16-rounded probabilities that PV
+// actually uses, so the output is an exact weighted mean of V rows.
+//
+// FUSED (route attention_f16_norm_rope): Q arrives pre-norm and is RMS-normalized and rotated in
+// fp32 as it is loaded; K arrives already normalized and rotated as two fp16 planes hi + lo
+// (written by norm_rope_f16). Q is also carried as hi + lo, and the score tile accumulates
+// K_hi*Q_lo + K_lo*Q_hi + K_hi*Q_hi in fp32, so the normalized q and k enter the dot products at
+// ~22-bit precision instead of fp16's 11 bits.
+//
+// All global loads are branch-free: out-of-range rows load a clamped in-bounds address and are
+// replaced by zero, so the compiler can issue every load of a phase back to back.
 // ---------------------------------------------------------------------------------------------
-template <int D, typename TOut, bool NORM_Q>
+template <int D, int KT>
+struct F16Tile {
+  static constexpr int KROW = D + 8;            // halves; 16-byte pad puts rows 4 banks apart
+  static constexpr int VROW = KT + 8;           // halves per V^T row (channel)
+  static constexpr int KCH = KT * D / 8;        // 16-byte K chunks per tile
+  static constexpr int KCPT = (KCH + 255) / 256;
+  static constexpr int VIT = (KT / 2) * (D / 8);  // (key pair, channel chunk) items per tile
+  static constexpr int VIPT = (VIT + 255) / 256;
+  static constexpr int NS = D / 16;             // k-steps per score tile
+  static constexpr int NU = KT / 32;            // 32-key sub-tiles per tile
+};
+
+__device__ __forceinline__ int pi_row(int key) {
+  return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
+}
+
+template <int D, typename TOut, bool FUSED, int KT>
 __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
     const _Float16* __restrict__ q, const _Float16* __restrict__ k, const _Float16* __restrict__ v,
     const uint32_t* __restrict__ lengths, TOut* __restrict__ out, int B, int S, int H, int KV,
     float scale_log2, int bidi, const uint16_t* __restrict__ gamma,
-    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, float eps) {
-  constexpr int KT = 64;
-  constexpr int KROW = D + 8;   // halves; 16-byte pad puts consecutive rows 4 banks apart
-  constexpr int VROW = KT + 8;  // halves per V^T row (channel)
-  constexpr int KCH = KT * D / 8;          // 16-byte K chunks per tile
-  constexpr int KCPT = (KCH + 255) / 256;
-  constexpr int VIT = (KT / 2) * (D / 8);  // (key pair, channel chunk) items per tile
-  constexpr int VIPT = (VIT + 255) / 256;
-  constexpr int NS = D / 16;               // k-steps per score tile
-  __shared__ __attribute__((aligned(16))) _Float16 Ks[KT * KROW];
+    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, float eps,
+    size_t k_plane) {
+  using T = F16Tile<D, KT>;
+  constexpr int NS = T::NS, NU = T::NU, KROW = T::KROW, VROW = T::VROW;
+  constexpr int KPLANES = FUSED ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) _Float16 Ks[KPLANES][KT * KROW];
   __shared__ __attribute__((aligned(16))) _Float16 Vt[D * VROW];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const Geom g = make_geom(lengths, B, S, H, KV, bidi, wave);
   const int qpos = g.p0 + l32;
   const bool qvalid = g.active && qpos < S;
+  const int qpos_c = min(qpos, S - 1);
   const int limit = bidi ? g.L : min(qpos + 1, g.L);
   const int ntiles = (g.wg_end + KT - 1) / KT;
+  const size_t kv_base = static_cast<size_t>(g.b) * S * KV + g.kvh;
 
-  // ---- Q fragment: lane holds channels 16s + 8h .. +7 of its query row --------------------
-  half8 qf[NS];
-  {
-    const size_t base = ((static_cast<size_t>(g.b) * S + qpos) * H + g.head) * D + 8 * hh;
+  // ---- tile prefetch registers (branch-free, clamped rows, zero outside [0, L)) -------------
+  half8 kreg[KPLANES][T::KCPT], vreg[T::VIPT][2];
+  auto load_tile = [&](int kt) {
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      half8 t = {};
-      if (qvalid) t = *reinterpret_cast<const half8*>(q + base + 16 * s);
-      qf[s] = t;
+    for (int i = 0; i < T::KCPT; ++i) {
+      const int c = min(tid + 256 * i, T::KCH - 1);
+      const int key = c / (D / 8), ck = c % (D / 8);
+      const int kg = kt * KT + key;
+      const bool ok = kg < g.L;
+      const size_t off = (kv_base + static_cast<size_t>(ok ? kg : 0) * KV) * D + 8 * ck;
+#pragma unroll
+      for (int pl = 0; pl < KPLANES; ++pl) {
+        const half8 t = *reinterpret_cast<const half8*>(k + pl * k_plane + off);
+        kreg[pl][i] = ok ? t : half8{};
+      }
     }
-    if constexpr (NORM_Q) {
-      // Per-head RMSNorm (x * rsqrt(mean(x^2) + eps) * gamma) then split-half RoPE, fp32 math,
-      // the composition of kernels.metal:53-63 and :65-74 applied to one query row.
-      float x[NS][8];
-      float ss = 0.0f;
 #pragma unroll
-      for (int s = 0; s < NS; ++s)
+    for (int i = 0; i < T::VIPT; ++i) {
+      const int c = min(tid + 256 * i, T::VIT - 1);
+      const int kp = c % (KT / 2), ck = c / (KT / 2);
 #pragma unroll
-        for (int m = 0; m < 8; ++m) {
-          x[s][m] = static_cast<float>(qf[s][m]);
-          ss += x[s][m] * x[s][m];
-        }
-      ss += __shfl_xor(ss, 32);
-      const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
-      if (qvalid) {
+      for (int r = 0; r < 2; ++r) {
+        const int kg = kt * KT + 2 * kp + r;
+        const bool ok = kg < g.L;
+        const half8 t = *reinterpret_cast<const half8*>(
+            v + (kv_base + static_cast<size_t>(ok ? kg : 0) * KV) * D + 8 * ck);
+        vreg[i][r] = ok ? t : half8{};
+      }
+    }
+  };
+
+  // ---- Q fragment: lane holds channels 16s + 8h .. +7 of its query row -----------------------
+  const size_t qbase = ((static_cast<size_t>(g.b) * S + qpos_c) * H + g.head) * D + 8 * hh;
+  half8 qh[NS], ql[FUSED ? NS : 1];
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          const uint4v gw = *reinterpret_cast<const uint4v*>(gamma + 16 * s + 8 * hh);
+  for (int s = 0; s < NS; ++s) qh[s] = *reinterpret_cast<const half8*>(q + qbase + 16 * s);
+  if (ntiles > 0) load_tile(0);  // overlaps the Q normalization below
+  if constexpr (FUSED) {
+    // Per-head RMSNorm (x * rsqrt(mean(x^2) + eps) * gamma) then split-half RoPE, fp32 math:
+    // the composition of kernels.metal:53-63 and :65-74 applied to one query row.
+    uint4v gw[NS];
+    floatx4 cs[NS / 2][2], sn[NS / 2][2];
+    const float* ct = rope_cos + static_cast<size_t>(qpos_c) * (D / 2) + 8 * hh;
+    const float* st = rope_sin + static_cast<size_t>(qpos_c) * (D / 2) + 8 * hh;
 #pragma unroll
-          for (int m = 0; m < 8; ++m) {
-            const uint16_t w = static_cast<uint16_t>((gw[m >> 1] >> (16 * (m & 1))) & 0xffffu);
-            x[s][m] = x[s][m] * inv * bf16_to_float(w);
-          }
-        }
-        const float* cs = rope_cos + static_cast<size_t>(qpos) * (D / 2);
-        const float* sn = rope_sin + static_cast<size_t>(qpos) * (D / 2);
+    for (int s = 0; s < NS; ++s) gw[s] = *reinterpret_cast<const uint4v*>(gamma + 16 * s + 8 * hh);
 #pragma unroll
-        for (int s = 0; s < NS / 2; ++s) {
-          const floatx4 c0 = *reinterpret_cast<const floatx4*>(cs + 16 * s + 8 * hh);
-          const floatx4 c1 = *reinterpret_cast<const floatx4*>(cs + 16 * s + 8 * hh + 4);
-          const floatx4 s0 = *reinterpret_cast<const floatx4*>(sn + 16 * s + 8 * hh);
-          const floatx4 s1 = *reinterpret_cast<const floatx4*>(sn + 16 * s + 8 * hh + 4);
+    for (int s = 0; s < NS / 2; ++s) {
+      cs[s][0] = *reinterpret_cast<const floatx4*>(ct + 16 * s);
+      cs[s][1] = *reinterpret_cast<const floatx4*>(ct + 16 * s + 4);
+      sn[s][0] = *reinterpret_cast<const floatx4*>(st + 16 * s);
+      sn[s][1] = *reinterpret_cast<const floatx4*>(st + 16 * s + 4);
+    }
+    float x[NS][8];
+    float ss = 0.0f;
 #pragma unroll
-          for (int m = 0; m < 8; ++m) {
-            const float cv = m < 4 ? c0[m] : c1[m - 4];
-            const float sv = m < 4 ? s0[m] : s1[m - 4];
-            const float a = x[s][m], bb = x[s + NS / 2][m];
-            x[s][m] = a * cv - bb * sv;
-            x[s + NS / 2][m] = a * sv + bb * cv;
-          }
-        }
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        x[s][m] = static_cast<float>(qh[s][m]);
+        ss += x[s][m] * x[s][m];
+      }
+    ss += __shfl_xor(ss, 32);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const uint16_t w = static_cast<uint16_t>((gw[s][m >> 1] >> (16 * (m & 1))) & 0xffffu);
+        x[s][m] = x[s][m] * inv * bf16_to_float(w);
       }
 #pragma unroll
-      for (int s = 0; s < NS; ++s)
+    for (int s = 0; s < NS / 2; ++s)
 #pragma unroll
-        for (int m = 0; m < 8; ++m) qf[s][m] = static_cast<_Float16>(x[s][m]);
+      for (int m = 0; m < 8; ++m) {
+        const float cv = cs[s][m >> 2][m & 3], sv = sn[s][m >> 2][m & 3];
+        const float a = x[s][m], bb = x[s + NS / 2][m];
+        x[s][m] = a * cv - bb * sv;
+        x[s + NS / 2][m] = a * sv + bb * cv;
+      }
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const _Float16 hi = static_cast<_Float16>(x[s][m]);
+        qh[s][m] = hi;
+        ql[s][m] = static_cast<_Float16>(x[s][m] - static_cast<float>(hi));
+      }
+  }
+  if (!qvalid) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qh[s] = half8{};
+    if constexpr (FUSED) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) ql[s] = half8{};
     }
   }
 
@@ -373,51 +435,23 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
     for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
 
-  half8 kreg[KCPT], vreg[VIPT][2];
-  auto load_tile = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < KCPT; ++i) {
-      const int c = tid + 256 * i;
-      const int key = c / (D / 8), ck = c % (D / 8);
-      const int kg = kt * KT + key;
-      half8 t = {};
-      if (c < KCH && kg < g.L)
-        t = *reinterpret_cast<const half8*>(
-            k + ((static_cast<size_t>(g.b) * S + kg) * KV + g.kvh) * D + 8 * ck);
-      kreg[i] = t;
-    }
-#pragma unroll
-    for (int i = 0; i < VIPT; ++i) {
-      const int c = tid + 256 * i;
-      const int kp = c % (KT / 2), ck = c / (KT / 2);
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int kg = kt * KT + 2 * kp + r;
-        half8 t = {};
-        if (c < VIT && kg < g.L)
-          t = *reinterpret_cast<const half8*>(
-              v + ((static_cast<size_t>(g.b) * S + kg) * KV + g.kvh) * D + 8 * ck);
-        vreg[i][r] = t;
-      }
-    }
-  };
-  if (ntiles > 0) load_tile(0);
-
   for (int kt = 0; kt < ntiles; ++kt) {
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < KCPT; ++i) {
+    for (int i = 0; i < T::KCPT; ++i) {
       const int c = tid + 256 * i;
-      if (c < KCH) {
+      if (c < T::KCH) {
         const int key = c / (D / 8), ck = c % (D / 8);
-        const int row = (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);  // pi(key)
-        *reinterpret_cast<half8*>(&Ks[row * KROW + 8 * ck]) = kreg[i];
+        const int row = (key & ~31) | pi_row(key & 31);
+#pragma unroll
+        for (int pl = 0; pl < KPLANES; ++pl)
+          *reinterpret_cast<half8*>(&Ks[pl][row * KROW + 8 * ck]) = kreg[pl][i];
       }
     }
 #pragma unroll
-    for (int i = 0; i < VIPT; ++i) {
+    for (int i = 0; i < T::VIPT; ++i) {
       const int c = tid + 256 * i;
-      if (c < VIT) {
+      if (c < T::VIT) {
         const int kp = c % (KT / 2), ck = c / (KT / 2);
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
@@ -429,53 +463,69 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
     __syncthreads();
     if (kt + 1 < ntiles) load_tile(kt + 1);
     if (kt * KT < g.wave_end) {
-      floatx16 sc[2];
+      floatx16 sc[NU];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
+      for (int u = 0; u < NU; ++u) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) sc[u][e] = 0.0f;
+        const int row = (32 * u + l32) * KROW + 8 * hh;
+        if constexpr (FUSED) {
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            const half8 ahi = *reinterpret_cast<const half8*>(&Ks[0][row + 16 * s]);
+            const half8 alo = *reinterpret_cast<const half8*>(&Ks[1][row + 16 * s]);
+            sc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi, ql[s], sc[u], 0, 0, 0);
+            sc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo, qh[s], sc[u], 0, 0, 0);
+          }
+        }
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-          const half8 a = *reinterpret_cast<const half8*>(&Ks[(32 * u + l32) * KROW + 16 * s + 8 * hh]);
-          sc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], sc[u], 0, 0, 0);
+          const half8 a = *reinterpret_cast<const half8*>(&Ks[0][row + 16 * s]);
+          sc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qh[s], sc[u], 0, 0, 0);
         }
       }
-      const bool full = kt * KT + KT <= g.limit_min;
+      // masks only where the tile crosses some row's key limit
+      if (kt * KT + KT > g.limit_min) {
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int a = e >> 2, c = e & 3;
+            const int key = kt * KT + 32 * u + 16 * (a >> 1) + 8 * hh + 4 * (a & 1) + c;
+            if (key >= limit) sc[u][e] = -INFINITY;
+          }
+      }
       float mloc = -INFINITY;
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < NU; ++u)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int a = e >> 2, c = e & 3;
-          const int key = kt * KT + 32 * u + 16 * (a >> 1) + 8 * hh + 4 * (a & 1) + c;
-          float val = sc[u][e] * scale_log2;
-          if (!full && key >= limit) val = -INFINITY;
-          sc[u][e] = val;
-          mloc = fmaxf(mloc, val);
-        }
-      const float m_tile = fmaxf(mloc, __shfl_xor(mloc, 32));
-      const float m_new = fmaxf(m_run, m_tile);
+        for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, sc[u][e]);
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32)) * scale_log2;
+      const float m_new = fmaxf(m_run, mloc);
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
       const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
-      half8 pb[2][2];
+      half8 pb[NU][2];
       float lsum = 0.0f;
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < NU; ++u)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const _Float16 ph = static_cast<_Float16>(__builtin_amdgcn_exp2f(sc[u][e] - m_use));
+          const _Float16 ph =
+              static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(sc[u][e], scale_log2, -m_use)));
           pb[u][e >> 3][e & 7] = ph;
           lsum += static_cast<float>(ph);
         }
       lsum += __shfl_xor(lsum, 32);
       l_run = l_run * corr + lsum;
       m_run = m_new;
+      if (__any(corr != 1.0f)) {
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
+        for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) o[dt][e] *= corr;
+          for (int e = 0; e < 16; ++e) o[dt][e] *= corr;
+      }
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < NU; ++u)
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -566,35 +616,36 @@ hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int D, bool NORM>
+template <int D, bool FUSED, int KT>
 static void launch_f16_d(const AttnArgs& a, unsigned grid, float sl2, hipStream_t st) {
   auto q = static_cast<const _Float16*>(a.q), k = static_cast<const _Float16*>(a.k),
        v = static_cast<const _Float16*>(a.v);
+  const size_t plane = static_cast<size_t>(a.B) * a.S * a.KV * a.D;
   if (a.out_f16)
-    attn_f16_mfma<D, _Float16, NORM><<<grid, 256, 0, st>>>(
+    attn_f16_mfma<D, _Float16, FUSED, KT><<<grid, 256, 0, st>>>(
         q, k, v, a.lengths, static_cast<_Float16*>(a.out), a.B, a.S, a.H, a.KV, sl2, a.bidi,
-        a.gamma_q, a.rope_cos, a.rope_sin, a.eps);
+        a.gamma_q, a.rope_cos, a.rope_sin, a.eps, plane);
   else
-    attn_f16_mfma<D, float, NORM><<<grid, 256, 0, st>>>(
+    attn_f16_mfma<D, float, FUSED, KT><<<grid, 256, 0, st>>>(
         q, k, v, a.lengths, static_cast<float*>(a.out), a.B, a.S, a.H, a.KV, sl2, a.bidi,
-        a.gamma_q, a.rope_cos, a.rope_sin, a.eps);
+        a.gamma_q, a.rope_cos, a.rope_sin, a.eps, plane);
 }
 
 hipError_t launch_attention_f16(const AttnArgs& a, hipStream_t st) {
   const unsigned grid = mfma_grid(a.B, a.S, a.H, a.KV);
   if (!grid) return hipSuccess;
   const float sl2 = a.scale * kLog2e;
-  const bool norm = a.gamma_q != nullptr;
-  if (norm && (!a.rope_cos || !a.rope_sin)) return hipErrorInvalidValue;
+  const bool fused = a.gamma_q != nullptr;
+  if (fused && (!a.rope_cos || !a.rope_sin)) return hipErrorInvalidValue;
   switch (a.D) {
     case 32:
-      norm ? launch_f16_d<32, true>(a, grid, sl2, st) : launch_f16_d<32, false>(a, grid, sl2, st);
+      fused ? launch_f16_d<32, true, 64>(a, grid, sl2, st) : launch_f16_d<32, false, 64>(a, grid, sl2, st);
       break;
     case 64:
-      norm ? launch_f16_d<64, true>(a, grid, sl2, st) : launch_f16_d<64, false>(a, grid, sl2, st);
+      fused ? launch_f16_d<64, true, 64>(a, grid, sl2, st) : launch_f16_d<64, false, 64>(a, grid, sl2, st);
       break;
     case 128:
-      norm ? launch_f16_d<128, true>(a, grid, sl2, st) : launch_f16_d<128, false>(a, grid, sl2, st);
+      fused ? launch_f16_d<128, true, 32>(a, grid, sl2, st) : launch_f16_d<128, false, 64>(a, grid, sl2, st);
       break;
     default:
       return hipErrorInvalidValue;

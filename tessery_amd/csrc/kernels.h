@@ -21,7 +21,8 @@ struct AttnArgs {
   int bidi;
   int in_f16;   // q/k/v are fp16 (else fp32)
   int out_f16;  // out is fp16 (else fp32)
-  // Fused per-head RMSNorm + RoPE of Q (fp16 MFMA kernel only); null when unused.
+  // Fused per-head RMSNorm + RoPE of Q (fp16 MFMA kernel only); null when unused. With it, k
+  // holds two fp16 planes (hi, then lo) of the normalized, rotated keys.
   const uint16_t* gamma_q;  // bf16 [D]
   const float* rope_cos;    // [S, D/2]
   const float* rope_sin;    // [S, D/2]
@@ -39,11 +40,12 @@ hipError_t launch_rms_norm_f32(const float* x, const uint16_t* w, float* out, in
 hipError_t launch_rope_f32(float* x, const float* cos_tab, const float* sin_tab, uint32_t n,
                            int heads, int seq, int dim, hipStream_t st);
 // Fused per-head RMSNorm + RoPE on fp16 rows [B,S,heads,D] -> fp16 rows, rows with
-// position >= lengths[b] skipped (they are padding that attention never reads).
+// position >= lengths[b] skipped (they are padding that attention never reads). With split the
+// output holds two planes: y[0 : rows*D] = fp16(r), y[rows*D : 2*rows*D] = fp16(r - fp16(r)).
 hipError_t launch_norm_rope_f16(const _Float16* x, _Float16* y, const uint16_t* gamma,
                                 const float* cos_tab, const float* sin_tab,
                                 const uint32_t* lengths, int B, int S, int heads, int D,
-                                float eps, hipStream_t st);
+                                float eps, bool split, hipStream_t st);
 
 // uint4 affine group-64 projection, fp32 activations, bf16 scale/bias (tessery linear4 family,
 // kernels.metal:11-19, 32-51, 489-605, 655-684, 733-773). Computes rows [row0, row1).

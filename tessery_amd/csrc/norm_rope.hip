@@ -46,7 +46,9 @@ __global__ __launch_bounds__(256) void rope_f32(float* x, const float* __restric
 }
 
 // fp16 rows [B,S,heads,D]; T = D/16 lanes per row, lane j owns channels 8j..8j+7 and their
-// RoPE partners D/2+8j..D/2+8j+7, so the rotation never leaves the lane. fp32 math.
+// RoPE partners D/2+8j..D/2+8j+7, so the rotation never leaves the lane. fp32 math. With
+// y_lo != null the result is also written as a second fp16 plane y_lo = fp16(y - y_hi), so that
+// y_hi + y_lo carries the fp32 value to ~22 bits for the split-precision attention.
 template <int D>
 __global__ __launch_bounds__(256) void norm_rope_f16(const _Float16* __restrict__ x,
                                                      _Float16* __restrict__ y,
@@ -54,7 +56,8 @@ __global__ __launch_bounds__(256) void norm_rope_f16(const _Float16* __restrict_
                                                      const float* __restrict__ cos_tab,
                                                      const float* __restrict__ sin_tab,
                                                      const uint32_t* __restrict__ lengths, int B,
-                                                     int S, int heads, float eps) {
+                                                     int S, int heads, float eps,
+                                                     _Float16* __restrict__ y_lo) {
   constexpr int T = D / 16;
   constexpr int HALF = D / 2;
   const int tid = threadIdx.x;
@@ -91,7 +94,7 @@ __global__ __launch_bounds__(256) void norm_rope_f16(const _Float16* __restrict_
   const uint4v ghi = *reinterpret_cast<const uint4v*>(gamma + HALF + 8 * j);
   const float* cs = cos_tab + static_cast<size_t>(pos) * HALF + 8 * j;
   const float* sn = sin_tab + static_cast<size_t>(pos) * HALF + 8 * j;
-  half8 olo, ohi;
+  half8 first, second, first_lo, second_lo;
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
     const int sh = 16 * (m & 1);
@@ -99,11 +102,18 @@ __global__ __launch_bounds__(256) void norm_rope_f16(const _Float16* __restrict_
     const float wh = bf16_to_float(static_cast<uint16_t>((ghi[m >> 1] >> sh) & 0xffffu));
     const float p = a[m] * inv * wl, q = c[m] * inv * wh;
     const float cv = cs[m], sv = sn[m];
-    olo[m] = static_cast<_Float16>(p * cv - q * sv);
-    ohi[m] = static_cast<_Float16>(p * sv + q * cv);
+    const float r0 = p * cv - q * sv, r1 = p * sv + q * cv;
+    first[m] = static_cast<_Float16>(r0);
+    second[m] = static_cast<_Float16>(r1);
+    first_lo[m] = static_cast<_Float16>(r0 - static_cast<float>(first[m]));
+    second_lo[m] = static_cast<_Float16>(r1 - static_cast<float>(second[m]));
   }
-  *reinterpret_cast<half8*>(y + base + 8 * j) = olo;
-  *reinterpret_cast<half8*>(y + base + HALF + 8 * j) = ohi;
+  *reinterpret_cast<half8*>(y + base + 8 * j) = first;
+  *reinterpret_cast<half8*>(y + base + HALF + 8 * j) = second;
+  if (y_lo) {
+    *reinterpret_cast<half8*>(y_lo + base + 8 * j) = first_lo;
+    *reinterpret_cast<half8*>(y_lo + base + HALF + 8 * j) = second_lo;
+  }
 }
 
 hipError_t launch_rms_norm_f32(const float* x, const uint16_t* w, float* out, int rows, int cols,
@@ -123,20 +133,21 @@ hipError_t launch_rope_f32(float* x, const float* cos_tab, const float* sin_tab,
 hipError_t launch_norm_rope_f16(const _Float16* x, _Float16* y, const uint16_t* gamma,
                                 const float* cos_tab, const float* sin_tab,
                                 const uint32_t* lengths, int B, int S, int heads, int D,
-                                float eps, hipStream_t st) {
+                                float eps, bool split, hipStream_t st) {
   const int64_t rows = static_cast<int64_t>(B) * S * heads;
   if (!rows) return hipSuccess;
   const int per_block = 256 / (D / 16);
   const unsigned grid = static_cast<unsigned>((rows + per_block - 1) / per_block);
+  _Float16* y_lo = split ? y + static_cast<size_t>(rows) * D : nullptr;
   switch (D) {
     case 32:
-      norm_rope_f16<32><<<grid, 256, 0, st>>>(x, y, gamma, cos_tab, sin_tab, lengths, B, S, heads, eps);
+      norm_rope_f16<32><<<grid, 256, 0, st>>>(x, y, gamma, cos_tab, sin_tab, lengths, B, S, heads, eps, y_lo);
       break;
     case 64:
-      norm_rope_f16<64><<<grid, 256, 0, st>>>(x, y, gamma, cos_tab, sin_tab, lengths, B, S, heads, eps);
+      norm_rope_f16<64><<<grid, 256, 0, st>>>(x, y, gamma, cos_tab, sin_tab, lengths, B, S, heads, eps, y_lo);
       break;
     case 128:
-      norm_rope_f16<128><<<grid, 256, 0, st>>>(x, y, gamma, cos_tab, sin_tab, lengths, B, S, heads, eps);
+      norm_rope_f16<128><<<grid, 256, 0, st>>>(x, y, gamma, cos_tab, sin_tab, lengths, B, S, heads, eps, y_lo);
       break;
     default:
       return hipErrorInvalidValue;

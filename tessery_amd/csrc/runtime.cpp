@@ -75,7 +75,7 @@ const RouteName kRoutes[] = {
     {"linear4_16x32_k64", R_LINEAR4_16X32, 5},
     {"linear4_32x32_k64", R_LINEAR4_32X32, 5},
     {"linear4_small3", R_LINEAR4_SMALL3, 5},
-    {"qkv4_f16", R_QKV4_F16, 8},
+    {"qkv4_f16", R_QKV4_F16, 7},
     {"add", R_ADD, 3},
     {"copy", R_COPY, 2},
 };
@@ -272,17 +272,20 @@ bool validate(Route r, const Params& p, uint64_t threads, uint32_t group, const 
     case R_ATTENTION_F16_NORM_ROPE: {
       AttnShape s;
       if (!attn_shape(r, p, threads, group, &s) || !attn_sizes(s, sz)) return false;
-      if (r == R_ATTENTION_F16_NORM_ROPE)
-        return sz[5] >= s.D * 2 && p.theta > 0.0f && p.eps >= 0.0f && std::isfinite(p.theta);
+      if (r == R_ATTENTION_F16_NORM_ROPE)  // k holds hi and lo planes
+        return sz[1] >= 2 * s.B * s.S * s.KV * s.D * 2 && sz[5] >= s.D * 2 && p.theta > 0.0f &&
+               p.eps >= 0.0f && std::isfinite(p.theta);
       return true;
     }
-    case R_NORM_ROPE_F16: {  // buffers: x, gamma, lengths, y
+    case R_NORM_ROPE_F16: {  // buffers: x, gamma, lengths, y; u1 bit 0: y gets hi + lo planes
       const uint64_t heads = p.heads, S = p.seq, D = p.dim, tokens = threads;
       if (group != 256 || !heads || heads > 1024 || !S || tokens % S || tokens > kMaxTokens ||
           (D != 32 && D != 64 && D != 128) || !(p.theta > 0.0f) || !std::isfinite(p.theta))
         return false;
       const uint64_t bytes = tokens * heads * D * 2;
-      return sz[0] >= bytes && sz[1] >= D * 2 && sz[2] >= tokens / S * 4 && sz[3] >= bytes;
+      const uint64_t planes = (p.u1 & 1u) ? 2 : 1;
+      return sz[0] >= bytes && sz[1] >= D * 2 && sz[2] >= tokens / S * 4 &&
+             sz[3] >= planes * bytes;
     }
     case R_RMS_NORM: {  // kernels.metal:53-63: rows*32 threads, groups of 32
       const uint64_t cols = p.cols;
@@ -310,6 +313,15 @@ bool validate(Route r, const Params& p, uint64_t threads, uint32_t group, const 
       return sz[0] >= rr.r1 * k * 4 && sz[1] >= cols * (k / 8) * 4 &&
              sz[2] >= cols * (k / 64) * 2 && sz[3] >= cols * (k / 64) * 2 &&
              sz[4] >= rr.r1 * cols * 4;
+    }
+    case R_QKV4_F16: {  // buffers: x, w_qkv, s_qkv, b_qkv, yq, yk, yv (weights concatenated on N)
+      const uint64_t M = p.rows, K = p.k, nq = p.cols, nkv = p.n, ntot = nq + 2 * nkv;
+      if (group != 256 || threads != M || !M || M > kMaxTokens || !K || K % 64 || K > 65536 ||
+          !nq || nq % 128 || !nkv || nkv % 128 || ntot > 65536)
+        return false;
+      return sz[0] >= M * K * 2 && sz[1] >= ntot * (K / 8) * 4 && sz[2] >= ntot * (K / 64) * 2 &&
+             sz[3] >= ntot * (K / 64) * 2 && sz[4] >= M * nq * 2 && sz[5] >= M * nkv * 2 &&
+             sz[6] >= M * nkv * 2;
     }
     case R_ADD: {  // kernels.metal:300-304
       const uint64_t n = p.n;
@@ -427,7 +439,8 @@ hipError_t launch(Runtime* rt, const Op& op) {
           static_cast<const _Float16*>(op.ptr[0]), static_cast<_Float16*>(op.ptr[3]),
           static_cast<const uint16_t*>(op.ptr[1]), t->cos, t->sin,
           static_cast<const uint32_t*>(op.ptr[2]), static_cast<int>(op.threads / p.seq),
-          static_cast<int>(p.seq), static_cast<int>(p.heads), static_cast<int>(p.dim), p.eps, st);
+          static_cast<int>(p.seq), static_cast<int>(p.heads), static_cast<int>(p.dim), p.eps,
+          (p.u1 & 1u) != 0, st);
     }
     case R_RMS_NORM:
       return tessery::launch_rms_norm_f32(
@@ -454,6 +467,24 @@ hipError_t launch(Runtime* rt, const Op& op) {
           static_cast<const uint16_t*>(op.ptr[2]), static_cast<const uint16_t*>(op.ptr[3]),
           static_cast<float*>(op.ptr[4]), static_cast<int>(rr.r0), static_cast<int>(rr.r1),
           static_cast<int>(p.cols), static_cast<int>(p.k), st);
+    }
+    case R_QKV4_F16: {
+      tessery::Qkv4Args a{};
+      const int K = static_cast<int>(p.k);
+      const int nq = static_cast<int>(p.cols), nkv = static_cast<int>(p.n);
+      const int offsets[3] = {0, nq, nq + nkv};
+      a.x = static_cast<const _Float16*>(op.ptr[0]);
+      for (int i = 0; i < 3; ++i) {
+        a.w[i] = static_cast<const uint32_t*>(op.ptr[1]) + static_cast<size_t>(offsets[i]) * (K / 8);
+        a.s[i] = static_cast<const uint16_t*>(op.ptr[2]) + static_cast<size_t>(offsets[i]) * (K / 64);
+        a.b[i] = static_cast<const uint16_t*>(op.ptr[3]) + static_cast<size_t>(offsets[i]) * (K / 64);
+        a.y[i] = static_cast<_Float16*>(op.ptr[4 + i]);
+        a.n[i] = i == 0 ? nq : nkv;
+      }
+      a.M = static_cast<int>(p.rows);
+      a.K = K;
+      a.scale_bf16 = p.u1 & 1u;
+      return tessery::launch_qkv4_f16(a, st);
     }
     case R_ADD:
       return tessery::launch_add_f32(static_cast<const float*>(op.ptr[0]),

@@ -220,19 +220,20 @@ def test_f16_scalar_route(runtime, d):
     assert np.max(np.abs(got - ref.attention(q, k, v, lengths, bidirectional=False))) <= F16_MAX
 
 
-def norm_rope_attend(engine, t, lengths, shape, out_dtype="f16"):
+def norm_rope_attend(engine, t, lengths, shape, out_dtype="f32"):
     b, s, h, kv, d = shape.batch, shape.seq, shape.heads, shape.kv_heads, shape.dim
     arrays = [t["q"], t["k"], t["v"], lengths.astype(np.uint32)]
     bufs = [engine.upload(a) for a in arrays]
     odt = np.float16 if out_dtype == "f16" else np.float32
     bufs.append(engine.buffer(t["q"].size * np.dtype(odt).itemsize))
-    bufs += [engine.upload(t["q_norm"]), engine.upload(t["k_norm"]), engine.buffer(t["k"].nbytes)]
+    bufs += [engine.upload(t["q_norm"]), engine.upload(t["k_norm"]), engine.buffer(2 * t["k"].nbytes)]
     try:
         with engine.command():
             engine._attention_norm_rope(bufs, tokens=b * s, seq=s, heads=h, kv_heads=kv, dim=d,
                                         eps=workloads.EPS, theta=workloads.THETA,
                                         out_dtype=out_dtype)
-        return engine.read(bufs[4], t["q"].shape, odt), engine.read(bufs[7], t["k"].shape, np.float16)
+        planes = engine.read(bufs[7], (2,) + t["k"].shape, np.float16)
+        return engine.read(bufs[4], t["q"].shape, odt), planes
     finally:
         for x in bufs:
             x.close()
@@ -246,19 +247,23 @@ def oracle_norm_rope(t, lengths):
     return k, ref.attention(q, k, t["v"], lengths, bidirectional=False)
 
 
-def test_qwen_norm_rope_fixture(runtime):
+@pytest.mark.parametrize("out_dtype", ["f32", "f16"])
+def test_qwen_norm_rope_fixture(runtime, out_dtype):
     f = np.load(GOLDEN / "qwen_small.npz")
     t = {name: f[name] for name in ("q", "k", "v", "q_norm", "k_norm")}
     shape = workloads.Shape(2, 40, 4, 2, 128, causal=True)
-    out, k_work = norm_rope_attend(runtime, t, f["lengths"], shape)
+    out, planes = norm_rope_attend(runtime, t, f["lengths"], shape, out_dtype)
     assert np.max(np.abs(out.astype(np.float64) - f["expected"])) <= F16_MAX
-    # the k prologue writes valid rows only, each within fp16 rounding of the float64 value
+    # the k prologue writes valid rows only: hi within fp16 rounding of the float64 value, and
+    # hi + lo within fp32 rounding of it
+    hi, lo = planes[0].astype(np.float64), planes[1].astype(np.float64)
     for bi, length in enumerate(f["lengths"]):
         exp = f["k_normed"][bi, :length]
-        assert np.all(np.abs(k_work[bi, :length] - exp) <= 2.0**-10 * np.abs(exp) + 1e-6)
+        assert np.all(np.abs(hi[bi, :length] - exp) <= 2.0**-11 * np.abs(exp) + 1e-7)
+        assert np.all(np.abs(hi[bi, :length] + lo[bi, :length] - exp) <= 2e-6 * np.abs(exp) + 1e-7)
 
 
-@pytest.mark.parametrize("out_dtype", ["f16", "f32"])
+@pytest.mark.parametrize("out_dtype", ["f32", "f16"])
 def test_qwen3_8x512(runtime, out_dtype):
     shape, lengths = workloads.qwen3_8x512()
     t = workloads.qwen_layer(shape, 0, seed=3)
@@ -268,11 +273,12 @@ def test_qwen3_8x512(runtime, out_dtype):
     assert err <= F16_MAX, err
 
 
-def test_qwen3_32x512_layer0(runtime):
-    """The benchmark workload itself (log-uniform lengths, execution width 464), layer 0."""
+@pytest.mark.parametrize("layer", [0, 27])
+def test_qwen3_32x512(runtime, layer):
+    """The benchmark workload itself (log-uniform lengths, execution width 464, fp32 output)."""
     shape, lengths = workloads.qwen3_32x512()
-    t = workloads.qwen_layer(shape, 0, seed=4)
-    out, _ = norm_rope_attend(runtime, t, lengths, shape, "f16")
+    t = workloads.qwen_layer(shape, layer, seed=4)
+    out, _ = norm_rope_attend(runtime, t, lengths, shape, "f32")
     _, expected = oracle_norm_rope(t, lengths)
     err = np.max(np.abs(out.astype(np.float64) - expected))
     assert err <= F16_MAX, err

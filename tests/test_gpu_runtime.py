@@ -1,0 +1,132 @@
+"""Runtime lifecycle on the GPU: resources, workspace leases, aborts, profiling limits and plan
+replay (the behaviour tessery's test_kernels.py:41-52, 578-647 checks on its Metal runtime)."""
+
+import numpy as np
+import pytest
+
+from oracle import attention as ref
+from tessery_amd import InferenceError
+from tests.test_gpu_attention import check_f32
+
+pytestmark = pytest.mark.gpu
+
+
+def test_add_and_resources(runtime):
+    rng = np.random.default_rng(42)
+    a = rng.normal(size=(7, 37)).astype(np.float32)
+    b = rng.normal(size=a.shape).astype(np.float32)
+    np.testing.assert_array_equal(runtime.add(a, b), a + b)
+    assert runtime.active_bytes == 0
+    assert runtime.peak_bytes == a.nbytes * 3
+    with pytest.raises(InferenceError):
+        runtime.add(a, b[:1])
+    with pytest.raises(InferenceError):
+        runtime.buffer(0)
+
+
+def test_workspace_reuse_bound_abort_and_trim(runtime):
+    runtime.workspace_limit_bytes = 1024
+    with runtime._workspace() as allocate:
+        a, b = allocate(512), allocate(512)
+        assert a is not b
+        with runtime.command():
+            runtime._dispatch("add", [a, b, a], threads=128, n=128)
+    assert runtime.active_bytes == runtime.cache_bytes == 1024
+    allocations = runtime.diagnostics()["allocations"]
+    with pytest.raises(InferenceError), runtime._workspace() as allocate:
+        recovered = allocate(512)
+        with runtime.command():
+            runtime._dispatch("nonexistent_kernel", [recovered], threads=1)
+    assert runtime.diagnostics()["allocations"] == allocations
+    with pytest.raises(InferenceError):
+        allocate(512)
+    with runtime._workspace() as allocate:
+        large = allocate(2048)
+        assert large.pointer
+    assert not large.pointer
+    assert runtime.cache_bytes <= 1024
+    runtime.trim_workspace()
+    assert runtime.active_bytes == runtime.cache_bytes == 0
+
+
+def test_invalid_shapes_are_rejected_before_launch(runtime):
+    """A buffer smaller than the shape Params imply is refused at dispatch time."""
+    q = np.zeros((1, 64, 4, 32), np.float32)
+    small = np.zeros((1, 32, 2, 32), np.float32)
+    bufs = [runtime.upload(q), runtime.upload(small), runtime.upload(small),
+            runtime.upload(np.array([64], np.uint32)), runtime.buffer(q.nbytes)]
+    try:
+        with pytest.raises(InferenceError), runtime.command():
+            runtime._attention(bufs, tokens=64, seq=64, heads=4, kv_heads=2, dim=32)
+        with pytest.raises(InferenceError), runtime.command():  # heads not a multiple of kv
+            runtime._attention(bufs[:1] * 3 + bufs[3:], tokens=64, seq=64, heads=4, kv_heads=3, dim=32)
+    finally:
+        for b in bufs:
+            b.close()
+
+
+def test_aborted_command_launches_nothing(runtime):
+    x = np.arange(64, dtype=np.float32)
+    a, out = runtime.upload(x), runtime.upload(np.full(64, -1.0, np.float32))
+    try:
+        with pytest.raises(InferenceError), runtime.command():
+            runtime._dispatch("add", [a, a, out], threads=64, n=64)
+            runtime._dispatch("absent", [a], threads=1)
+        np.testing.assert_array_equal(runtime.read(out, (64,)), -1.0)
+    finally:
+        a.close()
+        out.close()
+
+
+def test_profile_timings_abort_and_recovery(runtime):
+    a = np.arange(4096, dtype=np.float32)
+    with runtime.profile_kernels() as records:
+        np.testing.assert_array_equal(runtime.add(a, a), a + a)
+        assert len(records) == 1 and records[0]["kernel"] == "add"
+        assert np.isfinite(records[0]["gpu_seconds"]) and records[0]["gpu_seconds"] > 0
+        with pytest.raises(InferenceError), runtime.profile_kernels():
+            pass
+        with pytest.raises(InferenceError), runtime.command():
+            runtime._dispatch("absent", [], threads=1)
+        assert len(records) == 1
+        np.testing.assert_array_equal(runtime.add(a, a), a + a)
+        assert len(records) == 2
+    assert runtime.active_bytes == 0
+
+
+def test_profile_capacity_aborts_without_partial_results(runtime):
+    a = np.ones(1, dtype=np.float32)
+    buffers = [runtime.upload(a) for _ in range(3)]
+    try:
+        with runtime.profile_kernels() as records:
+            with pytest.raises(InferenceError), runtime.command():
+                for _ in range(2049):
+                    runtime._dispatch("add", buffers, threads=1, n=1)
+            assert records == []
+            np.testing.assert_array_equal(runtime.add(a, a), a + a)
+            assert len(records) == 1
+    finally:
+        for b in buffers:
+            b.close()
+
+
+def test_plan_capture_and_replay(runtime):
+    rng = np.random.default_rng(12)
+    q = rng.normal(size=(2, 128, 4, 32)).astype(np.float32)
+    k, v = [rng.normal(size=(2, 128, 2, 32)).astype(np.float32) for _ in range(2)]
+    lengths = np.array([128, 50], np.uint32)
+    expected = ref.attention(q, k, v, lengths, bidirectional=False)
+    outs = []
+    for _ in range(3):
+        with runtime._workspace() as new:
+            with runtime.command():
+                bufs = [new(a.nbytes, a) for a in (q, k, v, lengths)] + [new(q.nbytes)]
+                with runtime._execution_plan(("attn", 2, 128), bufs) as replayed:
+                    if not replayed:
+                        runtime._attention(bufs, tokens=256, seq=128, heads=4, kv_heads=2, dim=32)
+            outs.append(runtime.read(bufs[-1], q.shape))  # still inside the lease
+    for out in outs:
+        check_f32(out, expected)
+    diag = runtime.diagnostics()
+    assert diag["plan_builds"] == 1 and diag["plan_hits"] == 2
+    assert diag["dispatches"] == {"attention_tiled": 3}

@@ -49,9 +49,13 @@ def test_norm_rope_route_sequence():
                                     dim=128, eps=1e-6, theta=1e6)
     assert [a[0] for a, _ in calls] == ["norm_rope_f16", "attention_f16_norm_rope"]
     assert calls[0][0][1] == ["b", "g", "d", "h"]
-    assert calls[0][1]["heads"] == 8
+    assert calls[0][1]["heads"] == 8 and calls[0][1]["flags"] == 1  # hi + lo planes
     assert calls[1][0][1] == ["a", "h", "c", "d", "e", "f"]
-    assert calls[1][1]["heads"] == 16 and calls[1][1]["kv_heads"] == 8 and calls[1][1]["out_f16"] == 1
+    assert calls[1][1]["heads"] == 16 and calls[1][1]["kv_heads"] == 8 and calls[1][1]["out_f16"] == 0
+    calls.clear()
+    HipRuntime._attention_norm_rope(fake, bufs, tokens=1024, seq=512, heads=16, kv_heads=8,
+                                    dim=128, out_dtype="f16")
+    assert calls[1][1]["out_f16"] == 1
 
 
 @pytest.mark.parametrize("rows,cols,k,selected", ROUTES["linear4"]["small3"])
