@@ -81,13 +81,49 @@ __global__ __launch_bounds__(64) void attn_scalar(const TIn* __restrict__ q,
 }
 
 // ---------------------------------------------------------------------------------------------
-// Workgroup geometry shared by the MFMA kernels.
-//   grid = planes * wgs_per_plane, plane = (batch row, kv head), 4 row-blocks of 32 queries per
-//   workgroup, row-block rb = pos_block * G + head_in_group.
-// blockIdx.x % planes selects the plane, so with planes % 8 == 0 every workgroup of a plane lands
-// on the same XCD (round-robin dispatch) and K/V of that plane stay in one L2. The plane-major
-// index runs over row-blocks in reverse: the last (longest causal) query blocks start first.
+// Workgroup geometry of the fp32 MFMA kernel: grid = planes * wgs_per_plane, four row-blocks of
+// 32 queries per workgroup, row-block rb = pos_block * G + head_in_group, order from schedule().
 // ---------------------------------------------------------------------------------------------
+// Workgroup -> (plane, block-within-plane) schedule. A plane is one (batch row, kv head); its
+// workgroups share the plane's K/V tiles. Workgroups are dispatched round-robin over the eight
+// XCDs, each with its own L2, so index i runs on XCD i % 8. The schedule gives every XCD whole
+// planes and lists each plane's workgroups consecutively, so the K/V tiles of a plane are
+// fetched into one L2 once and reused while that plane's workgroups run together. Planes are
+// ordered by the length of their batch row, longest first (causal and bidirectional cost both
+// grow with it), and inside a plane the last (longest causal) query blocks go first.
+// The ranking is computed by every wavefront from `lengths` with one ballot; it needs
+// planes % 8 == 0 and B <= 64, otherwise planes keep their natural order.
+struct Sched {
+  int plane, wgp;
+};
+
+__device__ __forceinline__ Sched schedule(const uint32_t* lengths, int B, int S, int KV, int wpp) {
+  constexpr int kXcds = 8;
+  const int planes = B * KV;
+  const int bid = static_cast<int>(blockIdx.x);
+  Sched sc;
+  if (planes % kXcds == 0 && B <= 64) {
+    const int x = bid % kXcds, li = bid / kXcds;
+    const int j = (li / wpp) * kXcds + x;  // plane rank, longest row first
+    sc.wgp = wpp - 1 - li % wpp;
+    const int jrow = j / KV, kvh = j % KV;
+    const int lane = threadIdx.x & 63;
+    const uint32_t mine = lane < B ? min(lengths[lane], static_cast<uint32_t>(S)) : 0u;
+    int rank = 0;
+    for (int other = 0; other < B; ++other) {
+      const uint32_t lo = min(lengths[other], static_cast<uint32_t>(S));
+      rank += (lo > mine) || (lo == mine && other < lane);
+    }
+    const unsigned long long hit = __ballot(lane < B && rank == jrow);
+    const int b = __ffsll(hit) - 1;
+    sc.plane = b * KV + kvh;
+  } else {
+    sc.plane = bid / wpp;
+    sc.wgp = wpp - 1 - bid % wpp;
+  }
+  return sc;
+}
+
 struct Geom {
   int b, kvh, head, p0, L, wave_end, wg_end, limit_min;
   bool active;
@@ -99,11 +135,10 @@ __device__ __forceinline__ Geom make_geom(const uint32_t* lengths, int B, int S,
   const int G = H / KV;
   const int nrb = G * ((S + 31) / 32);
   const int wpp = (nrb + 3) / 4;
-  const int planes = B * KV;
-  const int plane = blockIdx.x % planes;
-  const int wgp = wpp - 1 - static_cast<int>(blockIdx.x / planes);
-  g.b = plane / KV;
-  g.kvh = plane % KV;
+  const Sched sc = schedule(lengths, B, S, KV, wpp);
+  const int wgp = sc.wgp;
+  g.b = sc.plane / KV;
+  g.kvh = sc.plane % KV;
   const int rb = wgp * 4 + wave;
   g.active = rb < nrb;
   g.head = g.kvh * G + rb % G;
@@ -273,116 +308,250 @@ __global__ __launch_bounds__(256, 2) void attn_f32_mfma(const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------------------------
-// fp16 MFMA kernel. v_mfma_f32_32x32x16_f16: lane l supplies A[l%32][8(l/32)..+7] and
-// B[8(l/32)..+7][l%32] (8 halves each); D as in the fp32 kernel.
-//   S^T = K * Q^T: 32-key sub-tiles, k-step s covers channels 16s..16s+15.
-//   The K tile is written into LDS with rows permuted by pi (swap of key-index bits 2 and 3), so
-//   accumulator element e = 4a+c of lane half h holds key 16(a>>1) + 8h + 4(a&1) + c. For PV
-//   k-step t the lane's own elements 8t..8t+7 are then the 8 CONSECUTIVE keys 16t+8h..16t+8h+7,
-//   matching a single 16-byte read of the transposed V tile (V^T: [channel][key] in LDS).
-// One softmax update per key tile of KT keys; l accumulates the fp16-rounded probabilities that PV
-// actually uses, so the output is an exact weighted mean of V rows.
+// fp16 MFMA kernel, 16 query rows per wavefront. v_mfma_f32_16x16x32_f16: lane l (r = l%16,
+// g = l/16) supplies A[r][8g..8g+7] and B[8g..8g+7][r] (8 halves each) and holds
+// D[4g+j][r] in acc[j].
+//   S^T = K * Q^T per 16-key block, k-step s covers channels 32s..32s+31: lane (r, g) owns the
+//   scores of query r for keys 4g+j of each block; the row max / sum of a query reduces over the
+//   four lanes r, r+16, r+32, r+48.
+//   The 32-key tile is stored in LDS with key p at row R(p) = 16*((p>>2)&1) + 4*(p>>3) + (p&3),
+//   so the lane's eight probabilities (two blocks x four) are the CONSECUTIVE keys 8g..8g+7 and
+//   form the B operand of O^T = V^T * P^T directly; its A operand is one 16-byte read of the
+//   transposed V tile (V^T: [channel][key] in LDS).
+//   O^T accumulates per 16-channel block: lane (r, g) holds channels 16*dt + 4g + j of query r.
+// Small register footprint (~100 VGPRs at D=128) keeps four wavefronts per SIMD resident, so
+// the streaming of Q in and O out overlaps other wavefronts' MFMA and softmax work.
 //
 // FUSED (route attention_f16_norm_rope): Q arrives pre-norm and is RMS-normalized and rotated in
 // fp32 as it is loaded; K arrives already normalized and rotated as two fp16 planes hi + lo
 // (written by norm_rope_f16). Q is also carried as hi + lo, and the score tile accumulates
 // K_hi*Q_lo + K_lo*Q_hi + K_hi*Q_hi in fp32, so the normalized q and k enter the dot products at
 // ~22-bit precision instead of fp16's 11 bits.
-//
-// All global loads are branch-free: out-of-range rows load a clamped in-bounds address and are
-// replaced by zero, so the compiler can issue every load of a phase back to back.
+// All global loads are branch-free: out-of-range rows read a clamped in-bounds address and are
+// replaced by zero, so every load of a phase issues back to back.
 // ---------------------------------------------------------------------------------------------
-template <int D, int KT>
-struct F16Tile {
-  static constexpr int KROW = D + 8;            // halves; 16-byte pad puts rows 4 banks apart
-  static constexpr int VROW = KT + 8;           // halves per V^T row (channel)
-  static constexpr int KCH = KT * D / 8;        // 16-byte K chunks per tile
-  static constexpr int KCPT = (KCH + 255) / 256;
-  static constexpr int VIT = (KT / 2) * (D / 8);  // (key pair, channel chunk) items per tile
-  static constexpr int VIPT = (VIT + 255) / 256;
-  static constexpr int NS = D / 16;             // k-steps per score tile
-  static constexpr int NU = KT / 32;            // 32-key sub-tiles per tile
+typedef _Float16 half8x __attribute__((ext_vector_type(8)));
+
+struct Geom16 {
+  int b, kvh, head, p0, L, wave_end, wg_end, limit_min;
+  bool active;
 };
 
-__device__ __forceinline__ int pi_row(int key) {
-  return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
+// grid = planes * wgs_per_plane; a workgroup holds four row-blocks of 16 queries of one
+// (batch row, kv head) plane, row-block rb = pos_block * G + head_in_group, order from
+// schedule().
+__device__ __forceinline__ Geom16 make_geom16(const uint32_t* lengths, int B, int S, int H, int KV,
+                                              int bidi, int wave) {
+  Geom16 g;
+  const int G = H / KV;
+  const int nrb = G * ((S + 15) / 16);
+  const int wpp = (nrb + 3) / 4;
+  const Sched sc = schedule(lengths, B, S, KV, wpp);
+  const int wgp = sc.wgp;
+  g.b = sc.plane / KV;
+  g.kvh = sc.plane % KV;
+  const int rb = wgp * 4 + wave;
+  g.active = rb < nrb;
+  g.head = g.kvh * G + rb % G;
+  g.p0 = (rb / G) * 16;
+  g.L = static_cast<int>(min(lengths[g.b], static_cast<uint32_t>(S)));
+  const int rb_last = min(wgp * 4 + 3, nrb - 1);
+  if (bidi) {
+    g.wave_end = g.active ? g.L : 0;
+    g.wg_end = g.L;
+    g.limit_min = g.L;
+  } else {
+    g.wave_end = g.active ? min(g.p0 + 16, g.L) : 0;
+    g.wg_end = min((rb_last / G) * 16 + 16, g.L);
+    g.limit_min = min(g.p0 + 1, g.L);
+  }
+  return g;
 }
 
-template <int D, typename TOut, bool FUSED, int KT>
+__device__ __forceinline__ int tile_row(int p) {  // LDS row of key p in a 32-key tile
+  return ((p & 4) << 2) | ((p & 24) >> 1) | (p & 3);
+}
+
+__device__ __forceinline__ int tile_key(int row) {  // inverse of tile_row
+  return ((row & 12) << 1) | ((row & 16) >> 2) | (row & 3);
+}
+
+typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 8 bytes of a row-major V tile, transposed across each 16-lane group (ds_read_b64_tr_b16):
+// result lane i, element j = element (i % 4) of the 4 halves addressed by lane 4j + i/4.
+__device__ __forceinline__ half4 lds_read_tr(const _Float16* p) {
+  const fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+      (__attribute__((address_space(3))) fp16x4_t*)(p));
+  return __builtin_bit_cast(half4, v);
+}
+
+// 16 bytes per lane, global -> LDS (global_load_lds_dwordx4): lane l's bytes land at the
+// wave-uniform LDS address + 16*l. Issued as inline asm so the compiler's wait insertion does not
+// treat the in-flight DMA as aliasing every later LDS read (it would wait for the whole ring);
+// completion is awaited explicitly with wait_vmcnt before the consuming barrier.
+__device__ __forceinline__ void dma16(const void* src, _Float16* lds) {
+  const unsigned addr = __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_ptr_t)(lds))));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(addr)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(n), leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Cross-row reductions with gfx950's VALU lane swaps: permlane16_swap(x, x) yields
+// (x[l & ~16], x[l | 16]) and permlane32_swap the same for lane bit 5, so both lanes of a pair
+// get op(pair) without going through the LDS crossbar.
+__device__ __forceinline__ float pair16(float x, bool take_max) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float a = __uint_as_float(p[0]), b = __uint_as_float(p[1]);
+  return take_max ? fmaxf(a, b) : a + b;
+}
+__device__ __forceinline__ float pair32(float x, bool take_max) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float a = __uint_as_float(p[0]), b = __uint_as_float(p[1]);
+  return take_max ? fmaxf(a, b) : a + b;
+}
+// reduce over the four lanes r, r+16, r+32, r+48 that hold one query's scores
+__device__ __forceinline__ float rowmax4(float x) { return pair32(pair16(x, true), true); }
+__device__ __forceinline__ float rowsum4(float x) { return pair32(pair16(x, false), false); }
+
+// Workgroup barrier without a memory fence. Each wavefront has already waited (vmcnt) for its
+// own DMA writes into the stage it is about to release, so after s_barrier every wavefront's
+// tile data is in LDS; the asm clobbers keep the compiler from moving LDS accesses across.
+// (__syncthreads() would add a release fence that waits for ALL outstanding DMA, including the
+// tiles still being prefetched.)
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Shared-memory stages of the K/V ring: [K plane 0][K plane 1 (fused)][V], each KT x D halves,
+// laid out in 1 KiB blocks exactly as the DMA writes them.
+template <int D, bool FUSED>
+struct F16Stage {
+  static constexpr int KT = 32;
+  static constexpr int TILE = KT * D;  // halves per plane tile
+  static constexpr int KPL = FUSED ? 2 : 1;
+  _Float16 k[KPL][TILE];
+  _Float16 v[TILE];
+};
+
+// ---------------------------------------------------------------------------------------------
+// fp16 MFMA kernel (v_mfma_f32_16x16x32_f16), 16 query rows per wavefront, four wavefronts per
+// workgroup sharing one (batch row, kv head) plane.
+//
+// Lane (r = l%16, g = l/16) supplies A[r][8g..8g+7], B[8g..8g+7][r] and holds D[4g+j][r].
+//   S^T = K * Q^T per 16-key block; k-step s covers channels 32s..32s+31. Lane (r, g) owns the
+//   scores of query r for keys 4g+j of each block; row max / sum reduce over lanes r+16i.
+//   In the K tile, key p sits at row tile_row(p) = 16*((p>>2)&1) + 4*(p>>3) + (p&3), so a lane's
+//   eight probabilities (two blocks x four) are the consecutive keys 8g..8g+7: the B operand of
+//   O^T = V^T * P^T. Its A operand V[8g..8g+7][16dt + r] comes from the row-major V tile with two
+//   ds_read_b64_tr_b16, each lane addressing 4 channels of one key row.
+//
+// K/V tiles of 32 keys stream through a 3-stage LDS ring filled by global_load_lds_dwordx4,
+// issued two tiles ahead of use, one barrier per tile. The DMA writes each 1 KiB block
+// contiguously; which global chunk a lane fetches sets the layout: K rows XOR-swizzle their
+// 16-byte chunks by (row & 7) and V rows by 2*(row & 3), so the MFMA operand reads are free of
+// bank conflicts. Key rows at or beyond L are fetched from key 0 (finite data) and masked.
+//
+// FUSED (route attention_f16_norm_rope): Q arrives pre-norm and is RMS-normalized and rotated in
+// fp32 as it is loaded; K arrives normalized and rotated as two fp16 planes hi + lo (written by
+// norm_rope_f16). Q is also carried as hi + lo, and the scores accumulate
+// K_hi*Q_lo + K_lo*Q_hi + K_hi*Q_hi in fp32: q and k enter the dot products at ~22 bits.
+// ---------------------------------------------------------------------------------------------
+template <int D, typename TOut, bool FUSED>
 __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
     const _Float16* __restrict__ q, const _Float16* __restrict__ k, const _Float16* __restrict__ v,
     const uint32_t* __restrict__ lengths, TOut* __restrict__ out, int B, int S, int H, int KV,
     float scale_log2, int bidi, const uint16_t* __restrict__ gamma,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, float eps,
     size_t k_plane) {
-  using T = F16Tile<D, KT>;
-  constexpr int NS = T::NS, NU = T::NU, KROW = T::KROW, VROW = T::VROW;
-  constexpr int KPLANES = FUSED ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) _Float16 Ks[KPLANES][KT * KROW];
-  __shared__ __attribute__((aligned(16))) _Float16 Vt[D * VROW];
+  using Stage = F16Stage<D, FUSED>;
+  constexpr int KT = Stage::KT, KPL = Stage::KPL;
+  constexpr int NS = D / 32;               // k-steps per 16x16 score block
+  constexpr int NDT = D / 16;              // 16-channel output blocks
+  constexpr int ROWH = D;                  // halves per tile row
+  constexpr int CPR = D / 8;               // 16-byte chunks per row
+  constexpr int RPB = 1024 / (2 * D);      // rows per 1 KiB DMA block
+  constexpr int BPW = (KT / RPB) / 4;      // DMA blocks per wavefront per plane tile
+  constexpr int LPT = BPW * (KPL + 1);     // DMA instructions per wavefront per tile
+  static_assert(D == 64 || D == 128, "pipelined fp16 kernel serves D = 64 or 128");
+  __shared__ __attribute__((aligned(1024))) Stage st0, st1, st2;
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  const Geom g = make_geom(lengths, B, S, H, KV, bidi, wave);
-  const int qpos = g.p0 + l32;
+  const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, gq = lane >> 4;
+  // the wavefront index is uniform; readfirstlane lets the compiler branch on it with scalars
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const Geom16 g = make_geom16(lengths, B, S, H, KV, bidi, wave);
+  const int qpos = g.p0 + r;
   const bool qvalid = g.active && qpos < S;
   const int qpos_c = min(qpos, S - 1);
   const int limit = bidi ? g.L : min(qpos + 1, g.L);
   const int ntiles = (g.wg_end + KT - 1) / KT;
-  const size_t kv_base = static_cast<size_t>(g.b) * S * KV + g.kvh;
+  const _Float16* kbase = k + (static_cast<size_t>(g.b) * S * KV + g.kvh) * D;
+  const _Float16* vbase = v + (static_cast<size_t>(g.b) * S * KV + g.kvh) * D;
+  const size_t krow = static_cast<size_t>(KV) * D;
 
-  // ---- tile prefetch registers (branch-free, clamped rows, zero outside [0, L)) -------------
-  half8 kreg[KPLANES][T::KCPT], vreg[T::VIPT][2];
-  auto load_tile = [&](int kt) {
+  // ---- Q fragment: lane (r, g) holds channels 32s + 8g .. +7 of query r ---------------------
+  const size_t qbase = ((static_cast<size_t>(g.b) * S + qpos_c) * H + g.head) * D + 8 * gq;
+  half8 qh[NS], ql[FUSED ? NS : 1];
 #pragma unroll
-    for (int i = 0; i < T::KCPT; ++i) {
-      const int c = min(tid + 256 * i, T::KCH - 1);
-      const int key = c / (D / 8), ck = c % (D / 8);
-      const int kg = kt * KT + key;
-      const bool ok = kg < g.L;
-      const size_t off = (kv_base + static_cast<size_t>(ok ? kg : 0) * KV) * D + 8 * ck;
+  for (int s = 0; s < NS; ++s) qh[s] = *reinterpret_cast<const half8*>(q + qbase + 32 * s);
+
+  // ---- DMA of one K/V tile into a stage (each lane one 16-byte chunk per block) -------------
+  auto issue = [&](Stage& stg, int kt) {
 #pragma unroll
-      for (int pl = 0; pl < KPLANES; ++pl) {
-        const half8 t = *reinterpret_cast<const half8*>(k + pl * k_plane + off);
-        kreg[pl][i] = ok ? t : half8{};
+    for (int j = 0; j < BPW; ++j) {
+      const int blk = wave * BPW + j;
+      const int row = blk * RPB + lane / CPR;
+      const int pos = lane % CPR;
+      {
+        const int key = tile_key(row);
+        const int kg = kt * KT + key;
+        const size_t off = static_cast<size_t>(kg < g.L ? kg : 0) * krow + 8 * (pos ^ (row & 7));
+#pragma unroll
+        for (int pl = 0; pl < KPL; ++pl) dma16(kbase + pl * k_plane + off, &stg.k[pl][blk * 512]);
       }
-    }
-#pragma unroll
-    for (int i = 0; i < T::VIPT; ++i) {
-      const int c = min(tid + 256 * i, T::VIT - 1);
-      const int kp = c % (KT / 2), ck = c / (KT / 2);
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int kg = kt * KT + 2 * kp + r;
-        const bool ok = kg < g.L;
-        const half8 t = *reinterpret_cast<const half8*>(
-            v + (kv_base + static_cast<size_t>(ok ? kg : 0) * KV) * D + 8 * ck);
-        vreg[i][r] = ok ? t : half8{};
+      {
+        const int kg = kt * KT + row;
+        const size_t off =
+            static_cast<size_t>(kg < g.L ? kg : 0) * krow + 8 * (pos ^ (2 * (row & 3)));
+        dma16(vbase + off, &stg.v[blk * 512]);
       }
     }
   };
-
-  // ---- Q fragment: lane holds channels 16s + 8h .. +7 of its query row -----------------------
-  const size_t qbase = ((static_cast<size_t>(g.b) * S + qpos_c) * H + g.head) * D + 8 * hh;
-  half8 qh[NS], ql[FUSED ? NS : 1];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) qh[s] = *reinterpret_cast<const half8*>(q + qbase + 16 * s);
-  if (ntiles > 0) load_tile(0);  // overlaps the Q normalization below
+  // register loads first, then the tile DMAs: waiting for the former never waits for the latter
+  uint4v gw[FUSED ? NS : 1];
+  floatx4 cs[FUSED ? NS / 2 : 1][2], sn[FUSED ? NS / 2 : 1][2];
   if constexpr (FUSED) {
-    // Per-head RMSNorm (x * rsqrt(mean(x^2) + eps) * gamma) then split-half RoPE, fp32 math:
-    // the composition of kernels.metal:53-63 and :65-74 applied to one query row.
-    uint4v gw[NS];
-    floatx4 cs[NS / 2][2], sn[NS / 2][2];
-    const float* ct = rope_cos + static_cast<size_t>(qpos_c) * (D / 2) + 8 * hh;
-    const float* st = rope_sin + static_cast<size_t>(qpos_c) * (D / 2) + 8 * hh;
+    const float* ct = rope_cos + static_cast<size_t>(qpos_c) * (D / 2) + 8 * gq;
+    const float* stt = rope_sin + static_cast<size_t>(qpos_c) * (D / 2) + 8 * gq;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) gw[s] = *reinterpret_cast<const uint4v*>(gamma + 16 * s + 8 * hh);
+    for (int s = 0; s < NS; ++s) gw[s] = *reinterpret_cast<const uint4v*>(gamma + 32 * s + 8 * gq);
 #pragma unroll
     for (int s = 0; s < NS / 2; ++s) {
-      cs[s][0] = *reinterpret_cast<const floatx4*>(ct + 16 * s);
-      cs[s][1] = *reinterpret_cast<const floatx4*>(ct + 16 * s + 4);
-      sn[s][0] = *reinterpret_cast<const floatx4*>(st + 16 * s);
-      sn[s][1] = *reinterpret_cast<const floatx4*>(st + 16 * s + 4);
+      cs[s][0] = *reinterpret_cast<const floatx4*>(ct + 32 * s);
+      cs[s][1] = *reinterpret_cast<const floatx4*>(ct + 32 * s + 4);
+      sn[s][0] = *reinterpret_cast<const floatx4*>(stt + 32 * s);
+      sn[s][1] = *reinterpret_cast<const floatx4*>(stt + 32 * s + 4);
     }
+  }
+  // Tile 0 unconditionally (rows past L clamp to key 0 of this batch row: always in bounds).
+  issue(st0, 0);
+  if (ntiles > 1) issue(st1, 1);
+
+  if constexpr (FUSED) {
+    // RMSNorm over the row (four lanes) then split-half RoPE: channel c < D/2 of step s pairs
+    // with channel c + D/2 of step s + NS/2 in the same lane (kernels.metal:53-63, :65-74).
     float x[NS][8];
     float ss = 0.0f;
 #pragma unroll
@@ -392,7 +561,7 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
         x[s][m] = static_cast<float>(qh[s][m]);
         ss += x[s][m] * x[s][m];
       }
-    ss += __shfl_xor(ss, 32);
+    ss = rowsum4(ss);
     const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
 #pragma unroll
     for (int s = 0; s < NS; ++s)
@@ -428,135 +597,116 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
     }
   }
 
-  floatx16 o[D / 32];
+  floatx4 o[NDT];
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
+  for (int dt = 0; dt < NDT; ++dt) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.0f;
 
-  for (int kt = 0; kt < ntiles; ++kt) {
-    __syncthreads();
+  // ---- one tile: wait for its DMA, release the oldest stage, compute --------------------------
+  auto step = [&](Stage& cur, Stage& next2, int kt) {
+    // in flight: this tile, then the next one (issued one step earlier or in the prologue)
+    if (kt + 1 < ntiles) wait_vmcnt<LPT>();
+    else wait_vmcnt<0>();
+    stage_barrier();
+    if (kt + 2 < ntiles) issue(next2, kt + 2);
+    if (kt * KT >= g.wave_end) return;
+    floatx4 sc[2];
 #pragma unroll
-    for (int i = 0; i < T::KCPT; ++i) {
-      const int c = tid + 256 * i;
-      if (c < T::KCH) {
-        const int key = c / (D / 8), ck = c % (D / 8);
-        const int row = (key & ~31) | pi_row(key & 31);
-#pragma unroll
-        for (int pl = 0; pl < KPLANES; ++pl)
-          *reinterpret_cast<half8*>(&Ks[pl][row * KROW + 8 * ck]) = kreg[pl][i];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < T::VIPT; ++i) {
-      const int c = tid + 256 * i;
-      if (c < T::VIT) {
-        const int kp = c % (KT / 2), ck = c / (KT / 2);
-#pragma unroll
-        for (int m = 0; m < 8; ++m) {
-          half2v pr = {vreg[i][0][m], vreg[i][1][m]};
-          *reinterpret_cast<half2v*>(&Vt[(8 * ck + m) * VROW + 2 * kp]) = pr;
-        }
-      }
-    }
-    __syncthreads();
-    if (kt + 1 < ntiles) load_tile(kt + 1);
-    if (kt * KT < g.wave_end) {
-      floatx16 sc[NU];
-#pragma unroll
-      for (int u = 0; u < NU; ++u) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sc[u][e] = 0.0f;
-        const int row = (32 * u + l32) * KROW + 8 * hh;
-        if constexpr (FUSED) {
-#pragma unroll
-          for (int s = 0; s < NS; ++s) {
-            const half8 ahi = *reinterpret_cast<const half8*>(&Ks[0][row + 16 * s]);
-            const half8 alo = *reinterpret_cast<const half8*>(&Ks[1][row + 16 * s]);
-            sc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi, ql[s], sc[u], 0, 0, 0);
-            sc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo, qh[s], sc[u], 0, 0, 0);
-          }
-        }
+    for (int blk = 0; blk < 2; ++blk) {
+      sc[blk] = floatx4{0.f, 0.f, 0.f, 0.f};
+      const int row = 16 * blk + r;
+      const int rbase = row * ROWH, sw = row & 7;
+      if constexpr (FUSED) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-          const half8 a = *reinterpret_cast<const half8*>(&Ks[0][row + 16 * s]);
-          sc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qh[s], sc[u], 0, 0, 0);
+          const int off = rbase + 8 * ((4 * s + gq) ^ sw);
+          const half8 ahi = *reinterpret_cast<const half8*>(&cur.k[0][off]);
+          const half8 alo = *reinterpret_cast<const half8*>(&cur.k[1][off]);
+          sc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, ql[s], sc[blk], 0, 0, 0);
+          sc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, qh[s], sc[blk], 0, 0, 0);
         }
       }
-      // masks only where the tile crosses some row's key limit
-      if (kt * KT + KT > g.limit_min) {
 #pragma unroll
-        for (int u = 0; u < NU; ++u)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int a = e >> 2, c = e & 3;
-            const int key = kt * KT + 32 * u + 16 * (a >> 1) + 8 * hh + 4 * (a & 1) + c;
-            if (key >= limit) sc[u][e] = -INFINITY;
-          }
+      for (int s = 0; s < NS; ++s) {
+        const half8 a =
+            *reinterpret_cast<const half8*>(&cur.k[0][rbase + 8 * ((4 * s + gq) ^ sw)]);
+        sc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[s], sc[blk], 0, 0, 0);
       }
-      float mloc = -INFINITY;
-#pragma unroll
-      for (int u = 0; u < NU; ++u)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, sc[u][e]);
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32)) * scale_log2;
-      const float m_new = fmaxf(m_run, mloc);
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
-      half8 pb[NU][2];
-      float lsum = 0.0f;
-#pragma unroll
-      for (int u = 0; u < NU; ++u)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const _Float16 ph =
-              static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(sc[u][e], scale_log2, -m_use)));
-          pb[u][e >> 3][e & 7] = ph;
-          lsum += static_cast<float>(ph);
-        }
-      lsum += __shfl_xor(lsum, 32);
-      l_run = l_run * corr + lsum;
-      m_run = m_new;
-      if (__any(corr != 1.0f)) {
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) o[dt][e] *= corr;
-      }
-#pragma unroll
-      for (int u = 0; u < NU; ++u)
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int dt = 0; dt < D / 32; ++dt) {
-            const half8 a =
-                *reinterpret_cast<const half8*>(&Vt[(32 * dt + l32) * VROW + 32 * u + 16 * t + 8 * hh]);
-            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[u][t], o[dt], 0, 0, 0);
-          }
     }
+    // element (blk, j) is key 8g + 4blk + j of this tile
+    if (kt * KT + KT > g.limit_min) {
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (kt * KT + 8 * gq + 4 * blk + j >= limit) sc[blk][j] = -INFINITY;
+    }
+    float mloc = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                       fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+    mloc = rowmax4(mloc) * scale_log2;
+    const float m_new = fmaxf(m_run, mloc);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+    half8 pb;
+    float lsum = 0.0f;
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const _Float16 ph =
+            static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(sc[blk][j], scale_log2, -m_use)));
+        pb[4 * blk + j] = ph;
+        lsum += static_cast<float>(ph);
+      }
+    // l_run holds this lane's share of the row sum (its own keys); the four shares of a query
+    // are combined once, after the last tile
+    l_run = l_run * corr + lsum;
+    m_run = m_new;
+    if (__any(corr != 1.0f)) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
+    }
+    // V rows 8g + 4h + r/4, channels 16dt + 4(r%4) .. +3, chunk swizzled by 2*(row & 3)
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      half8 a;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int vrow = 8 * gq + 4 * h + (r >> 2);
+        const int chunk = (2 * dt + ((r & 3) >> 1)) ^ (2 * (vrow & 3));
+        const half4 t = lds_read_tr(&cur.v[vrow * ROWH + 8 * chunk + 4 * (r & 1)]);
+        a[4 * h + 0] = t[0];
+        a[4 * h + 1] = t[1];
+        a[4 * h + 2] = t[2];
+        a[4 * h + 3] = t[3];
+      }
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, o[dt], 0, 0, 0);
+    }
+  };
+
+  for (int kt = 0; kt < ntiles; kt += 3) {
+    step(st0, st2, kt);
+    if (kt + 1 < ntiles) step(st1, st0, kt + 1);
+    if (kt + 2 < ntiles) step(st2, st1, kt + 2);
   }
+  // No DMA may still be writing this workgroup's LDS when its wavefronts end.
+  wait_vmcnt<0>();
+  const float l_row = rowsum4(l_run);
 
   if (qvalid) {
-    const float inv = 1.0f / l_run;
-    const size_t base = ((static_cast<size_t>(g.b) * S + qpos) * H + g.head) * D;
+    const float inv = 1.0f / l_row;
+    const size_t base = ((static_cast<size_t>(g.b) * S + qpos) * H + g.head) * D + 4 * gq;
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        TOut* dst = out + base + 32 * dt + 8 * a + 4 * hh;
-        if constexpr (sizeof(TOut) == 2) {
-          half4 r = {static_cast<_Float16>(o[dt][4 * a] * inv),
-                     static_cast<_Float16>(o[dt][4 * a + 1] * inv),
-                     static_cast<_Float16>(o[dt][4 * a + 2] * inv),
-                     static_cast<_Float16>(o[dt][4 * a + 3] * inv)};
-          *reinterpret_cast<half4*>(dst) = r;
-        } else {
-          floatx4 r = {o[dt][4 * a] * inv, o[dt][4 * a + 1] * inv, o[dt][4 * a + 2] * inv,
-                       o[dt][4 * a + 3] * inv};
-          *reinterpret_cast<floatx4*>(dst) = r;
-        }
+    for (int dt = 0; dt < NDT; ++dt) {
+      TOut* dst = out + base + 16 * dt;
+      if constexpr (sizeof(TOut) == 2) {
+        half4 rv = {static_cast<_Float16>(o[dt][0] * inv), static_cast<_Float16>(o[dt][1] * inv),
+                    static_cast<_Float16>(o[dt][2] * inv), static_cast<_Float16>(o[dt][3] * inv)};
+        *reinterpret_cast<half4*>(dst) = rv;
+      } else {
+        *reinterpret_cast<floatx4*>(dst) = o[dt] * inv;
       }
+    }
   }
 }
 
@@ -616,36 +766,39 @@ hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int D, bool FUSED, int KT>
+static unsigned mfma16_grid(int B, int S, int H, int KV) {
+  const int G = H / KV;
+  const int nrb = G * ((S + 15) / 16);
+  return static_cast<unsigned>(B * KV * ((nrb + 3) / 4));
+}
+
+template <int D, bool FUSED>
 static void launch_f16_d(const AttnArgs& a, unsigned grid, float sl2, hipStream_t st) {
   auto q = static_cast<const _Float16*>(a.q), k = static_cast<const _Float16*>(a.k),
        v = static_cast<const _Float16*>(a.v);
   const size_t plane = static_cast<size_t>(a.B) * a.S * a.KV * a.D;
   if (a.out_f16)
-    attn_f16_mfma<D, _Float16, FUSED, KT><<<grid, 256, 0, st>>>(
+    attn_f16_mfma<D, _Float16, FUSED><<<grid, 256, 0, st>>>(
         q, k, v, a.lengths, static_cast<_Float16*>(a.out), a.B, a.S, a.H, a.KV, sl2, a.bidi,
         a.gamma_q, a.rope_cos, a.rope_sin, a.eps, plane);
   else
-    attn_f16_mfma<D, float, FUSED, KT><<<grid, 256, 0, st>>>(
+    attn_f16_mfma<D, float, FUSED><<<grid, 256, 0, st>>>(
         q, k, v, a.lengths, static_cast<float*>(a.out), a.B, a.S, a.H, a.KV, sl2, a.bidi,
         a.gamma_q, a.rope_cos, a.rope_sin, a.eps, plane);
 }
 
 hipError_t launch_attention_f16(const AttnArgs& a, hipStream_t st) {
-  const unsigned grid = mfma_grid(a.B, a.S, a.H, a.KV);
+  const unsigned grid = mfma16_grid(a.B, a.S, a.H, a.KV);
   if (!grid) return hipSuccess;
   const float sl2 = a.scale * kLog2e;
   const bool fused = a.gamma_q != nullptr;
   if (fused && (!a.rope_cos || !a.rope_sin)) return hipErrorInvalidValue;
   switch (a.D) {
-    case 32:
-      fused ? launch_f16_d<32, true, 64>(a, grid, sl2, st) : launch_f16_d<32, false, 64>(a, grid, sl2, st);
-      break;
     case 64:
-      fused ? launch_f16_d<64, true, 64>(a, grid, sl2, st) : launch_f16_d<64, false, 64>(a, grid, sl2, st);
+      fused ? launch_f16_d<64, true>(a, grid, sl2, st) : launch_f16_d<64, false>(a, grid, sl2, st);
       break;
     case 128:
-      fused ? launch_f16_d<128, true, 32>(a, grid, sl2, st) : launch_f16_d<128, false, 64>(a, grid, sl2, st);
+      fused ? launch_f16_d<128, true>(a, grid, sl2, st) : launch_f16_d<128, false>(a, grid, sl2, st);
       break;
     default:
       return hipErrorInvalidValue;

@@ -58,12 +58,23 @@ __global__ __launch_bounds__(256) void linear4_f32(const float* __restrict__ x,
 #pragma unroll
       for (int t = 0; t < 32; ++t) wv[t] = 0.0f;
     }
+    // Two independent 32-product partial sums per group, added to the total: the K32 partial
+    // accumulation of tessery's tiled kernels (kernels.metal:500-518), which bounds the rounding
+    // growth over long K.
 #pragma unroll
-    for (int c4 = 0; c4 < 8; ++c4) {
-      const floatx4 xa = *reinterpret_cast<const floatx4*>(&xs[l32 * XROW + 32 * hh + 4 * c4]);
+    for (int half = 0; half < 2; ++half) {
+      floatx16 part;
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[t], wv[4 * c4 + t], acc, 0, 0, 0);
+      for (int e = 0; e < 16; ++e) part[e] = 0.0f;
+#pragma unroll
+      for (int c4 = 4 * half; c4 < 4 * half + 4; ++c4) {
+        const floatx4 xa = *reinterpret_cast<const floatx4*>(&xs[l32 * XROW + 32 * hh + 4 * c4]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          part = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[t], wv[4 * c4 + t], part, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] += part[e];
     }
   }
   if (!nvalid) return;

@@ -178,7 +178,7 @@ bool attn_shape(Route r, const Params& p, uint64_t threads, uint32_t group, Attn
     }
     case R_ATTENTION_F16:
     case R_ATTENTION_F16_NORM_ROPE:
-      if (group != 256 || (D != 32 && D != 64 && D != 128)) return false;
+      if (group != 256 || (D != 64 && D != 128)) return false;
       tokens = threads;
       s->in_f16 = 1;
       s->out_f16 = p.u1 & 1u;

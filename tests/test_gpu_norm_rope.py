@@ -75,7 +75,8 @@ def test_norm_rope_f16_prologue(runtime, dim):
     for b, length in enumerate(lengths):
         exp = expected[b, :length]
         assert np.all(np.abs(got[0, b, :length] - exp) <= 2.0**-11 * np.abs(exp) + 1e-7)
-        assert np.all(np.abs(got[0, b, :length] + got[1, b, :length] - exp) <= 2e-6 * np.abs(exp) + 1e-7)
+        # fp32 math: absolute error at the scale of the row (RoPE sums can cancel)
+        assert np.all(np.abs(got[0, b, :length] + got[1, b, :length] - exp) <= 2e-6 * (np.abs(exp) + 1))
         assert np.isnan(got[:, b, length:]).all()  # padded rows are never written
 
 

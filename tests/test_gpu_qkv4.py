@@ -1,0 +1,48 @@
+"""Fused uint4 QKV projection (fp16 activations) against the float64 oracle: every output within
+fp16 rounding of the exact projection (|err| <= 2^-11 |y| + 1e-4), for fp16 and bf16 scale words,
+rows that are not a multiple of the 128-row tile, and rows left untouched outside [0, M)."""
+
+import numpy as np
+import pytest
+
+from oracle import quant4 as ref
+from tessery_amd.workloads import bf16_words
+
+pytestmark = pytest.mark.gpu
+
+
+def weights(rng, n, k, kind):
+    codes = rng.integers(0, 16, size=(n, k), dtype=np.uint32)
+    if kind == "f16":
+        s = rng.normal(0, 0.02, size=(n, k // 64)).astype(np.float16).view(np.uint16)
+        b = rng.normal(0, 0.02, size=(n, k // 64)).astype(np.float16).view(np.uint16)
+    else:
+        s = bf16_words(rng.normal(0, 0.02, size=(n, k // 64)))
+        b = bf16_words(rng.normal(0, 0.02, size=(n, k // 64)))
+    return ref.pack(codes), s, b
+
+
+@pytest.mark.parametrize("kind", ["f16", "bf16"])
+@pytest.mark.parametrize("m,k,nq,nkv", [(300, 1024, 2048, 1024), (128, 256, 128, 128), (1, 64, 256, 128)])
+def test_qkv4_matches_f64(runtime, kind, m, k, nq, nkv):
+    rng = np.random.default_rng(5 + m)
+    x = rng.standard_normal((m, k), dtype=np.float32).astype(np.float16)
+    parts = [weights(rng, n, k, kind) for n in (nq, nkv, nkv)]
+    w = np.concatenate([p[0] for p in parts])
+    s = np.concatenate([p[1] for p in parts])
+    b = np.concatenate([p[2] for p in parts])
+    bufs = [runtime.upload(a) for a in (x, w, s, b)]
+    outs = [np.full((m + 1, n), np.nan, np.float16) for n in (nq, nkv, nkv)]
+    bufs += [runtime.upload(o) for o in outs]
+    try:
+        with runtime.command():
+            runtime._qkv4(bufs, rows=m, k=k, q_cols=nq, kv_cols=nkv, scale_dtype=kind)
+        got = [runtime.read(bufs[4 + i], outs[i].shape, np.float16) for i in range(3)]
+    finally:
+        for buf in bufs:
+            buf.close()
+    for (packed, sc, bi), y in zip(parts, got):
+        expected = ref.linear4(x, packed, sc, bi, kind)
+        err = np.abs(y[:m].astype(np.float64) - expected)
+        assert np.all(err <= 2.0**-11 * np.abs(expected) + 1e-4), float(err.max())
+        assert np.isnan(y[m:]).all()

@@ -29,7 +29,7 @@ def test_attention_route_table(case):
     assert kwargs["scale"] == dim**-0.5
 
 
-@pytest.mark.parametrize("dim,name,group", [(32, "attention_f16", 256), (64, "attention_f16", 256),
+@pytest.mark.parametrize("dim,name,group", [(32, "attention_f16_scalar", 64), (64, "attention_f16", 256),
                                             (128, "attention_f16", 256), (8, "attention_f16_scalar", 64),
                                             (96, "attention_f16_scalar", 64)])
 @pytest.mark.parametrize("out_dtype,flag", [(None, 0), ("f32", 0), ("f16", 1)])
