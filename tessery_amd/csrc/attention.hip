@@ -94,7 +94,7 @@ __global__ __launch_bounds__(64) void attn_scalar(const TIn* __restrict__ q,
 // The ranking is computed by every wavefront from `lengths` with one ballot; it needs
 // planes % 8 == 0 and B <= 64, otherwise planes keep their natural order.
 struct Sched {
-  int plane, wgp;
+  int plane, wgp, L;  // L: valid length of the plane's batch row, clamped to S
 };
 
 __device__ __forceinline__ Sched schedule(const uint32_t* lengths, int B, int S, int KV, int wpp) {
@@ -107,19 +107,23 @@ __device__ __forceinline__ Sched schedule(const uint32_t* lengths, int B, int S,
     const int j = (li / wpp) * kXcds + x;  // plane rank, longest row first
     sc.wgp = wpp - 1 - li % wpp;
     const int jrow = j / KV, kvh = j % KV;
+    // one vector load of the lengths; the ranking reads other lanes' values with v_readlane
+    // instead of a chain of dependent scalar loads
     const int lane = threadIdx.x & 63;
     const uint32_t mine = lane < B ? min(lengths[lane], static_cast<uint32_t>(S)) : 0u;
     int rank = 0;
     for (int other = 0; other < B; ++other) {
-      const uint32_t lo = min(lengths[other], static_cast<uint32_t>(S));
+      const uint32_t lo = __builtin_amdgcn_readlane(mine, other);
       rank += (lo > mine) || (lo == mine && other < lane);
     }
     const unsigned long long hit = __ballot(lane < B && rank == jrow);
     const int b = __ffsll(hit) - 1;
     sc.plane = b * KV + kvh;
+    sc.L = static_cast<int>(__builtin_amdgcn_readlane(mine, b));
   } else {
     sc.plane = bid / wpp;
     sc.wgp = wpp - 1 - bid % wpp;
+    sc.L = static_cast<int>(min(lengths[sc.plane / KV], static_cast<uint32_t>(S)));
   }
   return sc;
 }
@@ -143,7 +147,7 @@ __device__ __forceinline__ Geom make_geom(const uint32_t* lengths, int B, int S,
   g.active = rb < nrb;
   g.head = g.kvh * G + rb % G;
   g.p0 = (rb / G) * 32;
-  g.L = static_cast<int>(min(lengths[g.b], static_cast<uint32_t>(S)));
+  g.L = sc.L;
   const int rb_last = min(wgp * 4 + 3, nrb - 1);
   if (bidi) {
     g.wave_end = g.active ? g.L : 0;
@@ -354,7 +358,7 @@ __device__ __forceinline__ Geom16 make_geom16(const uint32_t* lengths, int B, in
   g.active = rb < nrb;
   g.head = g.kvh * G + rb % G;
   g.p0 = (rb / G) * 16;
-  g.L = static_cast<int>(min(lengths[g.b], static_cast<uint32_t>(S)));
+  g.L = sc.L;
   const int rb_last = min(wgp * 4 + 3, nrb - 1);
   if (bidi) {
     g.wave_end = g.active ? g.L : 0;
@@ -435,33 +439,43 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Shared-memory stages of the K/V ring: [K plane 0][K plane 1 (fused)][V], each KT x D halves,
-// laid out in 1 KiB blocks exactly as the DMA writes them.
+// K/V ring geometry. A tile holds KT = 2048 / D keys, so every plane tile (K hi, K lo when fused,
+// V) is 4 KiB: four 1 KiB DMA blocks, one per wavefront. D = 128 runs 16-key tiles, D = 64 runs
+// 32-key tiles. Three stages cost 36 KiB (fused) / 24 KiB (plain) of LDS per workgroup.
 template <int D, bool FUSED>
-struct F16Stage {
-  static constexpr int KT = 32;
-  static constexpr int TILE = KT * D;  // halves per plane tile
-  static constexpr int KPL = FUSED ? 2 : 1;
-  _Float16 k[KPL][TILE];
-  _Float16 v[TILE];
+struct F16Ring {
+  static constexpr int KT = 2048 / D;
+  static constexpr int KPL = FUSED ? 2 : 1;              // K planes (hi, lo)
+  static constexpr int TILE = KT * D;                    // halves per plane tile
+  static constexpr int STAGE = (KPL + 1) * TILE;         // halves per stage
+  static constexpr int NST = 3;                          // stages in the ring
+  static constexpr int RPB = 512 / D;                    // tile rows per 1 KiB block
+  static constexpr int CPR = D / 8;                      // 16-byte chunks per row
+  static constexpr int LPT = KPL + 1;                    // DMA instructions per wave per tile
 };
 
 // ---------------------------------------------------------------------------------------------
-// fp16 MFMA kernel (v_mfma_f32_16x16x32_f16), 16 query rows per wavefront, four wavefronts per
-// workgroup sharing one (batch row, kv head) plane.
+// fp16 MFMA kernel, 16 query rows per wavefront, four wavefronts per workgroup sharing one
+// (batch row, kv head) plane; fp32 accumulation throughout.
 //
-// Lane (r = l%16, g = l/16) supplies A[r][8g..8g+7], B[8g..8g+7][r] and holds D[4g+j][r].
-//   S^T = K * Q^T per 16-key block; k-step s covers channels 32s..32s+31. Lane (r, g) owns the
-//   scores of query r for keys 4g+j of each block; row max / sum reduce over lanes r+16i.
-//   In the K tile, key p sits at row tile_row(p) = 16*((p>>2)&1) + 4*(p>>3) + (p&3), so a lane's
-//   eight probabilities (two blocks x four) are the consecutive keys 8g..8g+7: the B operand of
-//   O^T = V^T * P^T. Its A operand V[8g..8g+7][16dt + r] comes from the row-major V tile with two
-//   ds_read_b64_tr_b16, each lane addressing 4 channels of one key row.
+// v_mfma_f32_16x16x32_f16: lane (r = l%16, g = l/16) supplies A[r][8g..8g+7], B[8g..8g+7][r] and
+// holds D[4g+j][r]; v_mfma_f32_16x16x16_f16 the same with four elements (A[r][4g..4g+3]).
+//   S^T = K * Q^T per 16-key block; k-step s covers channels 32s..32s+31, so lane (r, g) owns
+//   the scores of query r for keys 4g + j of the block and a query's row max / sum reduce over
+//   the four lanes r + 16i (two VALU lane swaps).
+//   D = 128 (KT = 16): the lane's four probabilities are keys 4g..4g+3, the B operand of
+//   O^T = V^T * P^T on 16x16x16; its A operand V[4g+j][16dt + r] is one ds_read_b64_tr_b16 of
+//   the row-major V tile.
+//   D = 64 (KT = 32): key p of the K tile sits at row tile_row(p), so the lane's eight
+//   probabilities (two blocks x four) are the consecutive keys 8g..8g+7, the B operand of
+//   16x16x32, with A from two ds_read_b64_tr_b16.
+//   O^T accumulates per 16-channel block: lane (r, g) holds channels 16dt + 4g + j of query r.
 //
-// K/V tiles of 32 keys stream through a 3-stage LDS ring filled by global_load_lds_dwordx4,
-// issued two tiles ahead of use, one barrier per tile. The DMA writes each 1 KiB block
-// contiguously; which global chunk a lane fetches sets the layout: K rows XOR-swizzle their
-// 16-byte chunks by (row & 7) and V rows by 2*(row & 3), so the MFMA operand reads are free of
+// K/V tiles stream through a three-stage LDS ring filled by global_load_lds_dwordx4, issued two
+// tiles ahead of use, with one barrier per tile; the stage is chosen at run time so the loop
+// body exists once. The DMA writes each 1 KiB block contiguously and the global chunk a lane
+// fetches sets the layout: K rows XOR-swizzle their 16-byte chunks by (row & 7), V rows by
+// 2 * (row & 7) (D = 128) or 2 * (row & 3) (D = 64), which keeps the MFMA operand reads free of
 // bank conflicts. Key rows at or beyond L are fetched from key 0 (finite data) and masked.
 //
 // FUSED (route attention_f16_norm_rope): Q arrives pre-norm and is RMS-normalized and rotated in
@@ -476,17 +490,12 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
     float scale_log2, int bidi, const uint16_t* __restrict__ gamma,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, float eps,
     size_t k_plane) {
-  using Stage = F16Stage<D, FUSED>;
-  constexpr int KT = Stage::KT, KPL = Stage::KPL;
-  constexpr int NS = D / 32;               // k-steps per 16x16 score block
-  constexpr int NDT = D / 16;              // 16-channel output blocks
-  constexpr int ROWH = D;                  // halves per tile row
-  constexpr int CPR = D / 8;               // 16-byte chunks per row
-  constexpr int RPB = 1024 / (2 * D);      // rows per 1 KiB DMA block
-  constexpr int BPW = (KT / RPB) / 4;      // DMA blocks per wavefront per plane tile
-  constexpr int LPT = BPW * (KPL + 1);     // DMA instructions per wavefront per tile
+  using R = F16Ring<D, FUSED>;
+  constexpr int KT = R::KT, KPL = R::KPL, NST = R::NST, RPB = R::RPB, CPR = R::CPR;
+  constexpr int NS = D / 32;   // k-steps per 16x16 score block
+  constexpr int NDT = D / 16;  // 16-channel output blocks
   static_assert(D == 64 || D == 128, "pipelined fp16 kernel serves D = 64 or 128");
-  __shared__ __attribute__((aligned(1024))) Stage st0, st1, st2;
+  __shared__ __attribute__((aligned(1024))) _Float16 ring[NST * R::STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, gq = lane >> 4;
   // the wavefront index is uniform; readfirstlane lets the compiler branch on it with scalars
@@ -501,35 +510,32 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
   const _Float16* vbase = v + (static_cast<size_t>(g.b) * S * KV + g.kvh) * D;
   const size_t krow = static_cast<size_t>(KV) * D;
 
+  // ---- DMA of one K/V tile into a stage: wavefront w fills block w of every plane tile -------
+  const int drow = wave * RPB + lane / CPR;  // tile row this lane's chunk lands in
+  const int dpos = lane % CPR;
+  const int dkey = KT == 16 ? drow : tile_key(drow);
+  const int kchunk = dpos ^ (drow & 7);
+  const int vchunk = dpos ^ (KT == 16 ? 2 * (drow & 7) : 2 * (drow & 3));
+  auto issue = [&](int stage, int kt) {
+    _Float16* st = ring + stage * R::STAGE + wave * 512;
+    const int kg = kt * KT + dkey, vg = kt * KT + drow;
+    const _Float16* ks = kbase + static_cast<size_t>(kg < g.L ? kg : 0) * krow + 8 * kchunk;
+#pragma unroll
+    for (int pl = 0; pl < KPL; ++pl) dma16(ks + pl * k_plane, st + pl * R::TILE);
+    dma16(vbase + static_cast<size_t>(vg < g.L ? vg : 0) * krow + 8 * vchunk, st + KPL * R::TILE);
+  };
+  // The first two tiles go out before the register loads. The compiler does not see the DMA
+  // (inline asm) and counts only its own loads when it waits for them; vmcnt retires in issue
+  // order, so DMA issued after the register loads would be waited for together with them.
+  // Tile 0 is unconditional (rows past L clamp to key 0 of this batch row: always in bounds).
+  issue(0, 0);
+  if (ntiles > 1) issue(1, 1);
+
   // ---- Q fragment: lane (r, g) holds channels 32s + 8g .. +7 of query r ---------------------
   const size_t qbase = ((static_cast<size_t>(g.b) * S + qpos_c) * H + g.head) * D + 8 * gq;
   half8 qh[NS], ql[FUSED ? NS : 1];
 #pragma unroll
   for (int s = 0; s < NS; ++s) qh[s] = *reinterpret_cast<const half8*>(q + qbase + 32 * s);
-
-  // ---- DMA of one K/V tile into a stage (each lane one 16-byte chunk per block) -------------
-  auto issue = [&](Stage& stg, int kt) {
-#pragma unroll
-    for (int j = 0; j < BPW; ++j) {
-      const int blk = wave * BPW + j;
-      const int row = blk * RPB + lane / CPR;
-      const int pos = lane % CPR;
-      {
-        const int key = tile_key(row);
-        const int kg = kt * KT + key;
-        const size_t off = static_cast<size_t>(kg < g.L ? kg : 0) * krow + 8 * (pos ^ (row & 7));
-#pragma unroll
-        for (int pl = 0; pl < KPL; ++pl) dma16(kbase + pl * k_plane + off, &stg.k[pl][blk * 512]);
-      }
-      {
-        const int kg = kt * KT + row;
-        const size_t off =
-            static_cast<size_t>(kg < g.L ? kg : 0) * krow + 8 * (pos ^ (2 * (row & 3)));
-        dma16(vbase + off, &stg.v[blk * 512]);
-      }
-    }
-  };
-  // register loads first, then the tile DMAs: waiting for the former never waits for the latter
   uint4v gw[FUSED ? NS : 1];
   floatx4 cs[FUSED ? NS / 2 : 1][2], sn[FUSED ? NS / 2 : 1][2];
   if constexpr (FUSED) {
@@ -545,10 +551,6 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
       sn[s][1] = *reinterpret_cast<const floatx4*>(stt + 32 * s + 4);
     }
   }
-  // Tile 0 unconditionally (rows past L clamp to key 0 of this batch row: always in bounds).
-  issue(st0, 0);
-  if (ntiles > 1) issue(st1, 1);
-
   if constexpr (FUSED) {
     // RMSNorm over the row (four lanes) then split-half RoPE: channel c < D/2 of step s pairs
     // with channel c + D/2 of step s + NS/2 in the same lane (kernels.metal:53-63, :65-74).
@@ -602,92 +604,126 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
   for (int dt = 0; dt < NDT; ++dt) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.0f;
 
-  // ---- one tile: wait for its DMA, release the oldest stage, compute --------------------------
-  auto step = [&](Stage& cur, Stage& next2, int kt) {
+  // QK^T of one 16-key block whose rows start at kr (rows kr..kr+15 of the K tile)
+  auto qk_block = [&](const _Float16* kt0, int kr) {
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int row = kr + r, rbase = row * D, sw = row & 7;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int off = rbase + 8 * ((4 * s + gq) ^ sw);
+      const half8 ahi = *reinterpret_cast<const half8*>(kt0 + off);
+      if constexpr (FUSED) {
+        const half8 alo = *reinterpret_cast<const half8*>(kt0 + R::TILE + off);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, ql[s], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, qh[s], acc, 0, 0, 0);
+      }
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, qh[s], acc, 0, 0, 0);
+    }
+    return acc;
+  };
+
+  int cur = 0, nxt = 2;  // stage of tile kt, stage tile kt + 2 goes to
+  for (int kt = 0; kt < ntiles; ++kt) {
     // in flight: this tile, then the next one (issued one step earlier or in the prologue)
-    if (kt + 1 < ntiles) wait_vmcnt<LPT>();
+    if (kt + 1 < ntiles) wait_vmcnt<R::LPT>();
     else wait_vmcnt<0>();
     stage_barrier();
-    if (kt + 2 < ntiles) issue(next2, kt + 2);
-    if (kt * KT >= g.wave_end) return;
-    floatx4 sc[2];
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      sc[blk] = floatx4{0.f, 0.f, 0.f, 0.f};
-      const int row = 16 * blk + r;
-      const int rbase = row * ROWH, sw = row & 7;
-      if constexpr (FUSED) {
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          const int off = rbase + 8 * ((4 * s + gq) ^ sw);
-          const half8 ahi = *reinterpret_cast<const half8*>(&cur.k[0][off]);
-          const half8 alo = *reinterpret_cast<const half8*>(&cur.k[1][off]);
-          sc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, ql[s], sc[blk], 0, 0, 0);
-          sc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, qh[s], sc[blk], 0, 0, 0);
-        }
-      }
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        const half8 a =
-            *reinterpret_cast<const half8*>(&cur.k[0][rbase + 8 * ((4 * s + gq) ^ sw)]);
-        sc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[s], sc[blk], 0, 0, 0);
-      }
-    }
-    // element (blk, j) is key 8g + 4blk + j of this tile
-    if (kt * KT + KT > g.limit_min) {
-#pragma unroll
-      for (int blk = 0; blk < 2; ++blk)
+    if (kt + 2 < ntiles) issue(nxt, kt + 2);
+    const _Float16* kst = ring + cur * R::STAGE;
+    const _Float16* vst = kst + KPL * R::TILE;
+    cur = cur == NST - 1 ? 0 : cur + 1;
+    nxt = nxt == NST - 1 ? 0 : nxt + 1;
+    if (kt * KT >= g.wave_end) continue;
+
+    if constexpr (KT == 16) {
+      floatx4 sc = qk_block(kst, 0);
+      // element j is key 4g + j of this tile
+      if (kt * KT + KT > g.limit_min) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          if (kt * KT + 8 * gq + 4 * blk + j >= limit) sc[blk][j] = -INFINITY;
-    }
-    float mloc = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
-                       fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
-    mloc = rowmax4(mloc) * scale_log2;
-    const float m_new = fmaxf(m_run, mloc);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
-    half8 pb;
-    float lsum = 0.0f;
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk)
+          if (kt * KT + 4 * gq + j >= limit) sc[j] = -INFINITY;
+      }
+      const float mloc = rowmax4(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]))) * scale_log2;
+      const float m_new = fmaxf(m_run, mloc);
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+      half4 pb;
+      float lsum = 0.0f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const _Float16 ph =
-            static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(sc[blk][j], scale_log2, -m_use)));
-        pb[4 * blk + j] = ph;
+            static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(sc[j], scale_log2, -m_use)));
+        pb[j] = ph;
         lsum += static_cast<float>(ph);
       }
-    // l_run holds this lane's share of the row sum (its own keys); the four shares of a query
-    // are combined once, after the last tile
-    l_run = l_run * corr + lsum;
-    m_run = m_new;
-    if (__any(corr != 1.0f)) {
+      // l_run holds this lane's share of the row sum (its own keys); the four shares of a query
+      // are combined once, after the last tile
+      l_run = l_run * corr + lsum;
+      m_run = m_new;
+      if (__any(corr != 1.0f)) {
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
-    }
-    // V rows 8g + 4h + r/4, channels 16dt + 4(r%4) .. +3, chunk swizzled by 2*(row & 3)
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      half8 a;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int vrow = 8 * gq + 4 * h + (r >> 2);
-        const int chunk = (2 * dt + ((r & 3) >> 1)) ^ (2 * (vrow & 3));
-        const half4 t = lds_read_tr(&cur.v[vrow * ROWH + 8 * chunk + 4 * (r & 1)]);
-        a[4 * h + 0] = t[0];
-        a[4 * h + 1] = t[1];
-        a[4 * h + 2] = t[2];
-        a[4 * h + 3] = t[3];
+        for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
       }
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, o[dt], 0, 0, 0);
+      // V row 4g + r/4, channels 16dt + 4(r%4) .. +3; chunk swizzled by 2*(row & 7)
+      const int vrow = 4 * gq + (r >> 2);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const int chunk = (2 * dt + ((r & 3) >> 1)) ^ (2 * (vrow & 7));
+        const half4 a = lds_read_tr(vst + vrow * D + 8 * chunk + 4 * (r & 1));
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, o[dt], 0, 0, 0);
+      }
+    } else {
+      floatx4 sc[2];
+      sc[0] = qk_block(kst, 0);
+      sc[1] = qk_block(kst, 16);
+      // element (blk, j) is key 8g + 4blk + j of this tile
+      if (kt * KT + KT > g.limit_min) {
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (kt * KT + 8 * gq + 4 * blk + j >= limit) sc[blk][j] = -INFINITY;
+      }
+      float mloc = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                         fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+      mloc = rowmax4(mloc) * scale_log2;
+      const float m_new = fmaxf(m_run, mloc);
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+      half8 pb;
+      float lsum = 0.0f;
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const _Float16 ph = static_cast<_Float16>(
+              __builtin_amdgcn_exp2f(fmaf(sc[blk][j], scale_log2, -m_use)));
+          pb[4 * blk + j] = ph;
+          lsum += static_cast<float>(ph);
+        }
+      l_run = l_run * corr + lsum;
+      m_run = m_new;
+      if (__any(corr != 1.0f)) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
+      }
+      // V rows 8g + 4h + r/4, channels 16dt + 4(r%4) .. +3, chunk swizzled by 2*(row & 3)
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        half8 a;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int vrow = 8 * gq + 4 * h + (r >> 2);
+          const int chunk = (2 * dt + ((r & 3) >> 1)) ^ (2 * (vrow & 3));
+          const half4 t = lds_read_tr(vst + vrow * D + 8 * chunk + 4 * (r & 1));
+          a[4 * h + 0] = t[0];
+          a[4 * h + 1] = t[1];
+          a[4 * h + 2] = t[2];
+          a[4 * h + 3] = t[3];
+        }
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, o[dt], 0, 0, 0);
+      }
     }
-  };
-
-  for (int kt = 0; kt < ntiles; kt += 3) {
-    step(st0, st2, kt);
-    if (kt + 1 < ntiles) step(st1, st0, kt + 1);
-    if (kt + 2 < ntiles) step(st2, st1, kt + 2);
   }
   // No DMA may still be writing this workgroup's LDS when its wavefronts end.
   wait_vmcnt<0>();
