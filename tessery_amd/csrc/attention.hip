@@ -337,36 +337,46 @@ __global__ __launch_bounds__(256, 2) void attn_f32_mfma(const float* __restrict_
 typedef _Float16 half8x __attribute__((ext_vector_type(8)));
 
 struct Geom16 {
-  int b, kvh, head, p0, L, wave_end, wg_end, limit_min;
+  int b, kvh, head0, p0, L, wave_end, wg_end, limit_min, hsh;
   bool active;
 };
 
-// grid = planes * wgs_per_plane; a workgroup holds four row-blocks of 16 queries of one
-// (batch row, kv head) plane, row-block rb = pos_block * G + head_in_group, order from
-// schedule().
+// The 16 query rows of a wavefront are HPW heads x 16/HPW positions: HPW = G (the q heads that
+// share one kv head) when G divides 16, else 1. Row r is position p0 + (r >> hsh) of head
+// head0 + (r & (HPW - 1)), so with HPW = G the rows of one position are adjacent in memory and
+// share their RoPE angles. A workgroup holds four consecutive wave blocks of one
+// (batch row, kv head) plane; wave block wb = position block * G/HPW + head block.
+__host__ __device__ inline int f16_heads_per_wave(int G) { return 16 % G == 0 ? G : 1; }
+__host__ __device__ inline int f16_wave_blocks(int S, int G) {
+  const int hpw = f16_heads_per_wave(G), ppw = 16 / hpw;
+  return (G / hpw) * ((S + ppw - 1) / ppw);
+}
+
 __device__ __forceinline__ Geom16 make_geom16(const uint32_t* lengths, int B, int S, int H, int KV,
                                               int bidi, int wave) {
   Geom16 g;
   const int G = H / KV;
-  const int nrb = G * ((S + 15) / 16);
-  const int wpp = (nrb + 3) / 4;
+  const int hpw = f16_heads_per_wave(G), ppw = 16 / hpw, hbn = G / hpw;
+  const int nwb = f16_wave_blocks(S, G);
+  const int wpp = (nwb + 3) / 4;
   const Sched sc = schedule(lengths, B, S, KV, wpp);
   const int wgp = sc.wgp;
   g.b = sc.plane / KV;
   g.kvh = sc.plane % KV;
-  const int rb = wgp * 4 + wave;
-  g.active = rb < nrb;
-  g.head = g.kvh * G + rb % G;
-  g.p0 = (rb / G) * 16;
+  g.hsh = __builtin_ctz(hpw);
+  const int wb = wgp * 4 + wave;
+  g.active = wb < nwb;
+  g.head0 = g.kvh * G + (wb % hbn) * hpw;
+  g.p0 = (wb / hbn) * ppw;
   g.L = sc.L;
-  const int rb_last = min(wgp * 4 + 3, nrb - 1);
+  const int wb_last = min(wgp * 4 + 3, nwb - 1);
   if (bidi) {
     g.wave_end = g.active ? g.L : 0;
     g.wg_end = g.L;
     g.limit_min = g.L;
   } else {
-    g.wave_end = g.active ? min(g.p0 + 16, g.L) : 0;
-    g.wg_end = min((rb_last / G) * 16 + 16, g.L);
+    g.wave_end = g.active ? min(g.p0 + ppw, g.L) : 0;
+    g.wg_end = min((wb_last / hbn) * ppw + ppw, g.L);
     g.limit_min = min(g.p0 + 1, g.L);
   }
   return g;
@@ -501,7 +511,8 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
   // the wavefront index is uniform; readfirstlane lets the compiler branch on it with scalars
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const Geom16 g = make_geom16(lengths, B, S, H, KV, bidi, wave);
-  const int qpos = g.p0 + r;
+  const int qpos = g.p0 + (r >> g.hsh);
+  const int qhead = g.head0 + (r & ((1 << g.hsh) - 1));
   const bool qvalid = g.active && qpos < S;
   const int qpos_c = min(qpos, S - 1);
   const int limit = bidi ? g.L : min(qpos + 1, g.L);
@@ -532,7 +543,7 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
   if (ntiles > 1) issue(1, 1);
 
   // ---- Q fragment: lane (r, g) holds channels 32s + 8g .. +7 of query r ---------------------
-  const size_t qbase = ((static_cast<size_t>(g.b) * S + qpos_c) * H + g.head) * D + 8 * gq;
+  const size_t qbase = ((static_cast<size_t>(g.b) * S + qpos_c) * H + qhead) * D + 8 * gq;
   half8 qh[NS], ql[FUSED ? NS : 1];
 #pragma unroll
   for (int s = 0; s < NS; ++s) qh[s] = *reinterpret_cast<const half8*>(q + qbase + 32 * s);
@@ -725,22 +736,52 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
       }
     }
   }
-  // No DMA may still be writing this workgroup's LDS when its wavefronts end.
+  // No DMA may still be writing this workgroup's LDS past this point, and after the barrier no
+  // wavefront reads the ring any more: it becomes the staging area of the output rows.
   wait_vmcnt<0>();
-  const float l_row = rowsum4(l_run);
+  const float inv = 1.0f / rowsum4(l_run);
+  stage_barrier();
 
-  if (qvalid) {
-    const float inv = 1.0f / l_row;
-    const size_t base = ((static_cast<size_t>(g.b) * S + qpos) * H + g.head) * D + 4 * gq;
+  // ---- epilogue: fragments -> row-major rows in LDS -> full-row global stores ---------------
+  // Each wavefront owns 16 rows of RS bytes (RB of data + 64 of padding, which spreads the rows
+  // of one ds_write over all banks). When the ring cannot hold 4 x 16 rows the rows go through
+  // in two rounds of eight.
+  constexpr int RB = D * static_cast<int>(sizeof(TOut));
+  constexpr int RS = RB + 64;
+  constexpr int RPR = NST * R::STAGE * 2 >= 4 * 16 * RS ? 16 : 8;  // rows per round
+  static_assert(NST * R::STAGE * 2 >= 4 * RPR * RS, "output staging exceeds the ring");
+  constexpr int OCH = RB / 16;  // 16-byte chunks per output row
+  char* const ob = reinterpret_cast<char*>(ring) + wave * RPR * RS;
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      TOut* dst = out + base + 16 * dt;
-      if constexpr (sizeof(TOut) == 2) {
-        half4 rv = {static_cast<_Float16>(o[dt][0] * inv), static_cast<_Float16>(o[dt][1] * inv),
-                    static_cast<_Float16>(o[dt][2] * inv), static_cast<_Float16>(o[dt][3] * inv)};
-        *reinterpret_cast<half4*>(dst) = rv;
-      } else {
-        *reinterpret_cast<floatx4*>(dst) = o[dt] * inv;
+  for (int round = 0; round < 16 / RPR; ++round) {
+    if ((r / RPR) == round) {
+      char* const orow = ob + (r % RPR) * RS;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        if constexpr (sizeof(TOut) == 2) {
+          const half4 rv = {static_cast<_Float16>(o[dt][0] * inv),
+                            static_cast<_Float16>(o[dt][1] * inv),
+                            static_cast<_Float16>(o[dt][2] * inv),
+                            static_cast<_Float16>(o[dt][3] * inv)};
+          *reinterpret_cast<half4*>(orow + 2 * (16 * dt + 4 * gq)) = rv;
+        } else {
+          *reinterpret_cast<floatx4*>(orow + 4 * (16 * dt + 4 * gq)) = o[dt] * inv;
+        }
+      }
+    }
+    // rows are read back by other lanes of the same wavefront: LDS executes a wavefront's
+    // accesses in order, so no barrier is needed
+#pragma unroll
+    for (int i = 0; i < RPR * OCH / 64; ++i) {
+      const int c = 64 * i + lane;
+      const int row = round * RPR + c / OCH, ch = c % OCH;
+      const int pos = g.p0 + (row >> g.hsh);
+      const int head = g.head0 + (row & ((1 << g.hsh) - 1));
+      const uint4v val = *reinterpret_cast<const uint4v*>(ob + (c / OCH) * RS + 16 * ch);
+      if (g.active && pos < S) {
+        char* dst = reinterpret_cast<char*>(out) +
+                    (((static_cast<size_t>(g.b) * S + pos) * H + head) * D) * sizeof(TOut);
+        *reinterpret_cast<uint4v*>(dst + 16 * ch) = val;
       }
     }
   }
@@ -803,9 +844,7 @@ hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st) {
 }
 
 static unsigned mfma16_grid(int B, int S, int H, int KV) {
-  const int G = H / KV;
-  const int nrb = G * ((S + 15) / 16);
-  return static_cast<unsigned>(B * KV * ((nrb + 3) / 4));
+  return static_cast<unsigned>(B * KV * ((f16_wave_blocks(S, H / KV) + 3) / 4));
 }
 
 template <int D, bool FUSED>
