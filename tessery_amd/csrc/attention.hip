@@ -452,6 +452,15 @@ __device__ __forceinline__ void stage_barrier() {
 // K/V ring geometry. A tile holds KT = 2048 / D keys, so every plane tile (K hi, K lo when fused,
 // V) is 4 KiB: four 1 KiB DMA blocks, one per wavefront. D = 128 runs 16-key tiles, D = 64 runs
 // 32-key tiles. Three stages cost 36 KiB (fused) / 24 KiB (plain) of LDS per workgroup.
+// K-tile chunk swizzle. LDS has 64 banks of 4 bytes and serves a 16-byte-per-lane read 16 lanes
+// at a time: the 16 rows r of one k-step read must land on 16 different 16-byte bank groups.
+// D = 128 rows are 256 bytes (one bank line), so the chunk is XORed with r & 15; D = 64 rows are
+// half a bank line, so row parity picks the half and (r >> 1) & 7 the chunk.
+template <int D>
+__device__ __forceinline__ int ksw(int row) {
+  return D == 128 ? (row & 15) : ((row >> 1) & 7);
+}
+
 template <int D, bool FUSED>
 struct F16Ring {
   static constexpr int KT = 2048 / D;
@@ -484,7 +493,7 @@ struct F16Ring {
 // K/V tiles stream through a three-stage LDS ring filled by global_load_lds_dwordx4, issued two
 // tiles ahead of use, with one barrier per tile; the stage is chosen at run time so the loop
 // body exists once. The DMA writes each 1 KiB block contiguously and the global chunk a lane
-// fetches sets the layout: K rows XOR-swizzle their 16-byte chunks by (row & 7), V rows by
+// fetches sets the layout: K rows XOR-swizzle their 16-byte chunks by ksw(row), V rows by
 // 2 * (row & 7) (D = 128) or 2 * (row & 3) (D = 64), which keeps the MFMA operand reads free of
 // bank conflicts. Key rows at or beyond L are fetched from key 0 (finite data) and masked.
 //
@@ -525,7 +534,7 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
   const int drow = wave * RPB + lane / CPR;  // tile row this lane's chunk lands in
   const int dpos = lane % CPR;
   const int dkey = KT == 16 ? drow : tile_key(drow);
-  const int kchunk = dpos ^ (drow & 7);
+  const int kchunk = dpos ^ ksw<D>(drow);
   const int vchunk = dpos ^ (KT == 16 ? 2 * (drow & 7) : 2 * (drow & 3));
   auto issue = [&](int stage, int kt) {
     _Float16* st = ring + stage * R::STAGE + wave * 512;
@@ -618,7 +627,7 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
   // QK^T of one 16-key block whose rows start at kr (rows kr..kr+15 of the K tile)
   auto qk_block = [&](const _Float16* kt0, int kr) {
     floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-    const int row = kr + r, rbase = row * D, sw = row & 7;
+    const int row = kr + r, rbase = row * D, sw = ksw<D>(row);
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       const int off = rbase + 8 * ((4 * s + gq) ^ sw);
@@ -743,11 +752,11 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
   stage_barrier();
 
   // ---- epilogue: fragments -> row-major rows in LDS -> full-row global stores ---------------
-  // Each wavefront owns 16 rows of RS bytes (RB of data + 64 of padding, which spreads the rows
-  // of one ds_write over all banks). When the ring cannot hold 4 x 16 rows the rows go through
+  // Each wavefront owns 16 rows of RS bytes (RB of data + 16 of padding: the 16 rows written
+  // by one group of 16 lanes start on 16 different bank groups). When the ring cannot hold 4 x 16 rows the rows go through
   // in two rounds of eight.
   constexpr int RB = D * static_cast<int>(sizeof(TOut));
-  constexpr int RS = RB + 64;
+  constexpr int RS = RB + 16;
   constexpr int RPR = NST * R::STAGE * 2 >= 4 * 16 * RS ? 16 : 8;  // rows per round
   static_assert(NST * R::STAGE * 2 >= 4 * RPR * RS, "output staging exceeds the ring");
   constexpr int OCH = RB / 16;  // 16-byte chunks per output row
