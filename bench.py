@@ -14,6 +14,7 @@ HIP-event timings, and the float64 NumPy CPU oracle timed on the host on a bound
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import sys
@@ -31,7 +32,10 @@ METRIC = "prefill attention tokens/s + TFLOP/s (% MFMA peak), Qwen3 GQA 32x512, 
 PEAK_F16_TFLOPS = 2516.6
 PEAK_HBM_GBS = 8000.0
 LAYERS = 28
-TRAFFIC_FILE = ROOT / "profiles" / "traffic_attention_f16_norm_rope.json"
+# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of the attention kernel on this workload, with the
+# copy-kernel calibration of each counter; valid for the kernel source it names
+TRAFFIC_FILE = ROOT / "profiles" / "attention_f16_norm_rope_qwen3_32x512_traffic.txt"
+KERNEL_SOURCE = ROOT / "tessery_amd" / "csrc" / "attention.hip"
 
 
 def log(message: str) -> None:
@@ -55,6 +59,28 @@ def upload_layers(rt: HipRuntime, shape: workloads.Shape, layers: int):
         if layer == 0:
             host0 = t
     return sets, host0
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per attention launch from the committed counter summary, or None when it is
+    missing or was measured on a different kernel source."""
+    if not TRAFFIC_FILE.is_file():
+        return None
+    fields = {}
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        key, sep, value = line.partition(":")
+        if sep:
+            fields[key.strip()] = value.strip()
+    try:
+        source = hashlib.sha256(KERNEL_SOURCE.read_bytes()).hexdigest()
+        if fields.get("attention.hip sha256") != source:
+            log("traffic summary was measured on another kernel source; traffic = null")
+            return None
+        fetch = float(fields["FETCH_SIZE KiB per dispatch"]) * float(fields["FETCH_SIZE factor"])
+        write = float(fields["WRITE_SIZE KiB per dispatch"]) * float(fields["WRITE_SIZE factor"])
+    except (KeyError, ValueError, OSError):
+        return None
+    return int(round((fetch + write) * 1024))
 
 
 def encode_step(rt, shape, sets, lengths_buf, k_work):
@@ -156,10 +182,13 @@ def main() -> int:
         wall = time.perf_counter() - launched
         gpu = rt.last_gpu_seconds
         log(f"timed {args.steps} steps: wall {wall * 1e3:.3f} ms, events {gpu * 1e3:.3f} ms")
-        # per-launch durations (HIP events bracketing each launch on the runtime stream)
+        # per-launch durations: HIP events recorded around every launch on the runtime stream,
+        # over the same steps replayed once more (a command profiles at most 2048 launches)
+        prof_steps = max(1, min(args.steps, 2048 // (2 * args.layers)))
         with rt.profile_kernels() as records:
             with rt.command():
-                encode_step(rt, shape, sets, lengths_buf, k_work)
+                for _ in range(prof_steps):
+                    encode_step(rt, shape, sets, lengths_buf, k_work)
         attn = [r["gpu_seconds"] for r in records if r["kernel"] == "attention_f16_norm_rope"]
         prologue = [r["gpu_seconds"] for r in records if r["kernel"] == "norm_rope_f16"]
         out0 = rt.read(sets[0]["out"], host0["q"].shape)
@@ -168,9 +197,7 @@ def main() -> int:
     tokens = shape.tokens * args.layers
     attn_avg = float(np.mean(attn))
     achieved = nbytes / attn_avg / 1e9
-    traffic = None
-    if TRAFFIC_FILE.is_file():
-        traffic = json.loads(TRAFFIC_FILE.read_text()).get("bytes_per_launch")
+    traffic = measured_traffic()
     tflops = flop * args.layers / step / 1e12
     result = {
         "metric": METRIC,
