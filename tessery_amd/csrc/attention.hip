@@ -8,19 +8,20 @@
 // Layout (row-major, no strides): q/out [B,S,H,D], k/v [B,S,KV,D], lengths u32[B].
 //
 // Three kernels:
-//   attn_scalar      one wavefront per (token, head); any D <= 256. Route "attention".
+//   attn_scalar      one wavefront per (token, head); any D <= 256. Routes "attention" and
+//                    "attention_f16_scalar".
 //   attn_f32_mfma    fp32 MFMA (v_mfma_f32_32x32x2_f32) tiles, D in {32,64,128}; any S.
 //                    Routes "attention_tiled", "attention_tail_32", "attention_tail_128".
-//   attn_f16_mfma    fp16 operands / fp32 accumulate (v_mfma_f32_32x32x16_f16), D in {32,64,128},
-//                    any S, optional fused per-head RMSNorm + RoPE of Q. Routes "attention_f16*".
+//   attn_f16_mfma    fp16 operands / fp32 accumulation (v_mfma_f32_16x16x32_f16 and
+//                    16x16x16_f16), D in {64,128}, any S, optional fused per-head RMSNorm + RoPE
+//                    of Q with split-precision scores. Routes "attention_f16",
+//                    "attention_f16_norm_rope".
 //
-// MFMA formulation (both MFMA kernels). Each wavefront owns 32 query rows of one head and
-// computes the TRANSPOSED score tile S^T = K * Q^T, so that lane l holds the scores of query
-// (l % 32) for 16 keys and its partner lane l ^ 32 holds the other 16. Row max / row sum then
-// need one cross-half exchange, the softmax statistics of a query live in the lane that owns
-// it, and P^T can be fed straight from the accumulator registers into O^T = V^T * P^T without
-// an LDS round trip. Workgroups hold four wavefronts that share one KV head, so the K/V tile
-// staged in LDS serves both query heads of a Qwen3 GQA pair.
+// Both MFMA kernels compute the TRANSPOSED score tile S^T = K * Q^T, so the scores of one query
+// sit in the lanes that own that query: the row max / row sum are cross-lane reductions over a
+// few lanes, the softmax statistics stay in registers, and P^T feeds O^T = V^T * P^T straight
+// from the accumulators without an LDS round trip. A workgroup holds four wavefronts that share
+// one KV head, so each K/V tile staged in LDS serves every query head of a GQA group.
 #include "common.h"
 #include "kernels.h"
 
