@@ -92,38 +92,46 @@ __global__ __launch_bounds__(64) void attn_scalar(const TIn* __restrict__ q,
 // fetched into one L2 once and reused while that plane's workgroups run together. Planes are
 // ordered by the length of their batch row, longest first (causal and bidirectional cost both
 // grow with it), and inside a plane the last (longest causal) query blocks go first.
-// The ranking is computed by every wavefront from `lengths` with one ballot; it needs
-// planes % 8 == 0 and B <= 64, otherwise planes keep their natural order.
+// The ranking is computed by every wavefront from `lengths` with one vector load; it needs
+// planes % 8 == 0 and B <= 64 (sched_ranked), otherwise planes keep their natural order.
+//
+// The grid carries the decomposition, so no division is needed to decode it (sched_grid):
+// ranked: (8, wpp, planes / 8) - linear id x + 8 * (y + wpp * z) runs on XCD x, and XCD x takes
+//         plane ranks z * 8 + x in z order with block y of each; otherwise: (wpp, planes, 1).
 struct Sched {
   int plane, wgp, L;  // L: valid length of the plane's batch row, clamped to S
 };
 
-__device__ __forceinline__ Sched schedule(const uint32_t* lengths, int B, int S, int KV, int wpp) {
-  constexpr int kXcds = 8;
-  const int planes = B * KV;
-  const int bid = static_cast<int>(blockIdx.x);
+__host__ __device__ inline bool sched_ranked(int B, int KV) { return (B * KV) % 8 == 0 && B <= 64; }
+
+__host__ inline dim3 sched_grid(int B, int KV, int wpp) {
+  const unsigned planes = static_cast<unsigned>(B * KV);
+  return sched_ranked(B, KV) ? dim3(8, static_cast<unsigned>(wpp), planes / 8)
+                             : dim3(static_cast<unsigned>(wpp), planes, 1);
+}
+
+__device__ __forceinline__ Sched schedule(const uint32_t* lengths, int B, int S, int KV) {
   Sched sc;
-  if (planes % kXcds == 0 && B <= 64) {
-    const int x = bid % kXcds, li = bid / kXcds;
-    const int j = (li / wpp) * kXcds + x;  // plane rank, longest row first
-    sc.wgp = wpp - 1 - li % wpp;
-    const int jrow = j / KV, kvh = j % KV;
-    // one vector load of the lengths; the ranking reads other lanes' values with v_readlane
-    // instead of a chain of dependent scalar loads
+  if (sched_ranked(B, KV)) {
+    const int j = static_cast<int>(blockIdx.z) * 8 + static_cast<int>(blockIdx.x);  // plane rank
+    sc.wgp = static_cast<int>(gridDim.y - 1 - blockIdx.y);
+    const int jrow = j / KV, kvh = j - jrow * KV;
+    // Lane l < B holds key (length << 6) | (63 - l): distinct keys, longer rows first and the
+    // lower index first among equal lengths. A row's rank counts the larger keys, read from the
+    // other lanes with v_readlane (no dependent loads).
+    // (the load is unconditional, from a clamped index, so it issues first thing)
     const int lane = threadIdx.x & 63;
-    const uint32_t mine = lane < B ? min(lengths[lane], static_cast<uint32_t>(S)) : 0u;
+    const uint32_t len = min(lengths[min(lane, B - 1)], static_cast<uint32_t>(S));
+    const uint32_t key = lane < B ? (len << 6) | static_cast<uint32_t>(63 - lane) : 0u;
     int rank = 0;
-    for (int other = 0; other < B; ++other) {
-      const uint32_t lo = __builtin_amdgcn_readlane(mine, other);
-      rank += (lo > mine) || (lo == mine && other < lane);
-    }
+    for (int other = 0; other < B; ++other) rank += __builtin_amdgcn_readlane(key, other) > key;
     const unsigned long long hit = __ballot(lane < B && rank == jrow);
     const int b = __ffsll(hit) - 1;
     sc.plane = b * KV + kvh;
-    sc.L = static_cast<int>(__builtin_amdgcn_readlane(mine, b));
+    sc.L = static_cast<int>(__builtin_amdgcn_readlane(len, b));
   } else {
-    sc.plane = bid / wpp;
-    sc.wgp = wpp - 1 - bid % wpp;
+    sc.plane = static_cast<int>(blockIdx.y);
+    sc.wgp = static_cast<int>(gridDim.x - 1 - blockIdx.x);
     sc.L = static_cast<int>(min(lengths[sc.plane / KV], static_cast<uint32_t>(S)));
   }
   return sc;
@@ -139,8 +147,7 @@ __device__ __forceinline__ Geom make_geom(const uint32_t* lengths, int B, int S,
   Geom g;
   const int G = H / KV;
   const int nrb = G * ((S + 31) / 32);
-  const int wpp = (nrb + 3) / 4;
-  const Sched sc = schedule(lengths, B, S, KV, wpp);
+  const Sched sc = schedule(lengths, B, S, KV);
   const int wgp = sc.wgp;
   g.b = sc.plane / KV;
   g.kvh = sc.plane % KV;
@@ -353,22 +360,27 @@ __host__ __device__ inline int f16_wave_blocks(int S, int G) {
   return (G / hpw) * ((S + ppw - 1) / ppw);
 }
 
-__device__ __forceinline__ Geom16 make_geom16(const uint32_t* lengths, int B, int S, int H, int KV,
-                                              int bidi, int wave) {
+// Shape constants computed once on the host: G = H / KV, hsh = log2(heads per wave), nwb = wave
+// blocks per plane.
+struct F16Shape {
+  int G, hsh, nwb;
+};
+
+__device__ __forceinline__ Geom16 make_geom16(const uint32_t* lengths, int B, int S, int KV,
+                                              int bidi, int wave, F16Shape sh) {
   Geom16 g;
-  const int G = H / KV;
-  const int hpw = f16_heads_per_wave(G), ppw = 16 / hpw, hbn = G / hpw;
-  const int nwb = f16_wave_blocks(S, G);
-  const int wpp = (nwb + 3) / 4;
-  const Sched sc = schedule(lengths, B, S, KV, wpp);
+  const int G = sh.G, nwb = sh.nwb;
+  const int hpw = 1 << sh.hsh, ppw = 16 >> sh.hsh, hbn = G >> sh.hsh;
+  const Sched sc = schedule(lengths, B, S, KV);
   const int wgp = sc.wgp;
   g.b = sc.plane / KV;
-  g.kvh = sc.plane % KV;
-  g.hsh = __builtin_ctz(hpw);
+  g.kvh = sc.plane - g.b * KV;
+  g.hsh = sh.hsh;
   const int wb = wgp * 4 + wave;
   g.active = wb < nwb;
-  g.head0 = g.kvh * G + (wb % hbn) * hpw;
-  g.p0 = (wb / hbn) * ppw;
+  const int pblk = hbn == 1 ? wb : wb / hbn;  // hbn == 1 whenever G divides 16
+  g.head0 = g.kvh * G + (wb - pblk * hbn) * hpw;
+  g.p0 = pblk * ppw;
   g.L = sc.L;
   const int wb_last = min(wgp * 4 + 3, nwb - 1);
   if (bidi) {
@@ -503,24 +515,35 @@ struct F16Ring {
 // norm_rope_f16). Q is also carried as hi + lo, and the scores accumulate
 // K_hi*Q_lo + K_lo*Q_hi + K_hi*Q_hi in fp32: q and k enter the dot products at ~22 bits.
 // ---------------------------------------------------------------------------------------------
+// The running max of a row moves only when a tile's max exceeds it by more than kMaxSlack (in
+// log2 units). Probabilities are then at most 2^kMaxSlack = 256, exact in range for fp16 P and
+// fp32 sums, and later tiles rarely pay the O rescale. The softmax is shift-invariant, so the
+// result does not depend on which max is used.
+constexpr float kMaxSlack = 8.0f;
+
 template <int D, typename TOut, bool FUSED>
 __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
     const _Float16* __restrict__ q, const _Float16* __restrict__ k, const _Float16* __restrict__ v,
     const uint32_t* __restrict__ lengths, TOut* __restrict__ out, int B, int S, int H, int KV,
     float scale_log2, int bidi, const uint16_t* __restrict__ gamma,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, float eps,
-    size_t k_plane) {
+    size_t k_plane, F16Shape shp) {
   using R = F16Ring<D, FUSED>;
   constexpr int KT = R::KT, KPL = R::KPL, NST = R::NST, RPB = R::RPB, CPR = R::CPR;
   constexpr int NS = D / 32;   // k-steps per 16x16 score block
   constexpr int NDT = D / 16;  // 16-channel output blocks
   static_assert(D == 64 || D == 128, "pipelined fp16 kernel serves D = 64 or 128");
-  __shared__ __attribute__((aligned(1024))) _Float16 ring[NST * R::STAGE];
+  // output staging after the loop: 4 wavefronts x 16 rows of RS bytes (RB of data + 16 of
+  // padding, so the 16 rows written by one group of 16 lanes start on 16 different bank groups)
+  constexpr int RB = D * static_cast<int>(sizeof(TOut));
+  constexpr int RS = RB + 16;
+  constexpr int LDS_HALVES = NST * R::STAGE > 4 * 16 * RS / 2 ? NST * R::STAGE : 4 * 16 * RS / 2;
+  __shared__ __attribute__((aligned(1024))) _Float16 ring[LDS_HALVES];
 
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, gq = lane >> 4;
   // the wavefront index is uniform; readfirstlane lets the compiler branch on it with scalars
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const Geom16 g = make_geom16(lengths, B, S, H, KV, bidi, wave);
+  const Geom16 g = make_geom16(lengths, B, S, KV, bidi, wave, shp);
   const int qpos = g.p0 + (r >> g.hsh);
   const int qhead = g.head0 + (r & ((1 << g.hsh) - 1));
   const bool qvalid = g.active && qpos < S;
@@ -665,7 +688,9 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
           if (kt * KT + 4 * gq + j >= limit) sc[j] = -INFINITY;
       }
       const float mloc = rowmax4(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]))) * scale_log2;
-      const float m_new = fmaxf(m_run, mloc);
+      // lazy running max: moved only when a tile exceeds it by more than kMaxSlack
+      const bool grow = mloc > m_run + kMaxSlack;
+      const float m_new = grow ? mloc : m_run;
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
       const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
       half4 pb;
@@ -681,7 +706,7 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
       // are combined once, after the last tile
       l_run = l_run * corr + lsum;
       m_run = m_new;
-      if (__any(corr != 1.0f)) {
+      if (__any(grow)) {
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
       }
@@ -708,7 +733,9 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
       float mloc = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
                          fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
       mloc = rowmax4(mloc) * scale_log2;
-      const float m_new = fmaxf(m_run, mloc);
+      // lazy running max: moved only when a tile exceeds it by more than kMaxSlack
+      const bool grow = mloc > m_run + kMaxSlack;
+      const float m_new = grow ? mloc : m_run;
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
       const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
       half8 pb;
@@ -724,7 +751,7 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
         }
       l_run = l_run * corr + lsum;
       m_run = m_new;
-      if (__any(corr != 1.0f)) {
+      if (__any(grow)) {
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
       }
@@ -753,57 +780,53 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
   stage_barrier();
 
   // ---- epilogue: fragments -> row-major rows in LDS -> full-row global stores ---------------
-  // Each wavefront owns 16 rows of RS bytes (RB of data + 16 of padding: the 16 rows written
-  // by one group of 16 lanes start on 16 different bank groups). When the ring cannot hold 4 x 16 rows the rows go through
-  // in two rounds of eight.
-  constexpr int RB = D * static_cast<int>(sizeof(TOut));
-  constexpr int RS = RB + 16;
-  constexpr int RPR = NST * R::STAGE * 2 >= 4 * 16 * RS ? 16 : 8;  // rows per round
-  static_assert(NST * R::STAGE * 2 >= 4 * RPR * RS, "output staging exceeds the ring");
-  constexpr int OCH = RB / 16;  // 16-byte chunks per output row
-  char* const ob = reinterpret_cast<char*>(ring) + wave * RPR * RS;
+  constexpr int OCH = RB / 16;         // 16-byte chunks per output row
+  constexpr int NI = 16 * OCH / 64;    // store instructions per wavefront
+  char* const ob = reinterpret_cast<char*>(ring) + wave * 16 * RS;
+  char* const obase =
+      reinterpret_cast<char*>(out) + ((static_cast<size_t>(g.b) * S + g.p0) * H + g.head0) * RB;
+  {
+    char* const orow = ob + r * RS;
 #pragma unroll
-  for (int round = 0; round < 16 / RPR; ++round) {
-    if ((r / RPR) == round) {
-      char* const orow = ob + (r % RPR) * RS;
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        if constexpr (sizeof(TOut) == 2) {
-          const half4 rv = {static_cast<_Float16>(o[dt][0] * inv),
-                            static_cast<_Float16>(o[dt][1] * inv),
-                            static_cast<_Float16>(o[dt][2] * inv),
-                            static_cast<_Float16>(o[dt][3] * inv)};
-          *reinterpret_cast<half4*>(orow + 2 * (16 * dt + 4 * gq)) = rv;
-        } else {
-          *reinterpret_cast<floatx4*>(orow + 4 * (16 * dt + 4 * gq)) = o[dt] * inv;
-        }
+    for (int dt = 0; dt < NDT; ++dt) {
+      if constexpr (sizeof(TOut) == 2) {
+        const half4 rv = {static_cast<_Float16>(o[dt][0] * inv),
+                          static_cast<_Float16>(o[dt][1] * inv),
+                          static_cast<_Float16>(o[dt][2] * inv),
+                          static_cast<_Float16>(o[dt][3] * inv)};
+        *reinterpret_cast<half4*>(orow + 2 * (16 * dt + 4 * gq)) = rv;
+      } else {
+        *reinterpret_cast<floatx4*>(orow + 4 * (16 * dt + 4 * gq)) = o[dt] * inv;
       }
     }
-    // rows are read back by other lanes of the same wavefront: LDS executes a wavefront's
-    // accesses in order, so no barrier is needed
+  }
+  // Rows are read back by other lanes of the same wavefront: LDS executes a wavefront's accesses
+  // in order, so no barrier is needed. All reads go out before the first store.
+  uint4v val[NI];
 #pragma unroll
-    for (int i = 0; i < RPR * OCH / 64; ++i) {
-      const int c = 64 * i + lane;
-      const int row = round * RPR + c / OCH, ch = c % OCH;
-      const int pos = g.p0 + (row >> g.hsh);
-      const int head = g.head0 + (row & ((1 << g.hsh) - 1));
-      const uint4v val = *reinterpret_cast<const uint4v*>(ob + (c / OCH) * RS + 16 * ch);
-      if (g.active && pos < S) {
-        char* dst = reinterpret_cast<char*>(out) +
-                    (((static_cast<size_t>(g.b) * S + pos) * H + head) * D) * sizeof(TOut);
-        *reinterpret_cast<uint4v*>(dst + 16 * ch) = val;
-      }
-    }
+  for (int i = 0; i < NI; ++i) {
+    const int c = 64 * i + lane;
+    val[i] = *reinterpret_cast<const uint4v*>(ob + (c / OCH) * RS + 16 * (c % OCH));
+  }
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int c = 64 * i + lane;
+    const int row = c / OCH;
+    const int prow = row >> g.hsh;  // position offset of the row inside the wave block
+    // output row index relative to (b, p0, head0): prow * H + head offset, 32-bit
+    const unsigned rel = static_cast<unsigned>(prow * H + (row & ((1 << g.hsh) - 1)));
+    if (g.active && g.p0 + prow < S)
+      *reinterpret_cast<uint4v*>(obase + rel * RB + 16 * (c % OCH)) = val[i];
   }
 }
 
 // ---------------------------------------------------------------------------------------------
 // Host launchers.
 // ---------------------------------------------------------------------------------------------
-static unsigned mfma_grid(int B, int S, int H, int KV) {
+static dim3 mfma_grid(int B, int S, int H, int KV) {
   const int G = H / KV;
   const int nrb = G * ((S + 31) / 32);
-  return static_cast<unsigned>(B * KV * ((nrb + 3) / 4));
+  return sched_grid(B, KV, (nrb + 3) / 4);
 }
 
 hipError_t launch_attention_scalar(const AttnArgs& a, hipStream_t st) {
@@ -831,8 +854,8 @@ hipError_t launch_attention_scalar(const AttnArgs& a, hipStream_t st) {
 }
 
 hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st) {
-  const unsigned grid = mfma_grid(a.B, a.S, a.H, a.KV);
-  if (!grid) return hipSuccess;
+  if (!a.B || !a.S || !a.H) return hipSuccess;
+  const dim3 grid = mfma_grid(a.B, a.S, a.H, a.KV);
   const float sl2 = a.scale * kLog2e;
   auto q = static_cast<const float*>(a.q), k = static_cast<const float*>(a.k),
        v = static_cast<const float*>(a.v);
@@ -853,37 +876,40 @@ hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-static unsigned mfma16_grid(int B, int S, int H, int KV) {
-  return static_cast<unsigned>(B * KV * ((f16_wave_blocks(S, H / KV) + 3) / 4));
-}
-
 template <int D, bool FUSED>
-static void launch_f16_d(const AttnArgs& a, unsigned grid, float sl2, hipStream_t st) {
+static void launch_f16_d(const AttnArgs& a, dim3 grid, F16Shape shp, float sl2, hipStream_t st) {
   auto q = static_cast<const _Float16*>(a.q), k = static_cast<const _Float16*>(a.k),
        v = static_cast<const _Float16*>(a.v);
   const size_t plane = static_cast<size_t>(a.B) * a.S * a.KV * a.D;
   if (a.out_f16)
     attn_f16_mfma<D, _Float16, FUSED><<<grid, 256, 0, st>>>(
         q, k, v, a.lengths, static_cast<_Float16*>(a.out), a.B, a.S, a.H, a.KV, sl2, a.bidi,
-        a.gamma_q, a.rope_cos, a.rope_sin, a.eps, plane);
+        a.gamma_q, a.rope_cos, a.rope_sin, a.eps, plane, shp);
   else
     attn_f16_mfma<D, float, FUSED><<<grid, 256, 0, st>>>(
         q, k, v, a.lengths, static_cast<float*>(a.out), a.B, a.S, a.H, a.KV, sl2, a.bidi,
-        a.gamma_q, a.rope_cos, a.rope_sin, a.eps, plane);
+        a.gamma_q, a.rope_cos, a.rope_sin, a.eps, plane, shp);
 }
 
 hipError_t launch_attention_f16(const AttnArgs& a, hipStream_t st) {
-  const unsigned grid = mfma16_grid(a.B, a.S, a.H, a.KV);
-  if (!grid) return hipSuccess;
+  if (!a.B || !a.S || !a.H) return hipSuccess;
+  F16Shape shp;
+  shp.G = a.H / a.KV;
+  shp.hsh = __builtin_ctz(static_cast<unsigned>(f16_heads_per_wave(shp.G)));
+  shp.nwb = f16_wave_blocks(a.S, shp.G);
+  const dim3 grid = sched_grid(a.B, a.KV, (shp.nwb + 3) / 4);
+
   const float sl2 = a.scale * kLog2e;
   const bool fused = a.gamma_q != nullptr;
   if (fused && (!a.rope_cos || !a.rope_sin)) return hipErrorInvalidValue;
   switch (a.D) {
     case 64:
-      fused ? launch_f16_d<64, true>(a, grid, sl2, st) : launch_f16_d<64, false>(a, grid, sl2, st);
+      fused ? launch_f16_d<64, true>(a, grid, shp, sl2, st)
+            : launch_f16_d<64, false>(a, grid, shp, sl2, st);
       break;
     case 128:
-      fused ? launch_f16_d<128, true>(a, grid, sl2, st) : launch_f16_d<128, false>(a, grid, sl2, st);
+      fused ? launch_f16_d<128, true>(a, grid, shp, sl2, st)
+            : launch_f16_d<128, false>(a, grid, shp, sl2, st);
       break;
     default:
       return hipErrorInvalidValue;
