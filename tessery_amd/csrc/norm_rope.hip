@@ -49,70 +49,80 @@ __global__ __launch_bounds__(256) void rope_f32(float* x, const float* __restric
 // RoPE partners D/2+8j..D/2+8j+7, so the rotation never leaves the lane. fp32 math. With
 // y_lo != null the result is also written as a second fp16 plane y_lo = fp16(y - y_hi), so that
 // y_hi + y_lo carries the fp32 value to ~22 bits for the split-precision attention.
+//
+// Grid (ceil(S / block), B): a workgroup owns `block` positions of one batch row, reads that
+// row's length once and leaves at once when the block starts past it. Each thread owns one
+// (position slot, head, lane) and walks the block's positions in passes of 256 / (T * heads)
+// positions; rows at or past the length are never read or written.
+
 template <int D>
 __global__ __launch_bounds__(256) void norm_rope_f16(const _Float16* __restrict__ x,
                                                      _Float16* __restrict__ y,
                                                      const uint16_t* __restrict__ gamma,
                                                      const float* __restrict__ cos_tab,
                                                      const float* __restrict__ sin_tab,
-                                                     const uint32_t* __restrict__ lengths, int B,
-                                                     int S, int heads, float eps,
+                                                     const uint32_t* __restrict__ lengths, int S,
+                                                     int heads, int block, float eps,
                                                      _Float16* __restrict__ y_lo) {
   constexpr int T = D / 16;
   constexpr int HALF = D / 2;
+  const int b = static_cast<int>(blockIdx.y);
+  const int p0 = static_cast<int>(blockIdx.x) * block;
+  const int L = static_cast<int>(min(lengths[b], static_cast<uint32_t>(S)));
+  if (p0 >= L) return;  // workgroup-uniform
   const int tid = threadIdx.x;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / T) + tid / T;
+  const int lanes_per_pos = T * heads;         // <= 256, checked by the launcher
+  const int ppp = 256 / lanes_per_pos;         // positions per pass
+  const int slot = tid / lanes_per_pos;        // position slot of this thread
+  const int head = (tid % lanes_per_pos) / T;
   const int j = tid % T;
-  const int64_t rows = static_cast<int64_t>(B) * S * heads;
-  bool valid = row < rows;
-  int pos = 0;
-  if (valid) {
-    const int64_t token = row / heads;
-    const int b = static_cast<int>(token / S);
-    pos = static_cast<int>(token % S);
-    valid = pos < static_cast<int>(min(lengths[b], static_cast<uint32_t>(S)));
-  }
-  half8 lo = {}, hi = {};
-  const size_t base = static_cast<size_t>(row) * D;
-  if (valid) {
-    lo = *reinterpret_cast<const half8*>(x + base + 8 * j);
-    hi = *reinterpret_cast<const half8*>(x + base + HALF + 8 * j);
-  }
-  float a[8], c[8];
-  float ss = 0.0f;
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    a[m] = static_cast<float>(lo[m]);
-    c[m] = static_cast<float>(hi[m]);
-    ss += a[m] * a[m] + c[m] * c[m];
-  }
-#pragma unroll
-  for (int off = T / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-  if (!valid) return;
-  const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+  if (slot >= ppp) return;  // idle threads when lanes_per_pos does not divide 256
+  const int end = min(p0 + block, L);
   const uint4v glo = *reinterpret_cast<const uint4v*>(gamma + 8 * j);
   const uint4v ghi = *reinterpret_cast<const uint4v*>(gamma + HALF + 8 * j);
-  const float* cs = cos_tab + static_cast<size_t>(pos) * HALF + 8 * j;
-  const float* sn = sin_tab + static_cast<size_t>(pos) * HALF + 8 * j;
-  half8 first, second, first_lo, second_lo;
+  // positions handled by this thread: p0 + slot + k * ppp, k = 0.. while < end
+  for (int pos = p0 + slot; pos < end; pos += ppp) {
+    const size_t base = ((static_cast<size_t>(b) * S + pos) * heads + head) * D;
+    const half8 lo = *reinterpret_cast<const half8*>(x + base + 8 * j);
+    const half8 hi = *reinterpret_cast<const half8*>(x + base + HALF + 8 * j);
+    const float* cs = cos_tab + static_cast<size_t>(pos) * HALF + 8 * j;
+    const float* sn = sin_tab + static_cast<size_t>(pos) * HALF + 8 * j;
+    const floatx4 c0 = *reinterpret_cast<const floatx4*>(cs);
+    const floatx4 c1 = *reinterpret_cast<const floatx4*>(cs + 4);
+    const floatx4 s0 = *reinterpret_cast<const floatx4*>(sn);
+    const floatx4 s1 = *reinterpret_cast<const floatx4*>(sn + 4);
+    float a[8], c[8];
+    float ss = 0.0f;
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    const int sh = 16 * (m & 1);
-    const float wl = bf16_to_float(static_cast<uint16_t>((glo[m >> 1] >> sh) & 0xffffu));
-    const float wh = bf16_to_float(static_cast<uint16_t>((ghi[m >> 1] >> sh) & 0xffffu));
-    const float p = a[m] * inv * wl, q = c[m] * inv * wh;
-    const float cv = cs[m], sv = sn[m];
-    const float r0 = p * cv - q * sv, r1 = p * sv + q * cv;
-    first[m] = static_cast<_Float16>(r0);
-    second[m] = static_cast<_Float16>(r1);
-    first_lo[m] = static_cast<_Float16>(r0 - static_cast<float>(first[m]));
-    second_lo[m] = static_cast<_Float16>(r1 - static_cast<float>(second[m]));
-  }
-  *reinterpret_cast<half8*>(y + base + 8 * j) = first;
-  *reinterpret_cast<half8*>(y + base + HALF + 8 * j) = second;
-  if (y_lo) {
-    *reinterpret_cast<half8*>(y_lo + base + 8 * j) = first_lo;
-    *reinterpret_cast<half8*>(y_lo + base + HALF + 8 * j) = second_lo;
+    for (int m = 0; m < 8; ++m) {
+      a[m] = static_cast<float>(lo[m]);
+      c[m] = static_cast<float>(hi[m]);
+      ss += a[m] * a[m] + c[m] * c[m];
+    }
+    // the T lanes of a row are consecutive threads of one wavefront (T divides 64)
+#pragma unroll
+    for (int off = T / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+    half8 first, second, first_lo, second_lo;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int sh = 16 * (m & 1);
+      const float wl = bf16_to_float(static_cast<uint16_t>((glo[m >> 1] >> sh) & 0xffffu));
+      const float wh = bf16_to_float(static_cast<uint16_t>((ghi[m >> 1] >> sh) & 0xffffu));
+      const float p = a[m] * inv * wl, q = c[m] * inv * wh;
+      const float cv = m < 4 ? c0[m] : c1[m - 4], sv = m < 4 ? s0[m] : s1[m - 4];
+      const float r0 = p * cv - q * sv, r1 = p * sv + q * cv;
+      first[m] = static_cast<_Float16>(r0);
+      second[m] = static_cast<_Float16>(r1);
+      first_lo[m] = static_cast<_Float16>(r0 - static_cast<float>(first[m]));
+      second_lo[m] = static_cast<_Float16>(r1 - static_cast<float>(second[m]));
+    }
+    *reinterpret_cast<half8*>(y + base + 8 * j) = first;
+    *reinterpret_cast<half8*>(y + base + HALF + 8 * j) = second;
+    if (y_lo) {
+      *reinterpret_cast<half8*>(y_lo + base + 8 * j) = first_lo;
+      *reinterpret_cast<half8*>(y_lo + base + HALF + 8 * j) = second_lo;
+    }
   }
 }
 
@@ -136,18 +146,20 @@ hipError_t launch_norm_rope_f16(const _Float16* x, _Float16* y, const uint16_t* 
                                 float eps, bool split, hipStream_t st) {
   const int64_t rows = static_cast<int64_t>(B) * S * heads;
   if (!rows) return hipSuccess;
-  const int per_block = 256 / (D / 16);
-  const unsigned grid = static_cast<unsigned>((rows + per_block - 1) / per_block);
+  if ((D / 16) * heads > 256) return hipErrorInvalidValue;  // one position per pass at least
+  // one pass per thread: as many workgroups in flight as there are position blocks
+  const int block = 256 / ((D / 16) * heads);
+  const dim3 grid(static_cast<unsigned>((S + block - 1) / block), static_cast<unsigned>(B));
   _Float16* y_lo = split ? y + static_cast<size_t>(rows) * D : nullptr;
   switch (D) {
     case 32:
-      norm_rope_f16<32><<<grid, 256, 0, st>>>(x, y, gamma, cos_tab, sin_tab, lengths, B, S, heads, eps, y_lo);
+      norm_rope_f16<32><<<grid, 256, 0, st>>>(x, y, gamma, cos_tab, sin_tab, lengths, S, heads, block, eps, y_lo);
       break;
     case 64:
-      norm_rope_f16<64><<<grid, 256, 0, st>>>(x, y, gamma, cos_tab, sin_tab, lengths, B, S, heads, eps, y_lo);
+      norm_rope_f16<64><<<grid, 256, 0, st>>>(x, y, gamma, cos_tab, sin_tab, lengths, S, heads, block, eps, y_lo);
       break;
     case 128:
-      norm_rope_f16<128><<<grid, 256, 0, st>>>(x, y, gamma, cos_tab, sin_tab, lengths, B, S, heads, eps, y_lo);
+      norm_rope_f16<128><<<grid, 256, 0, st>>>(x, y, gamma, cos_tab, sin_tab, lengths, S, heads, block, eps, y_lo);
       break;
     default:
       return hipErrorInvalidValue;
