@@ -447,6 +447,14 @@ __device__ __forceinline__ float pair32(float x, bool take_max) {
   const float a = __uint_as_float(p[0]), b = __uint_as_float(p[1]);
   return take_max ? fmaxf(a, b) : a + b;
 }
+// acc + sum of four fp16 values, exact (v_dot2_f32_f16 against ones)
+__device__ __forceinline__ float dot_ones(half4 p, float acc) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+  acc = __builtin_amdgcn_fdot2(h2{p[0], p[1]}, one, acc, false);
+  return __builtin_amdgcn_fdot2(h2{p[2], p[3]}, one, acc, false);
+}
+
 // reduce over the four lanes r, r+16, r+32, r+48 that hold one query's scores
 __device__ __forceinline__ float rowmax4(float x) { return pair32(pair16(x, true), true); }
 __device__ __forceinline__ float rowsum4(float x) { return pair32(pair16(x, false), false); }
@@ -604,17 +612,18 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
     for (int s = 0; s < NS; ++s)
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
-        x[s][m] = static_cast<float>(qh[s][m]);
-        ss += x[s][m] * x[s][m];
+        const float xf = static_cast<float>(qh[s][m]);
+        ss = fmaf(xf, xf, ss);
       }
     ss = rowsum4(ss);
     const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+    // x = q * (inv * gamma): the fp16 q feeds a mixed-precision fma directly
 #pragma unroll
     for (int s = 0; s < NS; ++s)
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
         const uint16_t w = static_cast<uint16_t>((gw[s][m >> 1] >> (16 * (m & 1))) & 0xffffu);
-        x[s][m] = x[s][m] * inv * bf16_to_float(w);
+        x[s][m] = fmaf(static_cast<float>(qh[s][m]), inv * bf16_to_float(w), 0.0f);
       }
 #pragma unroll
     for (int s = 0; s < NS / 2; ++s)
@@ -634,14 +643,8 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
         ql[s][m] = static_cast<_Float16>(x[s][m] - static_cast<float>(hi));
       }
   }
-  if (!qvalid) {
-#pragma unroll
-    for (int s = 0; s < NS; ++s) qh[s] = half8{};
-    if constexpr (FUSED) {
-#pragma unroll
-      for (int s = 0; s < NS; ++s) ql[s] = half8{};
-    }
-  }
+  // Rows past S read row S - 1 (finite data) and are never stored; query columns do not mix in
+  // either product, so they need no clearing.
 
   floatx4 o[NDT];
 #pragma unroll
@@ -690,21 +693,17 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
       const float mloc = rowmax4(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]))) * scale_log2;
       // lazy running max: moved only when a tile exceeds it by more than kMaxSlack
       const bool grow = mloc > m_run + kMaxSlack;
+      // every row sees key 0 in its first tile (L >= 1), so m_new is finite from tile 0 on
       const float m_new = grow ? mloc : m_run;
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+      const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
       half4 pb;
-      float lsum = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const _Float16 ph =
-            static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(sc[j], scale_log2, -m_use)));
-        pb[j] = ph;
-        lsum += static_cast<float>(ph);
-      }
-      // l_run holds this lane's share of the row sum (its own keys); the four shares of a query
+      for (int j = 0; j < 4; ++j)
+        pb[j] = static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(sc[j], scale_log2, -m_new)));
+      // l_run holds this lane's share of the row sum of the ROUNDED probabilities (the ones the
+      // PV product uses), accumulated exactly with fp16 dot products; the four shares of a query
       // are combined once, after the last tile
-      l_run = l_run * corr + lsum;
+      l_run = dot_ones(pb, l_run * corr);
       m_run = m_new;
       if (__any(grow)) {
 #pragma unroll
@@ -736,20 +735,15 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
       // lazy running max: moved only when a tile exceeds it by more than kMaxSlack
       const bool grow = mloc > m_run + kMaxSlack;
       const float m_new = grow ? mloc : m_run;
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+      const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
       half8 pb;
-      float lsum = 0.0f;
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const _Float16 ph = static_cast<_Float16>(
-              __builtin_amdgcn_exp2f(fmaf(sc[blk][j], scale_log2, -m_use)));
-          pb[4 * blk + j] = ph;
-          lsum += static_cast<float>(ph);
-        }
-      l_run = l_run * corr + lsum;
+        for (int j = 0; j < 4; ++j)
+          pb[4 * blk + j] = static_cast<_Float16>(
+              __builtin_amdgcn_exp2f(fmaf(sc[blk][j], scale_log2, -m_new)));
+      l_run = dot_ones(pb.lo, dot_ones(pb.hi, l_run * corr));
       m_run = m_new;
       if (__any(grow)) {
 #pragma unroll
