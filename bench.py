@@ -1,14 +1,21 @@
-"""Benchmark: Qwen3-shaped causal GQA prefill attention at maximum batch on one MI355X.
+"""Benchmark: tessery's prefill attention path on one MI355X.
 
-Workload qwen3_32x512: B=32 rows, log-uniform valid lengths in [1,512] (seed 4), execution width
-16*ceil(max L/16) = 464, 16 query / 8 KV heads, head dim 128, fp16 operands with fp32
-accumulation, per-head q/k RMSNorm + RoPE fused, 28 layers with independent inputs resident in
-HBM. One step = the 28 layers: per layer one k norm+RoPE launch and one attention launch (q
-norm+RoPE inside), through the C ABI (HipRuntime -> mi_dispatch).
+Default workload qwen3_32x512 (the headline): B=32 rows, log-uniform valid lengths in [1,512]
+(seed 4), execution width 16*ceil(max L/16) = 464, 16 query / 8 KV heads, head dim 128, fp16
+operands with fp32 accumulation, per-head q/k RMSNorm + RoPE fused, 28 layers with independent
+inputs resident in HBM. One step = the 28 layers: per layer one k norm+RoPE launch and one
+attention launch (q norm+RoPE inside), through the C ABI (HipRuntime -> mi_dispatch).
 
-Prints one JSON line: tokens/s (execution tokens B*S*layers per second), mask-exact TFLOP/s and
+It prints one JSON line: tokens/s (execution tokens B*S*layers per second), mask-exact TFLOP/s and
 its fraction of the fp16 MFMA peak, the HBM roofline of the attention kernel from live per-launch
 HIP-event timings, and the float64 NumPy CPU oracle timed on the host on a bounded sample.
+
+--workload selects one of the other measured configurations instead (one JSON line each):
+  qwen3_8x512       B=8, S=512, lengths U{64..512} (seed 3), same fused path, 8 layers
+  bge_32x512        BGE-small fp32 bidirectional attention, B=32, S=512, 12 heads x 32,
+                    lengths U{2..512} (seed 2), 12 layers, route attention_tiled
+  qwen_qkv4_16x256  uint4 QKV projection (x [4096,1024] fp16) -> k norm+RoPE -> fused attention,
+                    lengths U{1..256} (seed 5), 8 layers
 """
 
 from __future__ import annotations
@@ -20,6 +27,7 @@ import os
 import sys
 import time
 from pathlib import Path
+from typing import Any, Callable
 
 import numpy as np
 
@@ -30,6 +38,7 @@ from tessery_amd import HipRuntime, workloads  # noqa: E402
 
 METRIC = "prefill attention tokens/s + TFLOP/s (% MFMA peak), Qwen3 GQA 32x512, 1 GPU"
 PEAK_F16_TFLOPS = 2516.6
+PEAK_F32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 LAYERS = 28
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of the attention kernel on this workload, with the
@@ -40,25 +49,6 @@ KERNEL_SOURCE = ROOT / "tessery_amd" / "csrc" / "attention.hip"
 
 def log(message: str) -> None:
     print(message, file=sys.stderr, flush=True)
-
-
-def upload_layers(rt: HipRuntime, shape: workloads.Shape, layers: int):
-    sets = []
-    for layer in range(layers):
-        t = workloads.qwen_layer(shape, layer, seed=4)
-        sets.append(
-            {
-                "q": rt.upload(t["q"]),
-                "k": rt.upload(t["k"]),
-                "v": rt.upload(t["v"]),
-                "q_norm": rt.upload(t["q_norm"]),
-                "k_norm": rt.upload(t["k_norm"]),
-                "out": rt.buffer(t["q"].size * 4),
-            }
-        )
-        if layer == 0:
-            host0 = t
-    return sets, host0
 
 
 def measured_traffic() -> int | None:
@@ -83,31 +73,96 @@ def measured_traffic() -> int | None:
     return int(round((fetch + write) * 1024))
 
 
-def encode_step(rt, shape, sets, lengths_buf, k_work):
-    for s in sets:
-        rt._attention_norm_rope(
-            [s["q"], s["k"], s["v"], lengths_buf, s["out"], s["q_norm"], s["k_norm"], k_work],
-            tokens=shape.tokens,
-            seq=shape.seq,
-            heads=shape.heads,
-            kv_heads=shape.kv_heads,
-            dim=shape.dim,
-            eps=workloads.EPS,
-            theta=workloads.THETA,
-            out_dtype="f32",
-        )
-
-
-def cpu_baseline(shape, lengths, host0, budget_s: float = 12.0):
-    """float64 NumPy oracle (norm+RoPE on q and k, attention) on layer 0, all 32 rows."""
-    from oracle import attention, norm_rope
-
+def blas_threads() -> int:
     try:
         from threadpoolctl import threadpool_info
 
-        blas_threads = max((i.get("num_threads", 0) for i in threadpool_info()), default=0)
+        return max((i.get("num_threads", 0) for i in threadpool_info()), default=0)
     except Exception:  # threadpoolctl missing: report unknown
-        blas_threads = 0
+        return 0
+
+
+def time_cpu(layer: Callable[[], Any], budget_s: float = 12.0) -> tuple[Any, float, int]:
+    """Run `layer` once as warmup (its result is returned as the parity reference), then time up
+    to 5 more runs within budget_s; returns (result, median seconds, runs timed)."""
+    start = time.perf_counter()
+    expected = layer()
+    times = [time.perf_counter() - start]
+    while sum(times) < budget_s and len(times) < 6:
+        t0 = time.perf_counter()
+        layer()
+        times.append(time.perf_counter() - t0)
+    return expected, float(np.median(times[1:] if len(times) > 1 else times)), max(1, len(times) - 1)
+
+
+def run_timed(rt: HipRuntime, step: Callable[[], None], steps: int, warmup: int,
+              launches_per_step: int) -> dict[str, Any]:
+    """Warmup, then K steps launched back to back inside one command (synchronized before and
+    after), then the same steps replayed with HIP events around every launch on the runtime
+    stream (a command profiles at most 2048 launches). Returns wall seconds per step, event
+    seconds per step and the per-kernel mean launch durations."""
+    for _ in range(warmup):
+        with rt.command():
+            step()
+    with rt.command():
+        for _ in range(steps):
+            step()
+        launched = time.perf_counter()
+    wall = time.perf_counter() - launched
+    gpu = rt.last_gpu_seconds
+    log(f"timed {steps} steps: wall {wall * 1e3:.3f} ms, events {gpu * 1e3:.3f} ms")
+    prof_steps = max(1, min(steps, 2048 // launches_per_step))
+    with rt.profile_kernels() as records:
+        with rt.command():
+            for _ in range(prof_steps):
+                step()
+    kernels: dict[str, list[float]] = {}
+    for r in records:
+        kernels.setdefault(r["kernel"], []).append(r["gpu_seconds"])
+    return {
+        "step": wall / steps,
+        "gpu_step": gpu / steps if gpu >= 0 else None,
+        "kernel_s": {k: float(np.mean(v)) for k, v in kernels.items()},
+    }
+
+
+def upload_qwen_layers(rt: HipRuntime, shape: workloads.Shape, layers: int, seed: int):
+    sets = []
+    for layer in range(layers):
+        t = workloads.qwen_layer(shape, layer, seed=seed)
+        sets.append(
+            {
+                "q": rt.upload(t["q"]),
+                "k": rt.upload(t["k"]),
+                "v": rt.upload(t["v"]),
+                "q_norm": rt.upload(t["q_norm"]),
+                "k_norm": rt.upload(t["k_norm"]),
+                "out": rt.buffer(t["q"].size * 4),
+            }
+        )
+        if layer == 0:
+            host0 = t
+    return sets, host0
+
+
+def fused_attention(rt, shape, s, lengths_buf, k_work):
+    rt._attention_norm_rope(
+        [s["q"], s["k"], s["v"], lengths_buf, s["out"], s["q_norm"], s["k_norm"], k_work],
+        tokens=shape.tokens,
+        seq=shape.seq,
+        heads=shape.heads,
+        kv_heads=shape.kv_heads,
+        dim=shape.dim,
+        eps=workloads.EPS,
+        theta=workloads.THETA,
+        out_dtype="f32",
+    )
+
+
+def qwen_cpu_layer(shape, lengths, host0):
+    """float64 NumPy oracle of one layer: q/k norm + RoPE, then attention."""
+    from oracle import attention, norm_rope
+
     qn = workloads.bf16_values(host0["q_norm"]).astype(np.float64)
     kn = workloads.bf16_values(host0["k_norm"]).astype(np.float64)
 
@@ -116,32 +171,256 @@ def cpu_baseline(shape, lengths, host0, budget_s: float = 12.0):
         k = norm_rope.norm_rope(host0["k"], kn, workloads.EPS, workloads.THETA)
         return attention.attention(q, k, host0["v"], lengths, bidirectional=False)
 
-    start = time.perf_counter()
-    expected = layer()  # warmup, also the parity reference
-    times = [time.perf_counter() - start]
-    while sum(times) < budget_s and len(times) < 6:
-        t0 = time.perf_counter()
-        layer()
-        times.append(time.perf_counter() - t0)
-    per_layer = float(np.median(times[1:] if len(times) > 1 else times))
-    return expected, {
+    return layer
+
+
+def cpu_baseline_line(shape, per_layer: float, runs: int, layers: int, what: str) -> dict:
+    return {
         "value": shape.tokens / per_layer,
         "unit": "tokens/s",
         "cores": len(os.sched_getaffinity(0)),
-        "blas_threads": blas_threads,
+        "blas_threads": blas_threads(),
         "kind": "port",
-        "sample": f"1 of {LAYERS} layers (all {shape.batch} rows, S={shape.seq}), float64 NumPy "
-        f"oracle incl. q/k norm+RoPE, median of {max(1, len(times) - 1)} runs; "
-        f"{per_layer * 1e3:.1f} ms/layer",
+        "sample": f"1 of {layers} layers (all {shape.batch} rows, S={shape.seq}), float64 NumPy "
+        f"oracle{what}, median of {runs} runs; {per_layer * 1e3:.1f} ms/layer",
+    }
+
+
+def bench_qwen(args, name: str, shape, lengths, seed: int, layers: int, lengths_text: str,
+               headline: bool) -> dict:
+    flop = workloads.attention_flop(shape, lengths)
+    nbytes = workloads.attention_bytes(shape, lengths, 2, 4)
+    log(f"workload {name}: B={shape.batch} S={shape.seq} sumL={int(lengths.sum())} "
+        f"layers={layers}; generating inputs")
+    with HipRuntime() as rt:
+        sets, host0 = upload_qwen_layers(rt, shape, layers, seed)
+        lengths_buf = rt.upload(lengths)
+        k_work = rt.buffer(2 * host0["k"].nbytes)
+        if args.calibrate_copy_mib:
+            size = args.calibrate_copy_mib << 20
+            src, dst = rt.buffer(size), rt.buffer(size)
+            with rt.command():
+                rt._dispatch("copy", [src, dst], threads=size, group_size=256)
+            src.close()
+            dst.close()
+        log("inputs resident; warmup")
+
+        def step():
+            for s in sets:
+                fused_attention(rt, shape, s, lengths_buf, k_work)
+
+        t = run_timed(rt, step, args.steps, args.warmup, 2 * layers)
+        out0 = rt.read(sets[0]["out"], host0["q"].shape)
+
+    step_s = t["step"]
+    attn_avg = t["kernel_s"]["attention_f16_norm_rope"]
+    achieved = nbytes / attn_avg / 1e9
+    tflops = flop * layers / step_s / 1e12
+    result = {
+        "metric": METRIC if headline else f"prefill attention tokens/s, Qwen3 GQA {name}, 1 GPU",
+        "value": shape.tokens * layers / step_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_s * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{name} causal GQA prefill, fused q/k RMSNorm+RoPE",
+            "batch": shape.batch,
+            "seq": shape.seq,
+            "heads": shape.heads,
+            "kv_heads": shape.kv_heads,
+            "dim": shape.dim,
+            "layers": layers,
+            "valid_tokens": int(lengths.sum()),
+            "lengths": lengths_text,
+            "out_dtype": "f32",
+        },
+        "valid_tokens_per_s": int(lengths.sum()) * layers / step_s,
+        "tflops": tflops,
+        "mfma_frac": tflops / PEAK_F16_TFLOPS,
+        "dense_convention_tflops": workloads.dense_flop(shape) * layers / step_s / 1e12,
+        "gpu_event_ms_per_step": t["gpu_step"] * 1e3 if t["gpu_step"] is not None else None,
+        "kernel_us": {"attention_f16_norm_rope": attn_avg * 1e6,
+                      "norm_rope_f16": t["kernel_s"]["norm_rope_f16"] * 1e6},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": achieved / PEAK_HBM_GBS,
+            "traffic": measured_traffic() if headline else None,
+            "algorithmic_bytes": nbytes,
+            "kernel": "attention_f16_norm_rope",
+            "mfma_tflops": flop / attn_avg / 1e12,
+        },
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        expected, per_layer, runs = time_cpu(qwen_cpu_layer(shape, lengths, host0))
+        result["cpu_baseline"] = cpu_baseline_line(shape, per_layer, runs, layers,
+                                                   " incl. q/k norm+RoPE")
+        result["max_abs_err_layer0"] = float(np.max(np.abs(out0.astype(np.float64) - expected)))
+    else:
+        result["cpu_baseline"] = None
+    return result
+
+
+def bench_bge(args) -> dict:
+    """BGE-small fp32 bidirectional attention (route attention_tiled), 12 layers."""
+    layers = 12
+    shape, lengths = workloads.bge_small_32x512()
+    flop = workloads.attention_flop(shape, lengths)
+    nbytes = workloads.attention_bytes(shape, lengths, 4, 4)
+    log(f"workload bge_32x512: B={shape.batch} S={shape.seq} sumL={int(lengths.sum())}")
+    with HipRuntime() as rt:
+        host = [workloads.bge_layer(shape, layer) for layer in range(layers)]
+        sets = [{k: rt.upload(v) for k, v in t.items()} for t in host]
+        for s in sets:
+            s["out"] = rt.buffer(shape.tokens * shape.heads * shape.dim * 4)
+        lengths_buf = rt.upload(lengths)
+
+        def step():
+            for s in sets:
+                rt._attention([s["q"], s["k"], s["v"], lengths_buf, s["out"]], tokens=shape.tokens,
+                              seq=shape.seq, heads=shape.heads, kv_heads=shape.kv_heads,
+                              dim=shape.dim, bidirectional=1)
+
+        t = run_timed(rt, step, args.steps, args.warmup, layers)
+        out0 = rt.read(sets[0]["out"], host[0]["q"].shape)
+    step_s = t["step"]
+    (kernel, avg), = t["kernel_s"].items()
+    tflops_kernel = flop / avg / 1e12
+    result = {
+        "metric": "BGE-small encoder attention tokens/s + TFLOP/s (% fp32 MFMA peak), 32x512, 1 GPU",
+        "value": shape.tokens * layers / step_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_s * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "bge_32x512 bidirectional attention, key-padding mask",
+                   "batch": shape.batch, "seq": shape.seq, "heads": shape.heads,
+                   "dim": shape.dim, "layers": layers, "valid_tokens": int(lengths.sum()),
+                   "lengths": "uniform [2,512], seed 2"},
+        "tflops": flop * layers / step_s / 1e12,
+        "kernel_us": {kernel: avg * 1e6},
+        "roofline": {
+            "bound": "mfma",
+            "achieved": tflops_kernel,
+            "peak": PEAK_F32_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": tflops_kernel / PEAK_F32_TFLOPS,
+            "traffic": None,
+            "algorithmic_flop": flop,
+            "algorithmic_bytes": nbytes,
+            "hbm_gbs": nbytes / avg / 1e9,
+            "kernel": kernel,
+        },
+    }
+    if not args.no_cpu_baseline:
+        from oracle import attention
+
+        def layer():
+            return attention.attention(host[0]["q"], host[0]["k"], host[0]["v"], lengths,
+                                       bidirectional=True)
+
+        expected, per_layer, runs = time_cpu(layer)
+        result["cpu_baseline"] = cpu_baseline_line(shape, per_layer, runs, layers, "")
+        result["max_abs_err_layer0"] = float(np.max(np.abs(out0.astype(np.float64) - expected)))
+    else:
+        result["cpu_baseline"] = None
+    return result
+
+
+def bench_qkv4_block(args) -> dict:
+    """uint4 QKV projection -> k norm+RoPE -> fused attention, 8 independent layers."""
+    layers = 8
+    shape, lengths, d = workloads.qwen_qkv4_16x256()
+    m, k_in = d["x"].shape
+    nq, nkv = shape.heads * shape.dim, shape.kv_heads * shape.dim
+    n_total = nq + 2 * nkv
+    gemm_flop = workloads.qkv4_flop(m, k_in, n_total)
+    gemm_bytes = workloads.qkv4_bytes(m, k_in, n_total)
+    attn_flop = workloads.attention_flop(shape, lengths)
+    log(f"workload qwen_qkv4_16x256: M={m} K={k_in} N={n_total} sumL={int(lengths.sum())}")
+    with HipRuntime() as rt:
+        common = {name: rt.upload(d[name]) for name in ("w", "s", "b", "q_norm", "k_norm")}
+        lengths_buf = rt.upload(lengths)
+        k_work = rt.buffer(2 * m * nkv * 2)
+        rng = np.random.default_rng((5, 1))
+        sets = []
+        for _ in range(layers):
+            x = rt.upload(rng.standard_normal((m, k_in), dtype=np.float32).astype(np.float16))
+            sets.append({"x": x, "yq": rt.buffer(m * nq * 2), "yk": rt.buffer(m * nkv * 2),
+                         "yv": rt.buffer(m * nkv * 2), "out": rt.buffer(m * nq * 4)})
+
+        def step():
+            for s in sets:
+                rt._qkv4([s["x"], common["w"], common["s"], common["b"], s["yq"], s["yk"],
+                          s["yv"]], rows=m, k=k_in, q_cols=nq, kv_cols=nkv, scale_dtype="f16")
+                rt._attention_norm_rope(
+                    [s["yq"], s["yk"], s["yv"], lengths_buf, s["out"], common["q_norm"],
+                     common["k_norm"], k_work], tokens=m, seq=shape.seq, heads=shape.heads,
+                    kv_heads=shape.kv_heads, dim=shape.dim, eps=workloads.EPS,
+                    theta=workloads.THETA)
+
+        t = run_timed(rt, step, args.steps, args.warmup, 3 * layers)
+    step_s = t["step"]
+    ks = t["kernel_s"]
+    gemm = ks["qkv4_f16"]
+    return {
+        "metric": "Qwen3 uint4 QKV projection + fused attention tokens/s, 16x256, 1 GPU",
+        "value": m * layers / step_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_s * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "qwen_qkv4_16x256: qkv4 -> k norm+RoPE -> fused attention",
+                   "rows": m, "k": k_in, "n": n_total, "layers": layers,
+                   "valid_tokens": int(lengths.sum()), "lengths": "uniform [1,256], seed 5"},
+        "kernel_us": {k: v * 1e6 for k, v in ks.items()},
+        "roofline": {
+            "bound": "mfma",
+            "achieved": gemm_flop / gemm / 1e12,
+            "peak": PEAK_F16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": gemm_flop / gemm / 1e12 / PEAK_F16_TFLOPS,
+            "traffic": None,
+            "algorithmic_flop": gemm_flop,
+            "algorithmic_bytes": gemm_bytes,
+            "kernel": "qkv4_f16",
+        },
+        "attention_tflops": attn_flop / ks["attention_f16_norm_rope"] / 1e12,
+        "cpu_baseline": None,
     }
 
 
 def main() -> int:
-    parser = argparse.ArgumentParser(description=__doc__)
+    parser = argparse.ArgumentParser(description=__doc__,
+                                     formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--layers", type=int, default=LAYERS)
+    parser.add_argument("--layers", type=int, default=LAYERS, help="headline workload only")
+    parser.add_argument("--workload", default="qwen3_32x512",
+                        choices=["qwen3_32x512", "qwen3_8x512", "bge_32x512", "qwen_qkv4_16x256"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="also launch one copy of this many MiB (traffic-counter calibration)")
@@ -154,102 +433,18 @@ def main() -> int:
     if args.steps < 1 or args.warmup < 0 or not 1 <= args.layers <= LAYERS:
         parser.error("invalid steps / warmup / layers")
 
-    shape, lengths = workloads.qwen3_32x512()
-    flop = workloads.attention_flop(shape, lengths)
-    nbytes = workloads.attention_bytes(shape, lengths, 2, 4)
-    log(f"workload qwen3_32x512: B={shape.batch} S={shape.seq} sumL={int(lengths.sum())} "
-        f"layers={args.layers}; generating inputs")
-    with HipRuntime() as rt:
-        sets, host0 = upload_layers(rt, shape, args.layers)
-        lengths_buf = rt.upload(lengths)
-        k_work = rt.buffer(2 * host0["k"].nbytes)
-        if args.calibrate_copy_mib:
-            size = args.calibrate_copy_mib << 20
-            src, dst = rt.buffer(size), rt.buffer(size)
-            with rt.command():
-                rt._dispatch("copy", [src, dst], threads=size, group_size=256)
-            src.close()
-            dst.close()
-        log("inputs resident; warmup")
-        for _ in range(args.warmup):
-            with rt.command():
-                encode_step(rt, shape, sets, lengths_buf, k_work)
-        # timed region: K steps launched back to back; synchronized before and after
-        with rt.command():
-            for _ in range(args.steps):
-                encode_step(rt, shape, sets, lengths_buf, k_work)
-            launched = time.perf_counter()
-        wall = time.perf_counter() - launched
-        gpu = rt.last_gpu_seconds
-        log(f"timed {args.steps} steps: wall {wall * 1e3:.3f} ms, events {gpu * 1e3:.3f} ms")
-        # per-launch durations: HIP events recorded around every launch on the runtime stream,
-        # over the same steps replayed once more (a command profiles at most 2048 launches)
-        prof_steps = max(1, min(args.steps, 2048 // (2 * args.layers)))
-        with rt.profile_kernels() as records:
-            with rt.command():
-                for _ in range(prof_steps):
-                    encode_step(rt, shape, sets, lengths_buf, k_work)
-        attn = [r["gpu_seconds"] for r in records if r["kernel"] == "attention_f16_norm_rope"]
-        prologue = [r["gpu_seconds"] for r in records if r["kernel"] == "norm_rope_f16"]
-        out0 = rt.read(sets[0]["out"], host0["q"].shape)
-
-    step = wall / args.steps
-    tokens = shape.tokens * args.layers
-    attn_avg = float(np.mean(attn))
-    achieved = nbytes / attn_avg / 1e9
-    traffic = measured_traffic()
-    tflops = flop * args.layers / step / 1e12
-    result = {
-        "metric": METRIC,
-        "value": tokens / step,
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": step * 1e3,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f16",
-        "data": "synthetic",
-        "config": {
-            "workload": "qwen3_32x512 causal GQA prefill, fused q/k RMSNorm+RoPE",
-            "batch": shape.batch,
-            "seq": shape.seq,
-            "heads": shape.heads,
-            "kv_heads": shape.kv_heads,
-            "dim": shape.dim,
-            "layers": args.layers,
-            "valid_tokens": int(lengths.sum()),
-            "lengths": "log-uniform [1,512], seed 4",
-            "out_dtype": "f32",
-        },
-        "valid_tokens_per_s": int(lengths.sum()) * args.layers / step,
-        "tflops": tflops,
-        "mfma_frac": tflops / PEAK_F16_TFLOPS,
-        "dense_convention_tflops": workloads.dense_flop(shape) * args.layers / step / 1e12,
-        "gpu_event_ms_per_step": gpu / args.steps * 1e3 if gpu >= 0 else None,
-        "kernel_us": {"attention_f16_norm_rope": attn_avg * 1e6,
-                      "norm_rope_f16": float(np.mean(prologue)) * 1e6},
-        "roofline": {
-            "bound": "hbm",
-            "achieved": achieved,
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": achieved / PEAK_HBM_GBS,
-            "traffic": traffic,
-            "algorithmic_bytes": nbytes,
-            "kernel": "attention_f16_norm_rope",
-            "mfma_tflops": flop / attn_avg / 1e12,
-        },
-    }
-    if not args.no_cpu_baseline:
-        log("cpu baseline")
-        expected, baseline = cpu_baseline(shape, lengths, host0)
-        result["cpu_baseline"] = baseline
-        result["max_abs_err_layer0"] = float(np.max(np.abs(out0.astype(np.float64) - expected)))
+    if args.workload == "qwen3_32x512":
+        shape, lengths = workloads.qwen3_32x512()
+        result = bench_qwen(args, "qwen3_32x512", shape, lengths, 4, args.layers,
+                            "log-uniform [1,512], seed 4", headline=True)
+    elif args.workload == "qwen3_8x512":
+        shape, lengths = workloads.qwen3_8x512()
+        result = bench_qwen(args, "qwen3_8x512", shape, lengths, 3, 8, "uniform [64,512], seed 3",
+                            headline=False)
+    elif args.workload == "bge_32x512":
+        result = bench_bge(args)
     else:
-        result["cpu_baseline"] = None
+        result = bench_qkv4_block(args)
     print(json.dumps(result), flush=True)
     return 0
 

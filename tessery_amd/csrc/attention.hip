@@ -320,30 +320,8 @@ __global__ __launch_bounds__(256, 2) void attn_f32_mfma(const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------------------------
-// fp16 MFMA kernel, 16 query rows per wavefront. v_mfma_f32_16x16x32_f16: lane l (r = l%16,
-// g = l/16) supplies A[r][8g..8g+7] and B[8g..8g+7][r] (8 halves each) and holds
-// D[4g+j][r] in acc[j].
-//   S^T = K * Q^T per 16-key block, k-step s covers channels 32s..32s+31: lane (r, g) owns the
-//   scores of query r for keys 4g+j of each block; the row max / sum of a query reduces over the
-//   four lanes r, r+16, r+32, r+48.
-//   The 32-key tile is stored in LDS with key p at row R(p) = 16*((p>>2)&1) + 4*(p>>3) + (p&3),
-//   so the lane's eight probabilities (two blocks x four) are the CONSECUTIVE keys 8g..8g+7 and
-//   form the B operand of O^T = V^T * P^T directly; its A operand is one 16-byte read of the
-//   transposed V tile (V^T: [channel][key] in LDS).
-//   O^T accumulates per 16-channel block: lane (r, g) holds channels 16*dt + 4g + j of query r.
-// Small register footprint (~100 VGPRs at D=128) keeps four wavefronts per SIMD resident, so
-// the streaming of Q in and O out overlaps other wavefronts' MFMA and softmax work.
-//
-// FUSED (route attention_f16_norm_rope): Q arrives pre-norm and is RMS-normalized and rotated in
-// fp32 as it is loaded; K arrives already normalized and rotated as two fp16 planes hi + lo
-// (written by norm_rope_f16). Q is also carried as hi + lo, and the score tile accumulates
-// K_hi*Q_lo + K_lo*Q_hi + K_hi*Q_hi in fp32, so the normalized q and k enter the dot products at
-// ~22-bit precision instead of fp16's 11 bits.
-// All global loads are branch-free: out-of-range rows read a clamped in-bounds address and are
-// replaced by zero, so every load of a phase issues back to back.
+// fp16 MFMA kernel: geometry and helpers (the kernel and its layout notes follow further down).
 // ---------------------------------------------------------------------------------------------
-typedef _Float16 half8x __attribute__((ext_vector_type(8)));
-
 struct Geom16 {
   int b, kvh, head0, p0, L, wave_end, wg_end, limit_min, hsh;
   bool active;
@@ -521,7 +499,8 @@ struct F16Ring {
 // FUSED (route attention_f16_norm_rope): Q arrives pre-norm and is RMS-normalized and rotated in
 // fp32 as it is loaded; K arrives normalized and rotated as two fp16 planes hi + lo (written by
 // norm_rope_f16). Q is also carried as hi + lo, and the scores accumulate
-// K_hi*Q_lo + K_lo*Q_hi + K_hi*Q_hi in fp32: q and k enter the dot products at ~22 bits.
+// K_hi*Q_lo + K_lo*Q_hi + K_hi*Q_hi in fp32: q and k enter the dot products at ~22 bits. P is
+// split the same way (P_hi*V + P_lo*V), so the only fp16 roundings left are those of the inputs.
 // ---------------------------------------------------------------------------------------------
 // The running max of a row moves only when a tile's max exceeds it by more than kMaxSlack (in
 // log2 units). Probabilities are then at most 2^kMaxSlack = 256, exact in range for fp16 P and
@@ -696,14 +675,28 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
       // every row sees key 0 in its first tile (L >= 1), so m_new is finite from tile 0 on
       const float m_new = grow ? mloc : m_run;
       const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
-      half4 pb;
+      half4 pb, pl;
+      if constexpr (FUSED) {
+        // P as hi + lo fp16 pair: the PV product sees P to ~22 bits, and the row sum is the
+        // fp32 sum of the same values
+        float pf[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        pb[j] = static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(sc[j], scale_log2, -m_new)));
-      // l_run holds this lane's share of the row sum of the ROUNDED probabilities (the ones the
-      // PV product uses), accumulated exactly with fp16 dot products; the four shares of a query
+        for (int j = 0; j < 4; ++j) {
+          pf[j] = __builtin_amdgcn_exp2f(fmaf(sc[j], scale_log2, -m_new));
+          pb[j] = static_cast<_Float16>(pf[j]);
+          pl[j] = static_cast<_Float16>(pf[j] - static_cast<float>(pb[j]));
+        }
+        l_run = fmaf(l_run, corr, (pf[0] + pf[1]) + (pf[2] + pf[3]));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          pb[j] = static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(sc[j], scale_log2, -m_new)));
+        // the row sum of the ROUNDED probabilities (the ones the PV product uses), accumulated
+        // exactly with fp16 dot products
+        l_run = dot_ones(pb, l_run * corr);
+      }
+      // l_run holds this lane's share of the row sum (its own keys); the four shares of a query
       // are combined once, after the last tile
-      l_run = dot_ones(pb, l_run * corr);
       m_run = m_new;
       if (__any(grow)) {
 #pragma unroll
@@ -716,6 +709,7 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
         const int chunk = (2 * dt + ((r & 3) >> 1)) ^ (2 * (vrow & 7));
         const half4 a = lds_read_tr(vst + vrow * D + 8 * chunk + 4 * (r & 1));
         o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, o[dt], 0, 0, 0);
+        if constexpr (FUSED) o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pl, o[dt], 0, 0, 0);
       }
     } else {
       floatx4 sc[2];
@@ -736,14 +730,29 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
       const bool grow = mloc > m_run + kMaxSlack;
       const float m_new = grow ? mloc : m_run;
       const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
-      half8 pb;
+      half8 pb, pl;
+      if constexpr (FUSED) {
+        float pf[8];
 #pragma unroll
-      for (int blk = 0; blk < 2; ++blk)
+        for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          pb[4 * blk + j] = static_cast<_Float16>(
-              __builtin_amdgcn_exp2f(fmaf(sc[blk][j], scale_log2, -m_new)));
-      l_run = dot_ones(pb.lo, dot_ones(pb.hi, l_run * corr));
+          for (int j = 0; j < 4; ++j) {
+            const int e = 4 * blk + j;
+            pf[e] = __builtin_amdgcn_exp2f(fmaf(sc[blk][j], scale_log2, -m_new));
+            pb[e] = static_cast<_Float16>(pf[e]);
+            pl[e] = static_cast<_Float16>(pf[e] - static_cast<float>(pb[e]));
+          }
+        l_run = fmaf(l_run, corr,
+                     ((pf[0] + pf[1]) + (pf[2] + pf[3])) + ((pf[4] + pf[5]) + (pf[6] + pf[7])));
+      } else {
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            pb[4 * blk + j] = static_cast<_Float16>(
+                __builtin_amdgcn_exp2f(fmaf(sc[blk][j], scale_log2, -m_new)));
+        l_run = dot_ones(pb.lo, dot_ones(pb.hi, l_run * corr));
+      }
       m_run = m_new;
       if (__any(grow)) {
 #pragma unroll
@@ -764,6 +773,7 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
           a[4 * h + 3] = t[3];
         }
         o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, o[dt], 0, 0, 0);
+        if constexpr (FUSED) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl, o[dt], 0, 0, 0);
       }
     }
   }

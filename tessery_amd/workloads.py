@@ -112,6 +112,38 @@ def qwen_layer(shape: Shape, layer: int, seed: int) -> dict[str, NDArray]:
     return {"q": q, "k": k, "v": v, "q_norm": gq, "k_norm": gk}
 
 
+def qwen_qkv4_16x256(seed: int = 5) -> tuple[Shape, NDArray[np.uint32], dict[str, NDArray]]:
+    """uint4 QKV projection feeding causal GQA: x [16*256, 1024] fp16 ~ N(0,1); W_q 1024->2048 and
+    W_k, W_v 1024->1024 as weight4 words with codes U{0..15} and group-64 fp16 scale / bias
+    ~ N(0, 0.02), concatenated q|k|v along N; lengths U{1..256}; q/k norm weights U(0.5,1.5)."""
+    shape = Shape(16, 256, 16, 8, 128, causal=True)
+    lengths = lengths_uniform(seed, shape.batch, 1, shape.seq)
+    rng = np.random.default_rng((seed, 0))
+    k_in = 1024
+    x = normal(rng, (shape.tokens, k_in), np.float16)
+    n_total = (shape.heads + 2 * shape.kv_heads) * shape.dim
+    codes = rng.integers(0, 16, size=(n_total, k_in), dtype=np.uint32)
+    packed = np.zeros((n_total, k_in // 8), dtype=np.uint32)
+    for j in range(8):
+        packed |= codes[:, j::8] << np.uint32(4 * j)
+    scales = rng.normal(0.0, 0.02, size=(n_total, k_in // 64)).astype(np.float16).view(np.uint16)
+    biases = rng.normal(0.0, 0.02, size=(n_total, k_in // 64)).astype(np.float16).view(np.uint16)
+    gq = bf16_words(rng.uniform(0.5, 1.5, shape.dim))
+    gk = bf16_words(rng.uniform(0.5, 1.5, shape.dim))
+    return shape, lengths, {"x": x, "w": packed, "s": scales, "b": biases,
+                            "q_norm": gq, "k_norm": gk}
+
+
+def qkv4_flop(rows: int, k: int, n_total: int) -> int:
+    """2*M*K*N of the three projections."""
+    return 2 * rows * k * n_total
+
+
+def qkv4_bytes(rows: int, k: int, n_total: int) -> int:
+    """x fp16 in, packed codes + fp16 scale/bias in, q/k/v fp16 out."""
+    return rows * k * 2 + n_total * k // 2 + 2 * n_total * (k // 64) * 2 + rows * n_total * 2
+
+
 # ---- algorithmic work (per layer) ----------------------------------------------------------
 
 
