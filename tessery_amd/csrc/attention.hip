@@ -24,6 +24,7 @@
 // one KV head, so each K/V tile staged in LDS serves every query head of a GQA group.
 #include "common.h"
 #include "kernels.h"
+#include "lds_dma.h"
 
 #include <math.h>
 
@@ -382,7 +383,6 @@ __device__ __forceinline__ int tile_key(int row) {  // inverse of tile_row
 }
 
 typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // 8 bytes of a row-major V tile, transposed across each 16-lane group (ds_read_b64_tr_b16):
 // result lane i, element j = element (i % 4) of the 4 halves addressed by lane 4j + i/4.
@@ -390,26 +390,6 @@ __device__ __forceinline__ half4 lds_read_tr(const _Float16* p) {
   const fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
       (__attribute__((address_space(3))) fp16x4_t*)(p));
   return __builtin_bit_cast(half4, v);
-}
-
-// 16 bytes per lane, global -> LDS (global_load_lds_dwordx4): lane l's bytes land at the
-// wave-uniform LDS address + 16*l. Issued as inline asm so the compiler's wait insertion does not
-// treat the in-flight DMA as aliasing every later LDS read (it would wait for the whole ring);
-// completion is awaited explicitly with wait_vmcnt before the consuming barrier.
-__device__ __forceinline__ void dma16(const void* src, _Float16* lds) {
-  const unsigned addr = __builtin_amdgcn_readfirstlane(
-      static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_ptr_t)(lds))));
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(src), "s"(addr)
-               : "memory", "m0");
-}
-
-// s_waitcnt vmcnt(n), leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
 // Cross-row reductions with gfx950's VALU lane swaps: permlane16_swap(x, x) yields
@@ -436,17 +416,6 @@ __device__ __forceinline__ float dot_ones(half4 p, float acc) {
 // reduce over the four lanes r, r+16, r+32, r+48 that hold one query's scores
 __device__ __forceinline__ float rowmax4(float x) { return pair32(pair16(x, true), true); }
 __device__ __forceinline__ float rowsum4(float x) { return pair32(pair16(x, false), false); }
-
-// Workgroup barrier without a memory fence. Each wavefront has already waited (vmcnt) for its
-// own DMA writes into the stage it is about to release, so after s_barrier every wavefront's
-// tile data is in LDS; the asm clobbers keep the compiler from moving LDS accesses across.
-// (__syncthreads() would add a release fence that waits for ALL outstanding DMA, including the
-// tiles still being prefetched.)
-__device__ __forceinline__ void stage_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 
 // K/V ring geometry. A tile holds KT = 2048 / D keys, so every plane tile (K hi, K lo when fused,
 // V) is 4 KiB: four 1 KiB DMA blocks, one per wavefront. D = 128 runs 16-key tiles, D = 64 runs

@@ -1,0 +1,42 @@
+// LDS DMA helpers for gfx950 kernels that stage tiles with global_load_lds_dwordx4.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tessery {
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 16 bytes per lane, global -> LDS (global_load_lds_dwordx4): lane l's bytes land at the
+// wave-uniform LDS address + 16*l. Issued as inline asm so the compiler's wait insertion does not
+// treat the in-flight DMA as aliasing every later LDS read (it would wait for the whole ring);
+// completion is awaited explicitly with wait_vmcnt before the consuming barrier.
+__device__ __forceinline__ void dma16(const void* src, _Float16* lds) {
+  const unsigned addr = __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_ptr_t)(lds))));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(addr)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(n), leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier without a memory fence. Each wavefront has already waited (vmcnt) for its
+// own DMA writes into the stage it is about to release, so after s_barrier every wavefront's
+// tile data is in LDS; the asm clobbers keep the compiler from moving LDS accesses across.
+// (__syncthreads() would add a release fence that waits for ALL outstanding DMA, including the
+// tiles still being prefetched.)
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+}  // namespace tessery

@@ -13,26 +13,37 @@
 // accumulation is the final fp16 store of y.
 //
 // Tiling: 256 threads = 4 wavefronts in a 2x2 grid; workgroup tile 128 rows x 128 columns,
-// wavefront tile 64 x 64 = 2x2 MFMA tiles of 32x32 (v_mfma_f32_32x32x16_f16). The x tile of a
-// group (128 x 64 fp16) is staged in LDS; each lane decodes its weight words straight from
-// global memory into B operands. MFMA k-step s, lane half h covers columns 32h + 8s .. +7 of the
-// group, so one 16-byte load brings a lane's four words of a group. A word decodes into halves
-// (c0,c4),(c1,c5),(c2,c6),(c3,c7) with two integer ops per pair (0x6400 | c is 1024 + c in fp16,
-// then 1024 is subtracted exactly); the staged x chunk is stored in the same interleaved order.
+// wavefront tile 64 x 64 = 2x2 MFMA tiles of 32x32 (v_mfma_f32_32x32x16_f16). MFMA k-step s, lane
+// half h covers columns 32h + 8s .. +7 of the group, so one 16-byte load brings a lane's four
+// weight words of a group, and a word decodes into its eight codes in natural order.
+// Pipeline over the K/64 groups: the x tile of group g + 1 (128 x 64 fp16) is copied into the
+// second of two LDS stages by global_load_lds_dwordx4 and the next weight words, scales and biases
+// are loaded into registers, while group g runs. X_g comes from the MFMA too (x times a ones
+// matrix), so the VALU only decodes codes and folds the group into the accumulator.
+// x rows are XOR-swizzled in LDS by (row >> 1) & 7 over their 16-byte chunks: the 16 rows read by
+// one group of 16 lanes land on 16 different bank groups. Rows past M read row M - 1 and are
+// never stored.
 // One launch covers the three projections: column tiles run over q, then k, then v.
 #include "common.h"
 #include "kernels.h"
+#include "lds_dma.h"
 
 namespace tessery {
 
 namespace {
 
-constexpr int XROW = 64 + 8;  // halves per staged x row: 16-byte pad, rows 4 banks apart
-
+// codes c0..c7 of a weight word (nibble j = code of column 8q + j) as fp16 in natural order:
+// bytes of (w & 0x0F0F0F0F) hold c0 c2 c4 c6, of (w >> 4) & 0x0F0F0F0F hold c1 c3 c5 c7; v_perm
+// pairs them as (c_2p, c_2p+1) halves, 0x6400 | c is 1024 + c in fp16, and 1024 is subtracted
+// exactly.
 __device__ __forceinline__ half8 decode_codes(uint32_t w) {
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
   uint4v r;
 #pragma unroll
-  for (int p = 0; p < 4; ++p) r[p] = ((w >> (4 * p)) & 0x000F000Fu) | 0x64006400u;
+  for (int p = 0; p < 4; ++p) {
+    const uint32_t sel = 0x0C000C00u | (static_cast<uint32_t>(4 + p) << 16) | static_cast<uint32_t>(p);
+    r[p] = __builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u;
+  }
   half8 h = __builtin_bit_cast(half8, r);
   const half8 bias = {1024, 1024, 1024, 1024, 1024, 1024, 1024, 1024};
   return h - bias;
@@ -47,12 +58,15 @@ __device__ __forceinline__ float word_value(uint16_t w) {
   }
 }
 
+__device__ __forceinline__ int xsw(int row) { return (row >> 1) & 7; }
+
 template <bool BF16>
 __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
-  __shared__ __attribute__((aligned(16))) _Float16 xs[128 * XROW];
-  __shared__ __attribute__((aligned(16))) float xsum[128];
+  // two x stages of 128 rows x 64 halves, as the DMA writes them (1 KiB = 8 rows per block)
+  __shared__ __attribute__((aligned(1024))) _Float16 xs[2][128 * 64];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wm = wave >> 1, wn = wave & 1;
   const int M = a.M, K = a.K, groups = K / 64;
   const int m0 = blockIdx.x * 128;
@@ -71,6 +85,32 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
   _Float16* __restrict__ y = a.y[proj];
   const int nw = tile * 128 + wn * 64;  // wavefront's first column
 
+  // ---- DMA of the x tile of one group: wavefront w fills blocks 4w .. 4w+3 (rows 8 per block)
+  const int dchunk = lane & 7;
+  auto issue_x = [&](int stage, int g) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int blk = 4 * wave + j, row = 8 * blk + (lane >> 3);
+      const int grow = min(m0 + row, M - 1);
+      const _Float16* src =
+          a.x + static_cast<size_t>(grow) * K + 64 * g + 8 * (dchunk ^ xsw(row));
+      dma16(src, &xs[stage][blk * 512]);
+    }
+  };
+  // ---- weight words / scale / bias of one group for the lane's two columns
+  const size_t wrow[2] = {static_cast<size_t>(nw + l32) * (K / 8),
+                          static_cast<size_t>(nw + 32 + l32) * (K / 8)};
+  const size_t srow[2] = {static_cast<size_t>(nw + l32) * groups,
+                          static_cast<size_t>(nw + 32 + l32) * groups};
+  auto load_w = [&](int g, uint4v (&wd)[2], uint16_t (&sv)[2], uint16_t (&bv)[2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      wd[j] = *reinterpret_cast<const uint4v*>(w + wrow[j] + 8 * g + 4 * hh);
+      sv[j] = sc[srow[j] + g];
+      bv[j] = bi[srow[j] + g];
+    }
+  };
+
   floatx16 acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -79,76 +119,75 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  for (int g = 0; g < groups; ++g) {
-    // ---- stage x[m0 .. m0+127][64g .. 64g+63] in interleaved order, and its row sums ----
-    __syncthreads();
-    {
-      // 1024 chunks of 8 halves; thread t stages row t/2, chunks 4*(t%2) .. +3
-      const int row = tid >> 1, part = tid & 1;
-      float s = 0.0f;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int chunk = 4 * part + c;
-        half8 v = {};
-        if (m0 + row < M)
-          v = *reinterpret_cast<const half8*>(a.x + static_cast<size_t>(m0 + row) * K + 64 * g + 8 * chunk);
-        half8 p = {v[0], v[4], v[1], v[5], v[2], v[6], v[3], v[7]};
-        *reinterpret_cast<half8*>(&xs[row * XROW + 8 * chunk]) = p;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) s += static_cast<float>(v[j]);
-      }
-      s += __shfl_xor(s, 1);
-      if (part == 0) xsum[row] = s;
-    }
-    __syncthreads();
+  const half8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+  issue_x(0, 0);
+  uint4v wd[2];
+  uint16_t sv[2], bv[2];
+  load_w(0, wd, sv, bv);
 
-    // ---- B operands: codes of this lane's two weight rows, four k-steps each ----
+  for (int g = 0; g < groups; ++g) {
+    const int stage = g & 1;
+    // this group's x tile (own DMA) and registers, then everyone's: the other stage is free
+    wait_vmcnt<0>();
+    stage_barrier();
+    uint4v wn_[2];
+    uint16_t sn_[2], bn_[2];
+    if (g + 1 < groups) {
+      issue_x(stage ^ 1, g + 1);
+      load_w(g + 1, wn_, sn_, bn_);
+    }
+
     half8 bq[2][4];
     float gs[2], gb[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int n = nw + 32 * j + l32;
-      const uint4v words =
-          *reinterpret_cast<const uint4v*>(w + static_cast<size_t>(n) * (K / 8) + 8 * g + 4 * hh);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) bq[j][s] = decode_codes(words[s]);
-      gs[j] = word_value<BF16>(sc[static_cast<size_t>(n) * groups + g]);
-      gb[j] = word_value<BF16>(bi[static_cast<size_t>(n) * groups + g]);
+      for (int s = 0; s < 4; ++s) bq[j][s] = decode_codes(wd[j][s]);
+      gs[j] = word_value<BF16>(sv[j]);
+      gb[j] = word_value<BF16>(bv[j]);
     }
 
-    // ---- A_g for the 2x2 tiles ----
-    floatx16 part[2][2];
+    // ---- A_g for the 2x2 tiles and X_g (x times ones) per row tile ----
+    floatx16 part[2][2], xg[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) xg[i][e] = 0.0f;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int e = 0; e < 16; ++e) part[i][j][e] = 0.0f;
+    }
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int row = wm * 64 + 32 * i + l32;
-        const half8 av = *reinterpret_cast<const half8*>(&xs[row * XROW + 32 * hh + 8 * s]);
+        const half8 av =
+            *reinterpret_cast<const half8*>(&xs[stage][row * 64 + 8 * ((4 * hh + s) ^ xsw(row))]);
 #pragma unroll
         for (int j = 0; j < 2; ++j)
           part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bq[j][s], part[i][j], 0, 0, 0);
+        xg[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, ones, xg[i], 0, 0, 0);
       }
 
     // ---- fold: acc += scale * A_g + bias * X_g ----
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const floatx4 xg = *reinterpret_cast<const floatx4*>(&xsum[wm * 64 + 32 * i + 8 * q + 4 * hh]);
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int e = 0; e < 16; ++e)
+          acc[i][j][e] = fmaf(gs[j], part[i][j][e], fmaf(gb[j], xg[i][e], acc[i][j][e]));
+
+    if (g + 1 < groups) {
 #pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const int e = 4 * q + c;
-            acc[i][j][e] = fmaf(gs[j], part[i][j][e], fmaf(gb[j], xg[c], acc[i][j][e]));
-          }
+      for (int j = 0; j < 2; ++j) {
+        wd[j] = wn_[j];
+        sv[j] = sn_[j];
+        bv[j] = bn_[j];
       }
+    }
   }
 
   // ---- store y[m][n] as fp16 ----
