@@ -91,8 +91,9 @@ __global__ __launch_bounds__(64) void attn_scalar(const TIn* __restrict__ q,
 // XCDs, each with its own L2, so index i runs on XCD i % 8. The schedule gives every XCD whole
 // planes and lists each plane's workgroups consecutively, so the K/V tiles of a plane are
 // fetched into one L2 once and reused while that plane's workgroups run together. Planes are
-// ordered by the length of their batch row, longest first (causal and bidirectional cost both
-// grow with it), and inside a plane the last (longest causal) query blocks go first.
+// ordered by the length of their batch row (to 1/64 of S), longest first (causal and
+// bidirectional cost both grow with it), and inside a plane the last (longest causal) query
+// blocks go first.
 // The ranking is computed by every wavefront from `lengths` with one vector load; it needs
 // planes % 8 == 0 and B <= 64 (sched_ranked), otherwise planes keep their natural order.
 //
@@ -117,16 +118,31 @@ __device__ __forceinline__ Sched schedule(const uint32_t* lengths, int B, int S,
     const int j = static_cast<int>(blockIdx.z) * 8 + static_cast<int>(blockIdx.x);  // plane rank
     sc.wgp = static_cast<int>(gridDim.y - 1 - blockIdx.y);
     const int jrow = j / KV, kvh = j - jrow * KV;
-    // Lane l < B holds key (length << 6) | (63 - l): distinct keys, longer rows first and the
-    // lower index first among equal lengths. A row's rank counts the larger keys, read from the
-    // other lanes with v_readlane (no dependent loads).
+    // Lane l < B holds row l's length, quantized to its top six bits below S: q = len >> shift
+    // with S >> shift < 64. Rows are ordered by q descending, lower index first among equal q,
+    // and the row of rank jrow is found by radix selection over q's six bits: one ballot per
+    // bit and scalar arithmetic, then the jrow-th remaining lane in index order (v_mbcnt).
     // (the load is unconditional, from a clamped index, so it issues first thing)
     const int lane = threadIdx.x & 63;
     const uint32_t len = min(lengths[min(lane, B - 1)], static_cast<uint32_t>(S));
-    const uint32_t key = lane < B ? (len << 6) | static_cast<uint32_t>(63 - lane) : 0u;
-    int rank = 0;
-    for (int other = 0; other < B; ++other) rank += __builtin_amdgcn_readlane(key, other) > key;
-    const unsigned long long hit = __ballot(lane < B && rank == jrow);
+    const int shift = max(0, 26 - __clz(S));  // bit length of S minus six
+    const uint32_t q = len >> shift;
+    unsigned long long cand = __ballot(lane < B);
+    int r = jrow;
+#pragma unroll
+    for (int bit = 5; bit >= 0; --bit) {
+      const unsigned long long ones = __ballot((q >> bit) & 1u) & cand;
+      const int c = __popcll(ones);
+      if (r < c) {
+        cand = ones;
+      } else {
+        cand ^= ones;
+        r -= c;
+      }
+    }
+    const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(cand >> 32),
+                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(cand), 0u));
+    const unsigned long long hit = __ballot(((cand >> lane) & 1u) && below == static_cast<uint32_t>(r));
     const int b = __ffsll(hit) - 1;
     sc.plane = b * KV + kvh;
     sc.L = static_cast<int>(__builtin_amdgcn_readlane(len, b));
