@@ -54,10 +54,12 @@ def test_rope(runtime, shape, theta):
     np.testing.assert_allclose(got, ref.rope(x, theta), atol=2e-6)
 
 
-@pytest.mark.parametrize("dim", [32, 64, 128])
-def test_norm_rope_f16_prologue(runtime, dim):
-    shape = workloads.Shape(3, 70, 16, 8, dim, causal=True)
-    t = workloads.qwen_layer(shape, 0, seed=dim)
+# (dim, heads): lanes per position = dim / 16 * heads = 16, 32, 64, 24 (does not divide 256),
+# 256 (one position per pass), 40
+@pytest.mark.parametrize("dim,heads", [(32, 8), (64, 8), (128, 8), (128, 3), (128, 32), (64, 5)])
+def test_norm_rope_f16_prologue(runtime, dim, heads):
+    shape = workloads.Shape(3, 70, 2 * heads, heads, dim, causal=True)
+    t = workloads.qwen_layer(shape, 0, seed=dim + heads)
     lengths = np.array([70, 1, 33], np.uint32)
     sentinel = np.full((2,) + t["k"].shape, np.nan, np.float16)
     bufs = [runtime.upload(t["k"]), runtime.upload(t["k_norm"]), runtime.upload(lengths),
