@@ -570,42 +570,58 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
   if constexpr (FUSED) {
     // RMSNorm over the row (four lanes) then split-half RoPE: channel c < D/2 of step s pairs
     // with channel c + D/2 of step s + NS/2 in the same lane (kernels.metal:53-63, :65-74).
-    float x[NS][8];
+    // fp32 math; the fp16 q enters v_fma_mix directly and 1/rms is folded into cos and sin:
+    //   A = q_c g_c, B = q_{c+D/2} g_{c+D/2}, (A, B) -> (A cos' - B sin', A sin' + B cos')
+    // with cos' = cos / rms, sin' = sin / rms. Then hi = fp16(x), lo = fp16(x - hi).
+    // sum of squares with v_dot2_f32_f16 on the packed pairs (fp16 products are exact in fp32)
     float ss = 0.0f;
 #pragma unroll
     for (int s = 0; s < NS; ++s)
 #pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const float xf = static_cast<float>(qh[s][m]);
-        ss = fmaf(xf, xf, ss);
+      for (int m = 0; m < 8; m += 2) {
+        const half2v x2 = {qh[s][m], qh[s][m + 1]};
+        ss = __builtin_amdgcn_fdot2(x2, x2, ss, false);
       }
     ss = rowsum4(ss);
-    const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
-    // x = q * (inv * gamma): the fp16 q feeds a mixed-precision fma directly
-#pragma unroll
-    for (int s = 0; s < NS; ++s)
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const uint16_t w = static_cast<uint16_t>((gw[s][m >> 1] >> (16 * (m & 1))) & 0xffffu);
-        x[s][m] = fmaf(static_cast<float>(qh[s][m]), inv * bf16_to_float(w), 0.0f);
-      }
+    const float inv = __builtin_amdgcn_rsqf(ss * (1.0f / static_cast<float>(D)) + eps);
+    // an opaque 1.0 keeps (x - hi) an fma, which maps onto v_fma_mix with hi as an fp16 operand
+    float one = 1.0f;
+    asm("" : "+v"(one));
+    half2v hv[NS][4], lv[NS][4];  // packed channel pairs (m, m + 1)
 #pragma unroll
     for (int s = 0; s < NS / 2; ++s)
 #pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const float cv = cs[s][m >> 2][m & 3], sv = sn[s][m >> 2][m & 3];
-        const float a = x[s][m], bb = x[s + NS / 2][m];
-        x[s][m] = a * cv - bb * sv;
-        x[s + NS / 2][m] = a * sv + bb * cv;
+      for (int m = 0; m < 8; m += 2) {
+        float r[2][2];  // [first / second half of the row][channel m, m + 1]
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const uint32_t w0 = gw[s][m >> 1], w1 = gw[s + NS / 2][m >> 1];
+          const float g0 = __uint_as_float(e ? (w0 & 0xffff0000u) : (w0 << 16));
+          const float g1 = __uint_as_float(e ? (w1 & 0xffff0000u) : (w1 << 16));
+          const float a = fmaf(static_cast<float>(qh[s][m + e]), g0, 0.0f);
+          const float bb = fmaf(static_cast<float>(qh[s + NS / 2][m + e]), g1, 0.0f);
+          const float cv = cs[s][m >> 2][(m & 3) + e] * inv, sv = sn[s][m >> 2][(m & 3) + e] * inv;
+          r[0][e] = fmaf(a, cv, -(bb * sv));
+          r[1][e] = fmaf(a, sv, bb * cv);
+        }
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const half2v h = __builtin_convertvector((float2v){r[half][0], r[half][1]}, half2v);
+          const half2v l = {static_cast<_Float16>(fmaf(-static_cast<float>(h.x), one, r[half][0])),
+                            static_cast<_Float16>(fmaf(-static_cast<float>(h.y), one, r[half][1]))};
+          hv[s + half * (NS / 2)][m >> 1] = h;
+          lv[s + half * (NS / 2)][m >> 1] = l;
+        }
       }
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const _Float16 hi = static_cast<_Float16>(x[s][m]);
-        qh[s][m] = hi;
-        ql[s][m] = static_cast<_Float16>(x[s][m] - static_cast<float>(hi));
-      }
+    for (int s = 0; s < NS; ++s) {
+      qh[s] = __builtin_shufflevector(__builtin_shufflevector(hv[s][0], hv[s][1], 0, 1, 2, 3),
+                                      __builtin_shufflevector(hv[s][2], hv[s][3], 0, 1, 2, 3),
+                                      0, 1, 2, 3, 4, 5, 6, 7);
+      ql[s] = __builtin_shufflevector(__builtin_shufflevector(lv[s][0], lv[s][1], 0, 1, 2, 3),
+                                      __builtin_shufflevector(lv[s][2], lv[s][3], 0, 1, 2, 3),
+                                      0, 1, 2, 3, 4, 5, 6, 7);
+    }
   }
   // Rows past S read row S - 1 (finite data) and are never stored; query columns do not mix in
   // either product, so they need no clearing.
