@@ -709,8 +709,16 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
       for (int dt = 0; dt < NDT; ++dt) {
         const int chunk = (2 * dt + ((r & 3) >> 1)) ^ (2 * (vrow & 7));
         const half4 a = lds_read_tr(vst + vrow * D + 8 * chunk + 4 * (r & 1));
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, o[dt], 0, 0, 0);
-        if constexpr (FUSED) o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pl, o[dt], 0, 0, 0);
+        if constexpr (FUSED) {
+          // P_hi V + P_lo V as one 16x16x32 product (full rate; 16x16x16 runs at half): lane
+          // group g's k-slots 8g..8g+3 carry P_hi of its keys 4g..4g+3 and slots 8g+4..8g+7
+          // P_lo of the same keys, each against the same V fragment
+          const half8 a2 = __builtin_shufflevector(a, a, 0, 1, 2, 3, 0, 1, 2, 3);
+          const half8 p2 = __builtin_shufflevector(pb, pl, 0, 1, 2, 3, 4, 5, 6, 7);
+          o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, p2, o[dt], 0, 0, 0);
+        } else {
+          o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, o[dt], 0, 0, 0);
+        }
       }
     } else {
       floatx4 sc[2];
