@@ -431,6 +431,15 @@ __device__ __forceinline__ float dot_ones(half4 p, float acc) {
 
 // reduce over the four lanes r, r+16, r+32, r+48 that hold one query's scores
 __device__ __forceinline__ float rowmax4(float x) { return pair32(pair16(x, true), true); }
+// x ~ hi + lo in fp16 for a pair of floats: hi = fp16(x) rounded to nearest, lo = fp16(x - hi).
+// `one` is an opaque 1.0: it keeps x - hi an fma with hi as an fp16 operand (one v_fma_mix per
+// element) instead of a convert back and a subtraction.
+__device__ __forceinline__ void split2(float x0, float x1, float one, half2v& hi, half2v& lo) {
+  hi = __builtin_convertvector((float2v){x0, x1}, half2v);
+  lo = half2v{static_cast<_Float16>(fmaf(-static_cast<float>(hi.x), one, x0)),
+              static_cast<_Float16>(fmaf(-static_cast<float>(hi.y), one, x1))};
+}
+
 __device__ __forceinline__ float rowsum4(float x) { return pair32(pair16(x, false), false); }
 
 // K/V ring geometry. A tile holds KT = 2048 / D keys, so every plane tile (K hi, K lo when fused,
@@ -444,6 +453,11 @@ template <int D>
 __device__ __forceinline__ int ksw(int row) {
   return D == 128 ? (row & 15) : ((row >> 1) & 7);
 }
+
+template <int N>
+struct Stage {  // compile-time ring stage index
+  static constexpr int value = N;
+};
 
 template <int D, bool FUSED>
 struct F16Ring {
@@ -567,6 +581,10 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
       sn[s][1] = *reinterpret_cast<const floatx4*>(stt + 32 * s + 4);
     }
   }
+  float one = 1.0f;  // opaque 1.0 for split2
+  asm("" : "+v"(one));
+  int vzero = 0;  // opaque 0: two reads of one V fragment stay two reads
+  asm("" : "+s"(vzero));
   if constexpr (FUSED) {
     // RMSNorm over the row (four lanes) then split-half RoPE: channel c < D/2 of step s pairs
     // with channel c + D/2 of step s + NS/2 in the same lane (kernels.metal:53-63, :65-74).
@@ -584,9 +602,6 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
       }
     ss = rowsum4(ss);
     const float inv = __builtin_amdgcn_rsqf(ss * (1.0f / static_cast<float>(D)) + eps);
-    // an opaque 1.0 keeps (x - hi) an fma, which maps onto v_fma_mix with hi as an fp16 operand
-    float one = 1.0f;
-    asm("" : "+v"(one));
     half2v hv[NS][4], lv[NS][4];  // packed channel pairs (m, m + 1)
 #pragma unroll
     for (int s = 0; s < NS / 2; ++s)
@@ -605,13 +620,9 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
           r[1][e] = fmaf(a, sv, bb * cv);
         }
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const half2v h = __builtin_convertvector((float2v){r[half][0], r[half][1]}, half2v);
-          const half2v l = {static_cast<_Float16>(fmaf(-static_cast<float>(h.x), one, r[half][0])),
-                            static_cast<_Float16>(fmaf(-static_cast<float>(h.y), one, r[half][1]))};
-          hv[s + half * (NS / 2)][m >> 1] = h;
-          lv[s + half * (NS / 2)][m >> 1] = l;
-        }
+        for (int half = 0; half < 2; ++half)
+          split2(r[half][0], r[half][1], one, hv[s + half * (NS / 2)][m >> 1],
+                 lv[s + half * (NS / 2)][m >> 1]);
       }
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
@@ -649,8 +660,12 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
     return acc;
   };
 
-  int cur = 0, nxt = 2;  // stage of tile kt, stage tile kt + 2 goes to
-  for (int kt = 0; kt < ntiles; ++kt) {
+  // One K/V tile; tile kt lives in ring stage kt % 3 and tile kt + 2 goes to stage (kt + 2) % 3.
+  // The stage is a compile-time constant (the loop below is unrolled by the ring depth), so
+  // every LDS address of the tile is a per-lane register plus an immediate offset.
+  static_assert(NST == 3, "the tile loop is unrolled by the ring depth");
+  auto step = [&](int kt, auto stage) {
+    constexpr int cur = decltype(stage)::value, nxt = (cur + 2) % NST;
     // in flight: this tile, then the next one (issued one step earlier or in the prologue)
     if (kt + 1 < ntiles) wait_vmcnt<R::LPT>();
     else wait_vmcnt<0>();
@@ -658,9 +673,7 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
     if (kt + 2 < ntiles) issue(nxt, kt + 2);
     const _Float16* kst = ring + cur * R::STAGE;
     const _Float16* vst = kst + KPL * R::TILE;
-    cur = cur == NST - 1 ? 0 : cur + 1;
-    nxt = nxt == NST - 1 ? 0 : nxt + 1;
-    if (kt * KT >= g.wave_end) continue;
+    if (kt * KT >= g.wave_end) return;
 
     if constexpr (KT == 16) {
       floatx4 sc = qk_block(kst, 0);
@@ -682,11 +695,12 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
         // fp32 sum of the same values
         float pf[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          pf[j] = __builtin_amdgcn_exp2f(fmaf(sc[j], scale_log2, -m_new));
-          pb[j] = static_cast<_Float16>(pf[j]);
-          pl[j] = static_cast<_Float16>(pf[j] - static_cast<float>(pb[j]));
-        }
+        for (int j = 0; j < 4; ++j) pf[j] = __builtin_amdgcn_exp2f(fmaf(sc[j], scale_log2, -m_new));
+        half2v h0, h1, l0, l1;
+        split2(pf[0], pf[1], one, h0, l0);
+        split2(pf[2], pf[3], one, h1, l1);
+        pb = __builtin_shufflevector(h0, h1, 0, 1, 2, 3);
+        pl = __builtin_shufflevector(l0, l1, 0, 1, 2, 3);
         l_run = fmaf(l_run, corr, (pf[0] + pf[1]) + (pf[2] + pf[3]));
       } else {
 #pragma unroll
@@ -712,8 +726,10 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
         if constexpr (FUSED) {
           // P_hi V + P_lo V as one 16x16x32 product (full rate; 16x16x16 runs at half): lane
           // group g's k-slots 8g..8g+3 carry P_hi of its keys 4g..4g+3 and slots 8g+4..8g+7
-          // P_lo of the same keys, each against the same V fragment
-          const half8 a2 = __builtin_shufflevector(a, a, 0, 1, 2, 3, 0, 1, 2, 3);
+          // P_lo of the same keys, each against the same V fragment, read a second time into
+          // the upper half of the operand (an LDS read instead of two register copies)
+          const half4 a_again = lds_read_tr(vst + vzero + vrow * D + 8 * chunk + 4 * (r & 1));
+          const half8 a2 = __builtin_shufflevector(a, a_again, 0, 1, 2, 3, 4, 5, 6, 7);
           const half8 p2 = __builtin_shufflevector(pb, pl, 0, 1, 2, 3, 4, 5, 6, 7);
           o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, p2, o[dt], 0, 0, 0);
         } else {
@@ -745,12 +761,17 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int e = 4 * blk + j;
-            pf[e] = __builtin_amdgcn_exp2f(fmaf(sc[blk][j], scale_log2, -m_new));
-            pb[e] = static_cast<_Float16>(pf[e]);
-            pl[e] = static_cast<_Float16>(pf[e] - static_cast<float>(pb[e]));
-          }
+          for (int j = 0; j < 4; ++j)
+            pf[4 * blk + j] = __builtin_amdgcn_exp2f(fmaf(sc[blk][j], scale_log2, -m_new));
+        half2v h[4], l[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) split2(pf[2 * e], pf[2 * e + 1], one, h[e], l[e]);
+        pb = __builtin_shufflevector(__builtin_shufflevector(h[0], h[1], 0, 1, 2, 3),
+                                     __builtin_shufflevector(h[2], h[3], 0, 1, 2, 3),
+                                     0, 1, 2, 3, 4, 5, 6, 7);
+        pl = __builtin_shufflevector(__builtin_shufflevector(l[0], l[1], 0, 1, 2, 3),
+                                     __builtin_shufflevector(l[2], l[3], 0, 1, 2, 3),
+                                     0, 1, 2, 3, 4, 5, 6, 7);
         l_run = fmaf(l_run, corr,
                      ((pf[0] + pf[1]) + (pf[2] + pf[3])) + ((pf[4] + pf[5]) + (pf[6] + pf[7])));
       } else {
@@ -785,10 +806,20 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
         if constexpr (FUSED) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl, o[dt], 0, 0, 0);
       }
     }
+  };
+  // Every step stays inside the loop, so the q fragments stay live to the end: the registers of
+  // an operand are never reused as the destination of the MFMA that reads it.
+  for (int kt = 0; kt < ntiles; kt += NST) {
+    step(kt, Stage<0>{});
+    if (kt + 1 < ntiles) step(kt + 1, Stage<1>{});
+    if (kt + 2 < ntiles) step(kt + 2, Stage<2>{});
   }
   // No DMA may still be writing this workgroup's LDS past this point, and after the barrier no
-  // wavefront reads the ring any more: it becomes the staging area of the output rows.
+  // wavefront reads the ring any more: it becomes the staging area of the output rows. Each
+  // wavefront's own ring reads have returned before it arrives (the compiler may place the last
+  // tile's uses of them after the barrier).
   wait_vmcnt<0>();
+  wait_lgkmcnt<0>();
   const float inv = 1.0f / rowsum4(l_run);
   stage_barrier();
 

@@ -28,6 +28,13 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// s_waitcnt lgkmcnt(n): this wavefront's LDS reads (and scalar loads) down to n in flight.
+template <int N>
+__device__ __forceinline__ void wait_lgkmcnt() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (N << 8));
+}
+
 // Workgroup barrier without a memory fence. Each wavefront has already waited (vmcnt) for its
 // own DMA writes into the stage it is about to release, so after s_barrier every wavefront's
 // tile data is in LDS; the asm clobbers keep the compiler from moving LDS accesses across.
