@@ -331,7 +331,7 @@ __global__ __launch_bounds__(256, 2) void attn_f32_mfma(const float* __restrict_
       for (int a = 0; a < 4; ++a) {
         floatx4 r = {o[dt][4 * a] * inv, o[dt][4 * a + 1] * inv, o[dt][4 * a + 2] * inv,
                      o[dt][4 * a + 3] * inv};
-        *reinterpret_cast<floatx4*>(out + base + 32 * dt + 8 * a + 4 * hh) = r;
+        __builtin_nontemporal_store(r, reinterpret_cast<floatx4*>(out + base + 32 * dt + 8 * a + 4 * hh));
       }
   }
 }
@@ -860,7 +860,9 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
     // output row index relative to (b, p0, head0): prow * H + head offset, 32-bit
     const unsigned rel = static_cast<unsigned>(prow * H + (row & ((1 << g.hsh) - 1)));
     if (g.active && g.p0 + prow < S)
-      *reinterpret_cast<uint4v*>(obase + rel * RB + 16 * (c % OCH)) = val[i];
+      // non-temporal: output rows are written once and not read back here, so they should not
+      // stay dirty in L2 (K/V tiles keep it, and the end-of-kernel writeback stays short)
+      __builtin_nontemporal_store(val[i], reinterpret_cast<uint4v*>(obase + rel * RB + 16 * (c % OCH)));
   }
 }
 
