@@ -99,25 +99,42 @@ __global__ __launch_bounds__(64) void attn_scalar(const TIn* __restrict__ q,
 //
 // The grid carries the decomposition, so no division is needed to decode it (sched_grid):
 // ranked: (8, wpp, planes / 8) - linear id x + 8 * (y + wpp * z) runs on XCD x, and XCD x takes
-//         plane ranks z * 8 + x in z order with block y of each; otherwise: (wpp, planes, 1).
+//         plane ranks z * 8 + x in z order with block y of each (rank j is batch rank j / KV,
+//         kv head j % KV); otherwise (wpp, KV, B), the plane being (z, y).
 struct Sched {
-  int plane, wgp, L;  // L: valid length of the plane's batch row, clamped to S
+  int b, kvh, wgp, L;  // L: valid length of batch row b, clamped to S
 };
+
+// n / d without a division instruction: m = ceil(2^32 / d) (0 stands for d = 1) and
+// n / d = mulhi(n, m). With m = (2^32 + e) / d, 0 <= e < d, the quotient is exact whenever
+// n * d < 2^32 (the error term n * e / (d * 2^32) stays below 1 / d); launchers check that bound.
+struct Div {
+  uint32_t m;
+};
+
+__host__ inline Div make_div(uint32_t d) {
+  return Div{d <= 1 ? 0u : static_cast<uint32_t>(((1ull << 32) + d - 1) / d)};
+}
+
+__device__ __forceinline__ int quot(int n, Div v) {
+  return v.m ? static_cast<int>(__umulhi(static_cast<uint32_t>(n), v.m)) : n;
+}
 
 __host__ __device__ inline bool sched_ranked(int B, int KV) { return (B * KV) % 8 == 0 && B <= 64; }
 
 __host__ inline dim3 sched_grid(int B, int KV, int wpp) {
   const unsigned planes = static_cast<unsigned>(B * KV);
   return sched_ranked(B, KV) ? dim3(8, static_cast<unsigned>(wpp), planes / 8)
-                             : dim3(static_cast<unsigned>(wpp), planes, 1);
+                             : dim3(static_cast<unsigned>(wpp), static_cast<unsigned>(KV),
+                                    static_cast<unsigned>(B));
 }
 
-__device__ __forceinline__ Sched schedule(const uint32_t* lengths, int B, int S, int KV) {
+__device__ __forceinline__ Sched schedule(const uint32_t* lengths, int B, int S, int KV, Div kvdiv) {
   Sched sc;
   if (sched_ranked(B, KV)) {
     const int j = static_cast<int>(blockIdx.z) * 8 + static_cast<int>(blockIdx.x);  // plane rank
     sc.wgp = static_cast<int>(gridDim.y - 1 - blockIdx.y);
-    const int jrow = j / KV, kvh = j - jrow * KV;
+    const int jrow = quot(j, kvdiv), kvh = j - jrow * KV;
     // Lane l < B holds row l's length, quantized to its top six bits below S: q = len >> shift
     // with S >> shift < 64. Rows are ordered by q descending, lower index first among equal q,
     // and the row of rank jrow is found by radix selection over q's six bits: one ballot per
@@ -143,13 +160,14 @@ __device__ __forceinline__ Sched schedule(const uint32_t* lengths, int B, int S,
     const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(cand >> 32),
                                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(cand), 0u));
     const unsigned long long hit = __ballot(((cand >> lane) & 1u) && below == static_cast<uint32_t>(r));
-    const int b = __ffsll(hit) - 1;
-    sc.plane = b * KV + kvh;
-    sc.L = static_cast<int>(__builtin_amdgcn_readlane(len, b));
+    sc.b = __ffsll(hit) - 1;
+    sc.kvh = kvh;
+    sc.L = static_cast<int>(__builtin_amdgcn_readlane(len, sc.b));
   } else {
-    sc.plane = static_cast<int>(blockIdx.y);
+    sc.b = static_cast<int>(blockIdx.z);
+    sc.kvh = static_cast<int>(blockIdx.y);
     sc.wgp = static_cast<int>(gridDim.x - 1 - blockIdx.x);
-    sc.L = static_cast<int>(min(lengths[sc.plane / KV], static_cast<uint32_t>(S)));
+    sc.L = static_cast<int>(min(lengths[sc.b], static_cast<uint32_t>(S)));
   }
   return sc;
 }
@@ -159,19 +177,26 @@ struct Geom {
   bool active;
 };
 
-__device__ __forceinline__ Geom make_geom(const uint32_t* lengths, int B, int S, int H, int KV,
-                                          int bidi, int wave) {
+// Host-computed divisors of the fp32 kernel's geometry (G = H / KV query heads per kv head).
+struct F32Shape {
+  int G;
+  Div g, kv;
+};
+
+__device__ __forceinline__ Geom make_geom(const uint32_t* lengths, int B, int S, int KV, int bidi,
+                                          int wave, F32Shape sh) {
   Geom g;
-  const int G = H / KV;
+  const int G = sh.G;
   const int nrb = G * ((S + 31) / 32);
-  const Sched sc = schedule(lengths, B, S, KV);
+  const Sched sc = schedule(lengths, B, S, KV, sh.kv);
   const int wgp = sc.wgp;
-  g.b = sc.plane / KV;
-  g.kvh = sc.plane % KV;
+  g.b = sc.b;
+  g.kvh = sc.kvh;
   const int rb = wgp * 4 + wave;
   g.active = rb < nrb;
-  g.head = g.kvh * G + rb % G;
-  g.p0 = (rb / G) * 32;
+  const int pb = quot(rb, sh.g);
+  g.head = g.kvh * G + (rb - pb * G);
+  g.p0 = pb * 32;
   g.L = sc.L;
   const int rb_last = min(wgp * 4 + 3, nrb - 1);
   if (bidi) {
@@ -180,7 +205,7 @@ __device__ __forceinline__ Geom make_geom(const uint32_t* lengths, int B, int S,
     g.limit_min = g.L;
   } else {
     g.wave_end = g.active ? min(g.p0 + 32, g.L) : 0;
-    g.wg_end = min((rb_last / G) * 32 + 32, g.L);
+    g.wg_end = min(quot(rb_last, sh.g) * 32 + 32, g.L);
     g.limit_min = min(g.p0 + 1, g.L);  // smallest per-row key limit inside this wave
   }
   return g;
@@ -202,7 +227,7 @@ __global__ __launch_bounds__(256, 2) void attn_f32_mfma(const float* __restrict_
                                                         const uint32_t* __restrict__ lengths,
                                                         float* __restrict__ out, int B, int S,
                                                         int H, int KV, float scale_log2,
-                                                        int bidi) {
+                                                        int bidi, F32Shape shp) {
   constexpr int KT = 32;
   constexpr int ROW = D + 4;
   constexpr int CH = KT * D / 4;            // 16-byte chunks per K (or V) tile
@@ -212,7 +237,7 @@ __global__ __launch_bounds__(256, 2) void attn_f32_mfma(const float* __restrict_
   __shared__ __attribute__((aligned(16))) float Vs[KT * ROW];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  const Geom g = make_geom(lengths, B, S, H, KV, bidi, wave);
+  const Geom g = make_geom(lengths, B, S, KV, bidi, wave, shp);
   const int qpos = g.p0 + l32;
   const bool qvalid = g.active && qpos < S;
   const int limit = bidi ? g.L : min(qpos + 1, g.L);
@@ -359,6 +384,7 @@ __host__ __device__ inline int f16_wave_blocks(int S, int G) {
 // blocks per plane.
 struct F16Shape {
   int G, hsh, nwb;
+  Div kv, hbn;  // KV and G >> hsh (head blocks per position block)
 };
 
 __device__ __forceinline__ Geom16 make_geom16(const uint32_t* lengths, int B, int S, int KV,
@@ -366,14 +392,14 @@ __device__ __forceinline__ Geom16 make_geom16(const uint32_t* lengths, int B, in
   Geom16 g;
   const int G = sh.G, nwb = sh.nwb;
   const int hpw = 1 << sh.hsh, ppw = 16 >> sh.hsh, hbn = G >> sh.hsh;
-  const Sched sc = schedule(lengths, B, S, KV);
+  const Sched sc = schedule(lengths, B, S, KV, sh.kv);
   const int wgp = sc.wgp;
-  g.b = sc.plane / KV;
-  g.kvh = sc.plane - g.b * KV;
+  g.b = sc.b;
+  g.kvh = sc.kvh;
   g.hsh = sh.hsh;
   const int wb = wgp * 4 + wave;
   g.active = wb < nwb;
-  const int pblk = hbn == 1 ? wb : wb / hbn;  // hbn == 1 whenever G divides 16
+  const int pblk = quot(wb, sh.hbn);  // hbn == 1 whenever G divides 16
   g.head0 = g.kvh * G + (wb - pblk * hbn) * hpw;
   g.p0 = pblk * ppw;
   g.L = sc.L;
@@ -384,7 +410,7 @@ __device__ __forceinline__ Geom16 make_geom16(const uint32_t* lengths, int B, in
     g.limit_min = g.L;
   } else {
     g.wave_end = g.active ? min(g.p0 + ppw, g.L) : 0;
-    g.wg_end = min((wb_last / hbn) * ppw + ppw, g.L);
+    g.wg_end = min(quot(wb_last, sh.hbn) * ppw + ppw, g.L);
     g.limit_min = min(g.p0 + 1, g.L);
   }
   return g;
@@ -875,6 +901,15 @@ static dim3 mfma_grid(int B, int S, int H, int KV) {
   return sched_grid(B, KV, (nrb + 3) / 4);
 }
 
+// Grid limits and the exactness bound of the Div quotients (n * d < 2^32 for every quotient the
+// geometry takes: plane rank / KV on the ranked schedule, row block / head blocks).
+static bool geometry_fits(int B, int KV, int nblocks, int blockdiv) {
+  const uint64_t kv = static_cast<uint64_t>(KV);
+  if (B > 65535 || KV > 65535) return false;
+  if (sched_ranked(B, KV) && static_cast<uint64_t>(B) * kv * kv >= (1ull << 32)) return false;
+  return static_cast<uint64_t>(nblocks) * static_cast<uint64_t>(blockdiv) < (1ull << 32);
+}
+
 hipError_t launch_attention_scalar(const AttnArgs& a, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>(a.B * a.S * a.H);
   if (!grid) return hipSuccess;
@@ -902,19 +937,24 @@ hipError_t launch_attention_scalar(const AttnArgs& a, hipStream_t st) {
 hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st) {
   if (!a.B || !a.S || !a.H) return hipSuccess;
   const dim3 grid = mfma_grid(a.B, a.S, a.H, a.KV);
+  F32Shape shp;
+  shp.G = a.H / a.KV;
+  shp.g = make_div(static_cast<uint32_t>(shp.G));
+  shp.kv = make_div(static_cast<uint32_t>(a.KV));
+  if (!geometry_fits(a.B, a.KV, shp.G * ((a.S + 31) / 32), shp.G)) return hipErrorInvalidValue;
   const float sl2 = a.scale * kLog2e;
   auto q = static_cast<const float*>(a.q), k = static_cast<const float*>(a.k),
        v = static_cast<const float*>(a.v);
   auto o = static_cast<float*>(a.out);
   switch (a.D) {
     case 32:
-      attn_f32_mfma<32><<<grid, 256, 0, st>>>(q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi);
+      attn_f32_mfma<32><<<grid, 256, 0, st>>>(q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
       break;
     case 64:
-      attn_f32_mfma<64><<<grid, 256, 0, st>>>(q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi);
+      attn_f32_mfma<64><<<grid, 256, 0, st>>>(q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
       break;
     case 128:
-      attn_f32_mfma<128><<<grid, 256, 0, st>>>(q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi);
+      attn_f32_mfma<128><<<grid, 256, 0, st>>>(q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
       break;
     default:
       return hipErrorInvalidValue;
@@ -943,6 +983,9 @@ hipError_t launch_attention_f16(const AttnArgs& a, hipStream_t st) {
   shp.G = a.H / a.KV;
   shp.hsh = __builtin_ctz(static_cast<unsigned>(f16_heads_per_wave(shp.G)));
   shp.nwb = f16_wave_blocks(a.S, shp.G);
+  shp.kv = make_div(static_cast<uint32_t>(a.KV));
+  shp.hbn = make_div(static_cast<uint32_t>(shp.G >> shp.hsh));
+  if (!geometry_fits(a.B, a.KV, shp.nwb, shp.G >> shp.hsh)) return hipErrorInvalidValue;
   const dim3 grid = sched_grid(a.B, a.KV, (shp.nwb + 3) / 4);
 
   const float sl2 = a.scale * kLog2e;
