@@ -457,15 +457,6 @@ __device__ __forceinline__ float dot_ones(half4 p, float acc) {
 
 // reduce over the four lanes r, r+16, r+32, r+48 that hold one query's scores
 __device__ __forceinline__ float rowmax4(float x) { return pair32(pair16(x, true), true); }
-// x ~ hi + lo in fp16 for a pair of floats: hi = fp16(x) rounded to nearest, lo = fp16(x - hi).
-// `one` is an opaque 1.0: it keeps x - hi an fma with hi as an fp16 operand (one v_fma_mix per
-// element) instead of a convert back and a subtraction.
-__device__ __forceinline__ void split2(float x0, float x1, float one, half2v& hi, half2v& lo) {
-  hi = __builtin_convertvector((float2v){x0, x1}, half2v);
-  lo = half2v{static_cast<_Float16>(fmaf(-static_cast<float>(hi.x), one, x0)),
-              static_cast<_Float16>(fmaf(-static_cast<float>(hi.y), one, x1))};
-}
-
 __device__ __forceinline__ float rowsum4(float x) { return pair32(pair16(x, false), false); }
 
 // K/V ring geometry. A tile holds KT = 2048 / D keys, so every plane tile (K hi, K lo when fused,

@@ -31,6 +31,15 @@ __device__ __forceinline__ float bf16_to_float(uint16_t w) {
   return __uint_as_float(static_cast<uint32_t>(w) << 16);
 }
 
+// x ~ hi + lo in fp16 for a pair of floats: hi = fp16(x) rounded to nearest, lo = fp16(x - hi).
+// `one` is an opaque 1.0: it keeps x - hi an fma with hi as an fp16 operand (one v_fma_mix per
+// element) instead of a convert back and a subtraction.
+__device__ __forceinline__ void split2(float x0, float x1, float one, half2v& hi, half2v& lo) {
+  hi = __builtin_convertvector((float2v){x0, x1}, half2v);
+  lo = half2v{static_cast<_Float16>(fmaf(-static_cast<float>(hi.x), one, x0)),
+              static_cast<_Float16>(fmaf(-static_cast<float>(hi.y), one, x1))};
+}
+
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
