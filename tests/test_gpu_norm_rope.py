@@ -58,9 +58,18 @@ def test_rope(runtime, shape, theta):
 # 256 (one position per pass), 40
 @pytest.mark.parametrize("dim,heads", [(32, 8), (64, 8), (128, 8), (128, 3), (128, 32), (64, 5)])
 def test_norm_rope_f16_prologue(runtime, dim, heads):
-    shape = workloads.Shape(3, 70, 2 * heads, heads, dim, causal=True)
+    check_norm_rope_f16(runtime, dim, heads, np.array([70, 0, 1, 33], np.uint32), seq=70)
+
+
+def test_norm_rope_f16_many_rows(runtime):
+    """More than 64 batch rows: the launcher's per-row grid (the compacted one scans at most 64)."""
+    rng = np.random.default_rng(66)
+    check_norm_rope_f16(runtime, 128, 8, rng.integers(0, 6, 66).astype(np.uint32), seq=5)
+
+
+def check_norm_rope_f16(runtime, dim, heads, lengths, seq):
+    shape = workloads.Shape(len(lengths), seq, 2 * heads, heads, dim, causal=True)
     t = workloads.qwen_layer(shape, 0, seed=dim + heads)
-    lengths = np.array([70, 1, 33], np.uint32)
     sentinel = np.full((2,) + t["k"].shape, np.nan, np.float16)
     bufs = [runtime.upload(t["k"]), runtime.upload(t["k_norm"]), runtime.upload(lengths),
             runtime.upload(sentinel)]
