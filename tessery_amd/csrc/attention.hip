@@ -101,6 +101,11 @@ __global__ __launch_bounds__(64) void attn_scalar(const TIn* __restrict__ q,
 // ranked: (8, wpp, planes / 8) - linear id x + 8 * (y + wpp * z) runs on XCD x, and XCD x takes
 //         plane ranks z * 8 + x in z order with block y of each (rank j is batch rank j / KV,
 //         kv head j % KV); otherwise (wpp, KV, B), the plane being (z, y).
+template <int N>
+struct Stage {  // compile-time ring stage index
+  static constexpr int value = N;
+};
+
 struct Sched {
   int b, kvh, wgp, L;  // L: valid length of batch row b, clamped to S
 };
@@ -362,6 +367,179 @@ __global__ __launch_bounds__(256, 2) void attn_f32_mfma(const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------------------------
+// fp32 MFMA kernel with an LDS DMA ring, D = 32 and 64: the geometry, MFMA layout and arithmetic
+// of attn_f32_mfma, with the K and V tiles of 32 keys streamed through a 3-stage ring filled by
+// global_load_lds_dwordx4 two tiles ahead (one barrier per tile) instead of being staged through
+// registers, and the tile loop unrolled by the ring depth (LDS addresses = register + immediate).
+// LDS rows hold D floats, no padding:
+//   K: row r holds key r, its 16-byte chunks XOR-swizzled by ksw32(r), so the rows read by one
+//      group of 16 lanes (one chunk each) fall on 16 different bank groups;
+//   V: the rows that the two half-wavefronts read together (keys 4 apart) sit in opposite bank
+//      halves: for D = 32 key k lives in row k ^ ((k >> 2) & 1) (row parity picks the half), for
+//      D = 64 the two 128-byte halves of row r are swapped when bit 2 of r is set.
+// ---------------------------------------------------------------------------------------------
+template <int D>
+__device__ __forceinline__ int ksw32(int r) { return D == 32 ? (r >> 1) & 7 : r & 15; }
+template <int D>
+__device__ __forceinline__ int vrow32(int key) { return D == 32 ? key ^ ((key >> 2) & 1) : key; }
+template <int D>
+__device__ __forceinline__ int vsw32(int r) { return D == 32 ? 0 : ((r >> 2) & 1) * 8; }
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void attn_f32_ring(const float* __restrict__ q,
+                                                        const float* __restrict__ k,
+                                                        const float* __restrict__ v,
+                                                        const uint32_t* __restrict__ lengths,
+                                                        float* __restrict__ out, int B, int S,
+                                                        int H, int KV, float scale_log2,
+                                                        int bidi, F32Shape shp) {
+  static_assert(D == 32 || D == 64, "ring kernel serves D = 32 and 64");
+  constexpr int KT = 32, HALF = D / 2, NST = 3;
+  constexpr int TILE = KT * D;     // floats per plane tile
+  constexpr int STAGE = 2 * TILE;  // K tile, then V tile
+  constexpr int CPR = D / 4;       // 16-byte chunks per row
+  constexpr int RPB = 256 / D;     // rows per 1 KiB DMA block
+  constexpr int BPW = D / 32;      // DMA blocks per wavefront per plane tile
+  __shared__ __attribute__((aligned(1024))) float ring[NST * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const Geom g = make_geom(lengths, B, S, KV, bidi, wave, shp);
+  const int qpos = g.p0 + l32;
+  const bool qvalid = g.active && qpos < S;
+  const int limit = bidi ? g.L : min(qpos + 1, g.L);
+  const int ntiles = (g.wg_end + KT - 1) / KT;
+  const float* kbase = k + (static_cast<size_t>(g.b) * S * KV + g.kvh) * D;
+  const float* vbase = v + (static_cast<size_t>(g.b) * S * KV + g.kvh) * D;
+  const size_t krow = static_cast<size_t>(KV) * D;
+
+  // DMA of tile kt into a stage: wavefront w fills blocks w, w + 4, .. of each plane tile; lane l
+  // of block blk writes chunk l % CPR of LDS row blk * RPB + l / CPR. Keys at or past L read key 0
+  // of the batch row (finite data; masked, and multiplied by an exact zero weight).
+  auto issue = [&](int stage, int kt) {
+    float* st = ring + stage * STAGE;
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+      const int blk = wave + 4 * i;
+      const int r = blk * RPB + lane / CPR, c = lane % CPR;
+      const int kg = kt * KT + r;
+      dma16(kbase + static_cast<size_t>(kg < g.L ? kg : 0) * krow + 4 * (c ^ ksw32<D>(r)),
+            reinterpret_cast<_Float16*>(st + 256 * blk));
+      const int vk = kt * KT + vrow32<D>(r);  // key held by V row r (the map is an involution)
+      dma16(vbase + static_cast<size_t>(vk < g.L ? vk : 0) * krow + 4 * (c ^ vsw32<D>(r)),
+            reinterpret_cast<_Float16*>(st + TILE + 256 * blk));
+    }
+  };
+  // the first two tiles go out before the register loads of q (the compiler counts only its own
+  // loads when it waits for q; vmcnt retires in issue order)
+  if (ntiles > 0) issue(0, 0);
+  if (ntiles > 1) issue(1, 1);
+
+  // Q row slice held in registers as B operands.
+  float qf[HALF];
+  {
+    const size_t base = ((static_cast<size_t>(g.b) * S + qpos) * H + g.head) * D + hh * HALF;
+#pragma unroll
+    for (int c = 0; c < HALF / 4; ++c) {
+      floatx4 t = {0.f, 0.f, 0.f, 0.f};
+      if (qvalid) t = *reinterpret_cast<const floatx4*>(q + base + 4 * c);
+      qf[4 * c + 0] = t[0];
+      qf[4 * c + 1] = t[1];
+      qf[4 * c + 2] = t[2];
+      qf[4 * c + 3] = t[3];
+    }
+  }
+
+  floatx16 o[D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  auto step = [&](int kt, auto stage) {
+    constexpr int cur = decltype(stage)::value, nxt = (cur + 2) % NST;
+    // in flight: this tile, then the next one (issued one step earlier or in the prologue)
+    if (kt + 1 < ntiles) wait_vmcnt<2 * BPW>();
+    else wait_vmcnt<0>();
+    stage_barrier();
+    if (kt + 2 < ntiles) issue(nxt, kt + 2);
+    const float* Ks = ring + cur * STAGE;
+    const float* Vs = Ks + TILE;
+    if (kt * KT >= g.wave_end) return;
+    floatx16 s;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[e] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < HALF / 4; ++c) {
+      const int cg = hh * (HALF / 4) + c;
+      const floatx4 kk = *reinterpret_cast<const floatx4*>(&Ks[l32 * D + 4 * (cg ^ ksw32<D>(l32))]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[t], qf[4 * c + t], s, 0, 0, 0);
+    }
+    const bool full = kt * KT + KT <= g.limit_min;
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int key = kt * KT + 8 * (e >> 2) + 4 * hh + (e & 3);
+      float val = s[e] * scale_log2;
+      if (!full && key >= limit) val = -INFINITY;
+      s[e] = val;
+      mloc = fmaxf(mloc, val);
+    }
+    const float m_tile = fmaxf(mloc, __shfl_xor(mloc, 32));
+    const float m_new = fmaxf(m_run, m_tile);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+    float lsum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float p = __builtin_amdgcn_exp2f(s[e] - m_use);
+      s[e] = p;
+      lsum += p;
+    }
+    lsum += __shfl_xor(lsum, 32);
+    l_run = l_run * corr + lsum;
+    m_run = m_new;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[dt][e] *= corr;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int row = vrow32<D>(8 * (e >> 2) + 4 * hh + (e & 3));
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) {
+        const int d = 32 * dt + l32;
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+            Vs[row * D + 4 * ((d >> 2) ^ vsw32<D>(row)) + (d & 3)], s[e], o[dt], 0, 0, 0);
+      }
+    }
+  };
+  // all steps stay inside the loop (see attn_f16_mfma)
+  for (int kt = 0; kt < ntiles; kt += NST) {
+    step(kt, Stage<0>{});
+    if (kt + 1 < ntiles) step(kt + 1, Stage<1>{});
+    if (kt + 2 < ntiles) step(kt + 2, Stage<2>{});
+  }
+  wait_vmcnt<0>();  // no DMA may land in this workgroup's LDS after it exits
+
+  if (qvalid) {
+    const float inv = 1.0f / l_run;
+    const size_t base = ((static_cast<size_t>(g.b) * S + qpos) * H + g.head) * D;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        floatx4 r = {o[dt][4 * a] * inv, o[dt][4 * a + 1] * inv, o[dt][4 * a + 2] * inv,
+                     o[dt][4 * a + 3] * inv};
+        __builtin_nontemporal_store(r, reinterpret_cast<floatx4*>(out + base + 32 * dt + 8 * a + 4 * hh));
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // fp16 MFMA kernel: geometry and helpers (the kernel and its layout notes follow further down).
 // ---------------------------------------------------------------------------------------------
 struct Geom16 {
@@ -470,11 +648,6 @@ template <int D>
 __device__ __forceinline__ int ksw(int row) {
   return D == 128 ? (row & 15) : ((row >> 1) & 7);
 }
-
-template <int N>
-struct Stage {  // compile-time ring stage index
-  static constexpr int value = N;
-};
 
 template <int D, bool FUSED>
 struct F16Ring {
@@ -939,10 +1112,10 @@ hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st) {
   auto o = static_cast<float*>(a.out);
   switch (a.D) {
     case 32:
-      attn_f32_mfma<32><<<grid, 256, 0, st>>>(q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
+      attn_f32_ring<32><<<grid, 256, 0, st>>>(q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
       break;
     case 64:
-      attn_f32_mfma<64><<<grid, 256, 0, st>>>(q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
+      attn_f32_ring<64><<<grid, 256, 0, st>>>(q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
       break;
     case 128:
       attn_f32_mfma<128><<<grid, 256, 0, st>>>(q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
