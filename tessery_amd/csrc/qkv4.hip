@@ -62,8 +62,12 @@ __device__ __forceinline__ int xsw(int row) { return (row >> 1) & 7; }
 
 template <bool BF16>
 __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
-  // two x stages of 128 rows x 64 halves, as the DMA writes them (1 KiB = 8 rows per block)
-  __shared__ __attribute__((aligned(1024))) _Float16 xs[2][128 * 64];
+  // three x stages of 128 rows x 64 halves, as the DMA writes them (1 KiB = 8 rows per block)
+  __shared__ __attribute__((aligned(1024))) _Float16 xs[3][128 * 64];
+  // three stages of the packed weight words of the tile's 128 columns for one group (8 words each)
+  __shared__ __attribute__((aligned(1024))) uint32_t ws[3][128 * 8];
+  // scale and bias words of the tile's 128 columns, all groups: [2][128][groups] (dynamic size)
+  extern __shared__ __attribute__((aligned(1024))) uint16_t sbuf[];
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
@@ -97,19 +101,28 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
       dma16(src, &xs[stage][blk * 512]);
     }
   };
-  // ---- weight words / scale / bias of one group for the lane's two columns
-  const size_t wrow[2] = {static_cast<size_t>(nw + l32) * (K / 8),
-                          static_cast<size_t>(nw + 32 + l32) * (K / 8)};
-  const size_t srow[2] = {static_cast<size_t>(nw + l32) * groups,
-                          static_cast<size_t>(nw + 32 + l32) * groups};
-  auto load_w = [&](int g, uint4v (&wd)[2], uint16_t (&sv)[2], uint16_t (&bv)[2]) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      wd[j] = *reinterpret_cast<const uint4v*>(w + wrow[j] + 8 * g + 4 * hh);
-      sv[j] = sc[srow[j] + g];
-      bv[j] = bi[srow[j] + g];
-    }
+  // ---- DMA of the weight words of one group: wavefront w copies columns 32w .. 32w+31 of the
+  // tile (lane l: column 32w + l/2, words 4(l&1) .. +3), so lane l's 16 bytes land at byte 16l
+  const uint32_t* wsrc = w + static_cast<size_t>(tile * 128 + 32 * wave + (lane >> 1)) * (K / 8) +
+                         4 * (lane & 1);
+  auto issue_w = [&](int stage, int g) {
+    dma16(wsrc + 8 * g, reinterpret_cast<_Float16*>(&ws[stage][256 * wave]));
   };
+  // ---- scales and biases of the tile's columns, all groups: two contiguous runs of
+  // 128 * groups words (rows tile*128 .. +127 of [N, groups]), 16 bytes per lane, issued once
+  {
+    const int chunks = 128 * groups / 8;  // 16-byte chunks per run
+    const uint16_t* srcs[2] = {sc + static_cast<size_t>(tile * 128) * groups,
+                               bi + static_cast<size_t>(tile * 128) * groups};
+#pragma unroll
+    for (int part = 0; part < 2; ++part)
+      for (int blk = wave; blk * 64 < chunks; blk += 4) {
+        const int chunk = blk * 64 + lane;
+        if (chunk < chunks)
+          dma16(srcs[part] + 8 * chunk,
+                reinterpret_cast<_Float16*>(sbuf + part * 128 * groups + blk * 512));
+      }
+  }
 
   floatx16 acc[2][2];
 #pragma unroll
@@ -121,20 +134,32 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
 
   const half8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
   issue_x(0, 0);
-  uint4v wd[2];
-  uint16_t sv[2], bv[2];
-  load_w(0, wd, sv, bv);
+  issue_w(0, 0);
+  if (groups > 1) {
+    issue_x(1, 1);
+    issue_w(1, 1);
+  }
 
   for (int g = 0; g < groups; ++g) {
-    const int stage = g & 1;
-    // this group's x tile (own DMA) and registers, then everyone's: the other stage is free
-    wait_vmcnt<0>();
+    const int stage = g % 3;
+    // in flight: this group's tiles, then the next group's (5 DMA instructions per wavefront)
+    if (g + 1 < groups) wait_vmcnt<5>();
+    else wait_vmcnt<0>();
     stage_barrier();
-    uint4v wn_[2];
-    uint16_t sn_[2], bn_[2];
-    if (g + 1 < groups) {
-      issue_x(stage ^ 1, g + 1);
-      load_w(g + 1, wn_, sn_, bn_);
+    if (g + 2 < groups) {
+      const int nst = stage == 0 ? 2 : stage - 1;  // (g + 2) % 3
+      issue_x(nst, g + 2);
+      issue_w(nst, g + 2);
+    }
+    // the lane's four weight words of this group and the scale / bias of its two columns
+    uint4v wd[2];
+    uint16_t sv[2], bv[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = wn * 64 + 32 * j + l32;
+      wd[j] = *reinterpret_cast<const uint4v*>(&ws[stage][col * 8 + 4 * hh]);
+      sv[j] = sbuf[col * groups + g];
+      bv[j] = sbuf[128 * groups + col * groups + g];
     }
 
     half8 bq[2][4];
@@ -180,14 +205,6 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
         for (int e = 0; e < 16; ++e)
           acc[i][j][e] = fmaf(gs[j], part[i][j][e], fmaf(gb[j], xg[i][e], acc[i][j][e]));
 
-    if (g + 1 < groups) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        wd[j] = wn_[j];
-        sv[j] = sn_[j];
-        bv[j] = bn_[j];
-      }
-    }
   }
 
   // ---- store y[m][n] as fp16 ----
@@ -215,10 +232,14 @@ hipError_t launch_qkv4_f16(const Qkv4Args& a, hipStream_t st) {
     tiles += a.n[p] / 128;
   }
   dim3 grid((a.M + 127) / 128, tiles);
+  // scale and bias words of a column tile, all groups: 2 * 128 * groups halves (8 KiB at K = 1024);
+  // with the 60 KiB of x and weight stages, two workgroups fit a CU up to K = 2048
+  const size_t sb_bytes = static_cast<size_t>(2 * 128 * 2) * (a.K / 64);
+  if (sb_bytes > 64 * 1024) return hipErrorInvalidValue;  // K > 8192
   if (a.scale_bf16)
-    qkv4_f16<true><<<grid, 256, 0, st>>>(a);
+    qkv4_f16<true><<<grid, 256, sb_bytes, st>>>(a);
   else
-    qkv4_f16<false><<<grid, 256, 0, st>>>(a);
+    qkv4_f16<false><<<grid, 256, sb_bytes, st>>>(a);
   return hipGetLastError();
 }
 
