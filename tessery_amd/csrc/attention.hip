@@ -726,23 +726,31 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
   const int qpos_c = min(qpos, S - 1);
   const int limit = bidi ? g.L : min(qpos + 1, g.L);
   const int ntiles = (g.wg_end + KT - 1) / KT;
+  // plane bases are wave-uniform (SGPRs); per-lane DMA offsets are 32-bit bytes within the
+  // plane, below S * KV * D * 2 < 2^32 (checked by the launcher, as are S, KV * D * 2 < 2^24)
   const _Float16* kbase = k + (static_cast<size_t>(g.b) * S * KV + g.kvh) * D;
+  const _Float16* klo = kbase + k_plane;
   const _Float16* vbase = v + (static_cast<size_t>(g.b) * S * KV + g.kvh) * D;
-  const size_t krow = static_cast<size_t>(KV) * D;
+  const uint32_t rowbytes = static_cast<uint32_t>(KV * D * 2);
 
   // ---- DMA of one K/V tile into a stage: wavefront w fills block w of every plane tile -------
   const int drow = wave * RPB + lane / CPR;  // tile row this lane's chunk lands in
   const int dpos = lane % CPR;
   const int dkey = KT == 16 ? drow : tile_key(drow);
-  const int kchunk = dpos ^ ksw<D>(drow);
-  const int vchunk = dpos ^ (KT == 16 ? 2 * (drow & 7) : 2 * (drow & 3));
+  const uint32_t kcoff = 16 * (dpos ^ ksw<D>(drow));
+  const uint32_t vcoff = 16 * (dpos ^ (KT == 16 ? 2 * (drow & 7) : 2 * (drow & 3)));
   auto issue = [&](int stage, int kt) {
     _Float16* st = ring + stage * R::STAGE + wave * 512;
-    const int kg = kt * KT + dkey, vg = kt * KT + drow;
-    const _Float16* ks = kbase + static_cast<size_t>(kg < g.L ? kg : 0) * krow + 8 * kchunk;
-#pragma unroll
-    for (int pl = 0; pl < KPL; ++pl) dma16(ks + pl * k_plane, st + pl * R::TILE);
-    dma16(vbase + static_cast<size_t>(vg < g.L ? vg : 0) * krow + 8 * vchunk, st + KPL * R::TILE);
+    const int kg = kt * KT + dkey;
+    const uint32_t koff = __umul24(static_cast<uint32_t>(kg < g.L ? kg : 0), rowbytes);
+    dma16_at(kbase, koff + kcoff, st);
+    if constexpr (FUSED) dma16_at(klo, koff + kcoff, st + R::TILE);
+    uint32_t voff = koff;  // D = 128: the lane's V row is its K row
+    if constexpr (KT != 16) {
+      const int vg = kt * KT + drow;
+      voff = __umul24(static_cast<uint32_t>(vg < g.L ? vg : 0), rowbytes);
+    }
+    dma16_at(vbase, voff + vcoff, st + KPL * R::TILE);
   };
   // The first two tiles go out before the register loads. The compiler does not see the DMA
   // (inline asm) and counts only its own loads when it waits for them; vmcnt retires in issue
@@ -878,7 +886,10 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
       const bool grow = mloc > m_run + kMaxSlack;
       // every row sees key 0 in its first tile (L >= 1), so m_new is finite from tile 0 on
       const float m_new = grow ? mloc : m_run;
-      const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+      // rescale factor of what is accumulated: exactly 1 unless the max moved in some lane
+      const bool moved = __any(grow);
+      float corr = 1.0f;
+      if (moved) corr = __builtin_amdgcn_exp2f(m_run - m_new);
       half4 pb, pl;
       if constexpr (FUSED) {
         // P as hi + lo fp16 pair: the PV product sees P to ~22 bits, and the row sum is the
@@ -903,7 +914,7 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
       // l_run holds this lane's share of the row sum (its own keys); the four shares of a query
       // are combined once, after the last tile
       m_run = m_new;
-      if (__any(grow)) {
+      if (moved) {
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
       }
@@ -944,7 +955,9 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
       // lazy running max: moved only when a tile exceeds it by more than kMaxSlack
       const bool grow = mloc > m_run + kMaxSlack;
       const float m_new = grow ? mloc : m_run;
-      const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+      const bool moved = __any(grow);
+      float corr = 1.0f;
+      if (moved) corr = __builtin_amdgcn_exp2f(m_run - m_new);
       half8 pb, pl;
       if constexpr (FUSED) {
         float pf[8];
@@ -974,7 +987,7 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
         l_run = dot_ones(pb.lo, dot_ones(pb.hi, l_run * corr));
       }
       m_run = m_new;
-      if (__any(grow)) {
+      if (moved) {
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
       }
@@ -1150,6 +1163,12 @@ hipError_t launch_attention_f16(const AttnArgs& a, hipStream_t st) {
   shp.kv = make_div(static_cast<uint32_t>(a.KV));
   shp.hbn = make_div(static_cast<uint32_t>(shp.G >> shp.hsh));
   if (!geometry_fits(a.B, a.KV, shp.nwb, shp.G >> shp.hsh)) return hipErrorInvalidValue;
+  // K/V DMA offsets are 32-bit bytes inside one (batch row, kv head) plane, row * rowbytes by
+  // __umul24
+  const uint64_t rowbytes = static_cast<uint64_t>(a.KV) * a.D * 2;
+  if (static_cast<uint64_t>(a.S) * rowbytes >= (1ull << 32) || a.S >= (1 << 24) ||
+      rowbytes >= (1u << 24))
+    return hipErrorInvalidValue;
   const dim3 grid = sched_grid(a.B, a.KV, (shp.nwb + 3) / 4);
 
   const float sl2 = a.scale * kLog2e;

@@ -21,6 +21,17 @@ __device__ __forceinline__ void dma16(const void* src, _Float16* lds) {
                : "memory", "m0");
 }
 
+// The same DMA addressed as a wave-uniform 64-bit base (SGPR pair) plus a per-lane unsigned 32-bit
+// byte offset: the per-lane address arithmetic stays 32-bit.
+__device__ __forceinline__ void dma16_at(const void* base, uint32_t off, _Float16* lds) {
+  const unsigned addr = __builtin_amdgcn_readfirstlane(
+      static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_ptr_t)(lds))));
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(off), "s"(base), "s"(addr)
+               : "memory", "m0");
+}
+
 // s_waitcnt vmcnt(n), leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
