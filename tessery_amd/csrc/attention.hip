@@ -216,6 +216,26 @@ __device__ __forceinline__ Geom make_geom(const uint32_t* lengths, int B, int S,
   return g;
 }
 
+// Cross-row reductions with gfx950's VALU lane swaps: permlane16_swap(x, x) yields
+// (x[l & ~16], x[l | 16]) and permlane32_swap the same for lane bit 5, so both lanes of a pair
+// get op(pair) without going through the LDS crossbar.
+__device__ __forceinline__ float pair16(float x, bool take_max) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float a = __uint_as_float(p[0]), b = __uint_as_float(p[1]);
+  return take_max ? fmaxf(a, b) : a + b;
+}
+__device__ __forceinline__ float pair32(float x, bool take_max) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float a = __uint_as_float(p[0]), b = __uint_as_float(p[1]);
+  return take_max ? fmaxf(a, b) : a + b;
+}
+
+// The running max of a row moves only when a tile's max exceeds it by more than kMaxSlack (in
+// log2 units). Probabilities are then at most 2^kMaxSlack = 256, exact in range for fp16 P and
+// fp32 sums, and later tiles rarely pay the O rescale. The softmax is shift-invariant, so the
+// result does not depend on which max is used.
+constexpr float kMaxSlack = 8.0f;
+
 // ---------------------------------------------------------------------------------------------
 // fp32 MFMA kernel. v_mfma_f32_32x32x2_f32: A[i][k] from lane (i, k=l/32), B[k][j] from lane
 // (j, k=l/32), D[8a+4(l/32)+c][l%32] in acc[4a+c].
@@ -478,34 +498,40 @@ __global__ __launch_bounds__(256, 2) void attn_f32_ring(const float* __restrict_
       for (int t = 0; t < 4; ++t)
         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[t], qf[4 * c + t], s, 0, 0, 0);
     }
-    const bool full = kt * KT + KT <= g.limit_min;
+    // raw scores; keys at or past a row's limit are masked only in tiles that reach one
+    if (kt * KT + KT > g.limit_min) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (kt * KT + 8 * (e >> 2) + 4 * hh + (e & 3) >= limit) s[e] = -INFINITY;
+    }
     float mloc = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int key = kt * KT + 8 * (e >> 2) + 4 * hh + (e & 3);
-      float val = s[e] * scale_log2;
-      if (!full && key >= limit) val = -INFINITY;
-      s[e] = val;
-      mloc = fmaxf(mloc, val);
-    }
-    const float m_tile = fmaxf(mloc, __shfl_xor(mloc, 32));
-    const float m_new = fmaxf(m_run, m_tile);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+    for (int e = 0; e < 16; e += 2) mloc = fmaxf(mloc, fmaxf(s[e], s[e + 1]));
+    // the two lane halves hold the same query rows (keys 4 apart): one lane swap; the log2 scale
+    // is positive, so it commutes with the max
+    mloc = pair32(mloc, true) * scale_log2;
+    // lazy running max, as in the fp16 kernel; every row sees key 0 in its first tile
+    const bool grow = mloc > m_run + kMaxSlack;
+    const float m_new = grow ? mloc : m_run;
+    const bool moved = __any(grow);
+    float corr = 1.0f;
+    if (moved) corr = __builtin_amdgcn_exp2f(m_run - m_new);
     float lsum = 0.0f;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const float p = __builtin_amdgcn_exp2f(s[e] - m_use);
+      const float p = __builtin_amdgcn_exp2f(fmaf(s[e], scale_log2, -m_new));
       s[e] = p;
       lsum += p;
     }
-    lsum += __shfl_xor(lsum, 32);
-    l_run = l_run * corr + lsum;
+    // this lane's share of the row sum (its keys); the two halves are added after the last tile
+    l_run = fmaf(l_run, corr, lsum);
     m_run = m_new;
+    if (moved) {
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
+      for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) o[dt][e] *= corr;
+        for (int e = 0; e < 16; ++e) o[dt][e] *= corr;
+    }
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int row = vrow32<D>(8 * (e >> 2) + 4 * hh + (e & 3));
@@ -525,8 +551,8 @@ __global__ __launch_bounds__(256, 2) void attn_f32_ring(const float* __restrict_
   }
   wait_vmcnt<0>();  // no DMA may land in this workgroup's LDS after it exits
 
+  const float inv = 1.0f / pair32(l_run, false);
   if (qvalid) {
-    const float inv = 1.0f / l_run;
     const size_t base = ((static_cast<size_t>(g.b) * S + qpos) * H + g.head) * D;
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
@@ -612,19 +638,6 @@ __device__ __forceinline__ half4 lds_read_tr(const _Float16* p) {
   return __builtin_bit_cast(half4, v);
 }
 
-// Cross-row reductions with gfx950's VALU lane swaps: permlane16_swap(x, x) yields
-// (x[l & ~16], x[l | 16]) and permlane32_swap the same for lane bit 5, so both lanes of a pair
-// get op(pair) without going through the LDS crossbar.
-__device__ __forceinline__ float pair16(float x, bool take_max) {
-  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  const float a = __uint_as_float(p[0]), b = __uint_as_float(p[1]);
-  return take_max ? fmaxf(a, b) : a + b;
-}
-__device__ __forceinline__ float pair32(float x, bool take_max) {
-  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  const float a = __uint_as_float(p[0]), b = __uint_as_float(p[1]);
-  return take_max ? fmaxf(a, b) : a + b;
-}
 // acc + sum of four fp16 values, exact (v_dot2_f32_f16 against ones)
 __device__ __forceinline__ float dot_ones(half4 p, float acc) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -691,11 +704,6 @@ struct F16Ring {
 // K_hi*Q_lo + K_lo*Q_hi + K_hi*Q_hi in fp32: q and k enter the dot products at ~22 bits. P is
 // split the same way (P_hi*V + P_lo*V), so the only fp16 roundings left are those of the inputs.
 // ---------------------------------------------------------------------------------------------
-// The running max of a row moves only when a tile's max exceeds it by more than kMaxSlack (in
-// log2 units). Probabilities are then at most 2^kMaxSlack = 256, exact in range for fp16 P and
-// fp32 sums, and later tiles rarely pay the O rescale. The softmax is shift-invariant, so the
-// result does not depend on which max is used.
-constexpr float kMaxSlack = 8.0f;
 
 template <int D, typename TOut, bool FUSED>
 __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
