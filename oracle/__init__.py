@@ -12,10 +12,13 @@ Modules and what pins each one (the tests under tests/test_oracle_*.py run these
   norm_rope   per-head RMSNorm and split-half RoPE. Pinned by torch.nn.functional.rms_norm,
               transformers' Qwen3RMSNorm / apply_rotary_pos_emb, a complex-number rotation and
               rotation invariants.
-  quant4      uint4 group-64 packing, dequantization and projection. Pinned by tessery's
-              known-answer tests (test_kernels.py:55-81, 759-776) and a scalar restatement of
-              the kernel indexing (kernels.metal:11-19).
-  qwen_block  composition QKV projection -> q/k norm + RoPE -> attention (qwen3.py:194-245),
-              pinned through the three modules above.
+  quant4      uint4 group-64 packing, dequantization and projection, silu_gate and the fused
+              gate/up projection. Pinned by tessery's known-answer tests (test_kernels.py:55-81,
+              286-294, 759-776, 842-857), a scalar restatement of the kernel indexing
+              (kernels.metal:11-19), torch's silu and transformers' Qwen3MLP.
+  qwen_block  compositions of the Qwen3 layer: QKV projection -> q/k norm + RoPE -> attention
+              (qwen3.py:194-245), pinned through the modules above, and the layer tail o_proj ->
+              residual -> RMSNorm -> gate/up + SiLU -> down -> residual (qwen3.py:246-280), pinned
+              against torch's rms_norm and transformers' Qwen3MLP.
 No function here is "parity unpinned".
 """

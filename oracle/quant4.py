@@ -59,3 +59,18 @@ def weight4_scalar(packed: NDArray, scales: NDArray, biases: NDArray, row: int, 
     s = decode_words(np.asarray(scales).reshape(-1)[g : g + 1], kind)[0]
     b = decode_words(np.asarray(biases).reshape(-1)[g : g + 1], kind)[0]
     return code * s + b
+
+
+def silu_gate(gate: NDArray, up: NDArray) -> NDArray[np.float64]:
+    """silu(gate) * up = gate / (1 + exp(-gate)) * up (kernels.metal:334-337), float64."""
+    g = np.asarray(gate, dtype=np.float64)
+    with np.errstate(over="ignore"):
+        return g / (1.0 + np.exp(-g)) * np.asarray(up, dtype=np.float64)
+
+
+def gated4(x: NDArray, gate: tuple[NDArray, NDArray, NDArray], up: tuple[NDArray, NDArray, NDArray],
+           kind: str = "bf16") -> NDArray[np.float64]:
+    """silu(x @ Wg^T) * (x @ Wu^T) with (packed, scales, biases) weight sets (metal.py:501-530,
+    kernels.metal:609-656)."""
+    return silu_gate(linear4(x, *gate, kind=kind), linear4(x, *up, kind=kind))
+

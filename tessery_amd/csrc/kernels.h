@@ -52,6 +52,14 @@ hipError_t launch_norm_rope_f16(const _Float16* x, _Float16* y, const uint16_t* 
 hipError_t launch_linear4_f32(const float* x, const uint32_t* w, const uint16_t* scales,
                               const uint16_t* biases, float* out, int row0, int row1, int cols,
                               int k, hipStream_t st);
+// Gate and up projections of rows [row0, row1) with out = silu(gate) * up (tessery gated4,
+// kernels.metal:609-656, 687-731), bit-identical to linear4 + linear4 + silu_gate.
+hipError_t launch_gated4_f32(const float* x, const uint32_t* w, const uint16_t* scales,
+                             const uint16_t* biases, const uint32_t* uw, const uint16_t* uscales,
+                             const uint16_t* ubiases, float* out, int row0, int row1, int cols,
+                             int k, hipStream_t st);
+// gate[i] = silu(gate[i]) * up[i] for i < n (tessery silu_gate, kernels.metal:334-337).
+hipError_t launch_silu_gate_f32(float* gate, const float* up, uint32_t n, hipStream_t st);
 
 // Fused uint4 QKV projection for fp16 activations: three weight sets, outputs written in the
 // attention layout. scale/bias words are fp16 (scale_bf16 = 0) or bf16 (scale_bf16 = 1).

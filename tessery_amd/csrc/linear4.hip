@@ -8,21 +8,73 @@
 // linear4_f32 serves every tessery linear4 route name (linear4, linear4_tiled, linear4_tail,
 // linear4_16x32_k64, linear4_32x32_k64, linear4_small3): one kernel, one reduction order per
 // output element, so every route over the same rows produces bit-identical results.
+//
+// gated4_f32 is the same kernel run over two weight sets (gate and up) with the SwiGLU epilogue
+// out = silu(gate) * up (kernels.metal:609-656, 687-731); each projection keeps the linear4
+// reduction order and the epilogue is silu_gate's expression, so the fused routes are
+// bit-identical to linear4 + linear4 + silu_gate over the same rows.
 #include "common.h"
 #include "kernels.h"
 
 namespace tessery {
 
+// silu(g) * u as tessery's silu_gate computes it (kernels.metal:334-337)
+__device__ __forceinline__ float silu_times(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+// The 32 dequantized weights of lane (column n, k-slot h) for group gi: w = code * scale + bias in
+// fp32, codes 32h .. 32h + 31 of the group (zero for columns past the end).
+__device__ __forceinline__ void decode_group(const uint32_t* __restrict__ w,
+                                             const uint16_t* __restrict__ scales,
+                                             const uint16_t* __restrict__ biases, int n, bool nvalid,
+                                             int k, int gi, int hh, float (&wv)[32]) {
+  if (nvalid) {
+    const uint4v words =
+        *reinterpret_cast<const uint4v*>(w + static_cast<size_t>(n) * (k / 8) + gi * 8 + 4 * hh);
+    const size_t gidx = static_cast<size_t>(n) * (k / 64) + gi;
+    const float sc = bf16_to_float(scales[gidx]), bi = bf16_to_float(biases[gidx]);
+#pragma unroll
+    for (int t = 0; t < 32; ++t)
+      wv[t] = static_cast<float>((words[t >> 3] >> (4 * (t & 7))) & 15u) * sc + bi;
+  } else {
+#pragma unroll
+    for (int t = 0; t < 32; ++t) wv[t] = 0.0f;
+  }
+}
+
+// Two independent 32-product partial sums per group, added to the total: the K32 partial
+// accumulation of tessery's tiled kernels (kernels.metal:500-518), which bounds the rounding
+// growth over long K.
+__device__ __forceinline__ void group_product(const float* xs, int xrow, int l32, int hh,
+                                              const float (&wv)[32], floatx16& acc) {
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    floatx16 part;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) part[e] = 0.0f;
+#pragma unroll
+    for (int c4 = 4 * half; c4 < 4 * half + 4; ++c4) {
+      const floatx4 xa = *reinterpret_cast<const floatx4*>(&xs[l32 * xrow + 32 * hh + 4 * c4]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        part = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[t], wv[4 * c4 + t], part, 0, 0, 0);
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] += part[e];
+  }
+}
+
 // 256 threads = 4 wavefronts; tile 32 rows x 128 columns (32 columns per wavefront); the K loop
 // walks one quantization group (64) at a time. fp32 MFMA v_mfma_f32_32x32x2_f32 computes
 // Y = X * W^T with lane (column n = l%32, k-slot h = l/32); k-step t pairs k = 32h + t, so each
 // lane decodes 32 consecutive codes (four words) of its weight row per group.
-__global__ __launch_bounds__(256) void linear4_f32(const float* __restrict__ x,
-                                                   const uint32_t* __restrict__ w,
-                                                   const uint16_t* __restrict__ scales,
-                                                   const uint16_t* __restrict__ biases,
-                                                   float* __restrict__ out, int row0, int row1,
-                                                   int cols, int k) {
+// GATED: a second weight set (uw, us, ub) accumulates the up projection beside the gate.
+template <bool GATED>
+__global__ __launch_bounds__(256) void linear4_f32(
+    const float* __restrict__ x, const uint32_t* __restrict__ w,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    const uint32_t* __restrict__ uw, const uint16_t* __restrict__ uscales,
+    const uint16_t* __restrict__ ubiases, float* __restrict__ out, int row0, int row1, int cols,
+    int k) {
   constexpr int XROW = 64 + 4;
   __shared__ __attribute__((aligned(16))) float xs[32 * XROW];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
@@ -30,9 +82,12 @@ __global__ __launch_bounds__(256) void linear4_f32(const float* __restrict__ x,
   const int n = blockIdx.y * 128 + wave * 32 + l32;
   const bool nvalid = n < cols;
   const int groups = k / 64;
-  floatx16 acc;
+  floatx16 acc, uacc;
 #pragma unroll
-  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+  for (int e = 0; e < 16; ++e) {
+    acc[e] = 0.0f;
+    uacc[e] = 0.0f;
+  }
   for (int gi = 0; gi < groups; ++gi) {
     __syncthreads();
 #pragma unroll
@@ -46,43 +101,25 @@ __global__ __launch_bounds__(256) void linear4_f32(const float* __restrict__ x,
     }
     __syncthreads();
     float wv[32];
-    if (nvalid) {
-      const uint4v words =
-          *reinterpret_cast<const uint4v*>(w + static_cast<size_t>(n) * (k / 8) + gi * 8 + 4 * hh);
-      const size_t gidx = static_cast<size_t>(n) * groups + gi;
-      const float sc = bf16_to_float(scales[gidx]), bi = bf16_to_float(biases[gidx]);
-#pragma unroll
-      for (int t = 0; t < 32; ++t)
-        wv[t] = static_cast<float>((words[t >> 3] >> (4 * (t & 7))) & 15u) * sc + bi;
-    } else {
-#pragma unroll
-      for (int t = 0; t < 32; ++t) wv[t] = 0.0f;
-    }
-    // Two independent 32-product partial sums per group, added to the total: the K32 partial
-    // accumulation of tessery's tiled kernels (kernels.metal:500-518), which bounds the rounding
-    // growth over long K.
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      floatx16 part;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) part[e] = 0.0f;
-#pragma unroll
-      for (int c4 = 4 * half; c4 < 4 * half + 4; ++c4) {
-        const floatx4 xa = *reinterpret_cast<const floatx4*>(&xs[l32 * XROW + 32 * hh + 4 * c4]);
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          part = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[t], wv[4 * c4 + t], part, 0, 0, 0);
-      }
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[e] += part[e];
+    decode_group(w, scales, biases, n, nvalid, k, gi, hh, wv);
+    group_product(xs, XROW, l32, hh, wv, acc);
+    if constexpr (GATED) {
+      decode_group(uw, uscales, ubiases, n, nvalid, k, gi, hh, wv);
+      group_product(xs, XROW, l32, hh, wv, uacc);
     }
   }
   if (!nvalid) return;
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     const int r = rbase + 8 * (e >> 2) + 4 * hh + (e & 3);
-    if (r < row1) out[static_cast<size_t>(r) * cols + n] = acc[e];
+    if (r < row1) out[static_cast<size_t>(r) * cols + n] = GATED ? silu_times(acc[e], uacc[e]) : acc[e];
   }
+}
+
+__global__ __launch_bounds__(256) void silu_gate_f32(float* __restrict__ gate,
+                                                     const float* __restrict__ up, uint32_t n) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i < n) gate[i] = silu_times(gate[i], up[i]);
 }
 
 hipError_t launch_linear4_f32(const float* x, const uint32_t* w, const uint16_t* scales,
@@ -91,7 +128,26 @@ hipError_t launch_linear4_f32(const float* x, const uint32_t* w, const uint16_t*
   if (row1 <= row0 || cols <= 0) return hipSuccess;
   if (k % 64) return hipErrorInvalidValue;
   dim3 grid((row1 - row0 + 31) / 32, (cols + 127) / 128);
-  linear4_f32<<<grid, 256, 0, st>>>(x, w, scales, biases, out, row0, row1, cols, k);
+  linear4_f32<false><<<grid, 256, 0, st>>>(x, w, scales, biases, nullptr, nullptr, nullptr, out,
+                                           row0, row1, cols, k);
+  return hipGetLastError();
+}
+
+hipError_t launch_gated4_f32(const float* x, const uint32_t* w, const uint16_t* scales,
+                             const uint16_t* biases, const uint32_t* uw, const uint16_t* uscales,
+                             const uint16_t* ubiases, float* out, int row0, int row1, int cols,
+                             int k, hipStream_t st) {
+  if (row1 <= row0 || cols <= 0) return hipSuccess;
+  if (k % 64) return hipErrorInvalidValue;
+  dim3 grid((row1 - row0 + 31) / 32, (cols + 127) / 128);
+  linear4_f32<true><<<grid, 256, 0, st>>>(x, w, scales, biases, uw, uscales, ubiases, out, row0,
+                                          row1, cols, k);
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_gate_f32(float* gate, const float* up, uint32_t n, hipStream_t st) {
+  if (!n) return hipSuccess;
+  silu_gate_f32<<<(n + 255) / 256, 256, 0, st>>>(gate, up, n);
   return hipGetLastError();
 }
 

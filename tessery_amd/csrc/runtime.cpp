@@ -47,6 +47,9 @@ enum Route : int {
   R_LINEAR4_32X32,
   R_LINEAR4_SMALL3,
   R_QKV4_F16,
+  R_GATED4_16X32,
+  R_GATED4_8X32,
+  R_SILU_GATE,
   R_ADD,
   R_COPY,
   R_NONE
@@ -76,6 +79,9 @@ const RouteName kRoutes[] = {
     {"linear4_32x32_k64", R_LINEAR4_32X32, 5},
     {"linear4_small3", R_LINEAR4_SMALL3, 5},
     {"qkv4_f16", R_QKV4_F16, 7},
+    {"gated4_16x32_k64", R_GATED4_16X32, 8},
+    {"gated4_8x32", R_GATED4_8X32, 8},
+    {"silu_gate", R_SILU_GATE, 2},
     {"add", R_ADD, 3},
     {"copy", R_COPY, 2},
 };
@@ -258,6 +264,26 @@ bool linear4_range(Route r, const Params& p, uint64_t threads, uint32_t group, R
   return out->r0 < out->r1;
 }
 
+// Rows of a fused gate/up launch: gated4_16x32_k64 runs 16-row tiles from row 0
+// (kernels.metal:609-616), gated4_8x32 one complete 8-row tile from row n (kernels.metal:687-694).
+bool gated4_range(Route r, const Params& p, uint64_t threads, uint32_t group, RowRange* out) {
+  const uint64_t rows = p.rows, cols = p.cols, k = p.k, n = p.n;
+  if (!rows || !cols || !k || k % 64 || cols % 32 || rows > kMaxTokens || cols > 65536 ||
+      k > 65536)
+    return false;
+  if (r == R_GATED4_16X32) {
+    const uint64_t per = (cols / 32) * 256;
+    if (group != 256 || threads % per) return false;
+    out->r0 = 0;
+    out->r1 = 16 * (threads / per);
+  } else {
+    if (group != 128 || threads != (cols / 32) * 128) return false;
+    out->r0 = n;
+    out->r1 = n + 8;
+  }
+  return out->r0 < out->r1 && out->r1 <= rows;
+}
+
 // Validates one launch against the buffer sizes it would touch. Pure: no allocation.
 bool validate(Route r, const Params& p, uint64_t threads, uint32_t group, const uint64_t* sz,
               uint32_t count, uint32_t nbuf) {
@@ -322,6 +348,19 @@ bool validate(Route r, const Params& p, uint64_t threads, uint32_t group, const 
       return sz[0] >= M * K * 2 && sz[1] >= ntot * (K / 8) * 4 && sz[2] >= ntot * (K / 64) * 2 &&
              sz[3] >= ntot * (K / 64) * 2 && sz[4] >= M * nq * 2 && sz[5] >= M * nkv * 2 &&
              sz[6] >= M * nkv * 2;
+    }
+    case R_GATED4_16X32:
+    case R_GATED4_8X32: {  // buffers: x, w, s, b, up w, up s, up b, out
+      RowRange rr;
+      if (!gated4_range(r, p, threads, group, &rr)) return false;
+      const uint64_t cols = p.cols, k = p.k;
+      const uint64_t wb = cols * (k / 8) * 4, sb = cols * (k / 64) * 2;
+      return sz[0] >= rr.r1 * k * 4 && sz[1] >= wb && sz[2] >= sb && sz[3] >= sb &&
+             sz[4] >= wb && sz[5] >= sb && sz[6] >= sb && sz[7] >= rr.r1 * cols * 4;
+    }
+    case R_SILU_GATE: {  // kernels.metal:334-337: gate, up
+      const uint64_t n = p.n;
+      return n && n <= (1ull << 32) - 256 && sz[0] >= n * 4 && sz[1] >= n * 4;
     }
     case R_ADD: {  // kernels.metal:300-304
       const uint64_t n = p.n;
@@ -486,6 +525,21 @@ hipError_t launch(Runtime* rt, const Op& op) {
       a.scale_bf16 = p.u1 & 1u;
       return tessery::launch_qkv4_f16(a, st);
     }
+    case R_GATED4_16X32:
+    case R_GATED4_8X32: {
+      RowRange rr;
+      if (!gated4_range(op.route, p, op.threads, op.group, &rr)) return hipErrorInvalidValue;
+      return tessery::launch_gated4_f32(
+          static_cast<const float*>(op.ptr[0]), static_cast<const uint32_t*>(op.ptr[1]),
+          static_cast<const uint16_t*>(op.ptr[2]), static_cast<const uint16_t*>(op.ptr[3]),
+          static_cast<const uint32_t*>(op.ptr[4]), static_cast<const uint16_t*>(op.ptr[5]),
+          static_cast<const uint16_t*>(op.ptr[6]), static_cast<float*>(op.ptr[7]),
+          static_cast<int>(rr.r0), static_cast<int>(rr.r1), static_cast<int>(p.cols),
+          static_cast<int>(p.k), st);
+    }
+    case R_SILU_GATE:
+      return tessery::launch_silu_gate_f32(static_cast<float*>(op.ptr[0]),
+                                           static_cast<const float*>(op.ptr[1]), p.n, st);
     case R_ADD:
       return tessery::launch_add_f32(static_cast<const float*>(op.ptr[0]),
                                      static_cast<const float*>(op.ptr[1]),

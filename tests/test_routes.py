@@ -82,3 +82,36 @@ def test_large_tile_partition(rows, cols, k, selected):
             regions.append((start, end))
         assert regions[0][0] == 0 and regions[-1][1] == rows
         assert all(a[1] == b[0] for a, b in zip(regions[:-1], regions[1:]))
+
+
+GATED_CASES = [(m, 3072, 1024) for m in (7, 16, 23, 24, 25, 48, 127, 128, 129, 159, 160, 161, 255,
+                                         256, 257, 511, 512, 513, 4096)]
+GATED_CASES += [(m, n, k) for m in (24, 128, 160) for n, k in ((1024, 1024), (3072, 2048), (3071, 1024))]
+
+
+@pytest.mark.parametrize("rows,cols,k", GATED_CASES)
+def test_gated_projection_guard_and_buffer_binding(rows, cols, k):
+    """The fused gate/up selection and buffer binding of tessery's
+    test_runtime_loading.py:167-218 (metal.py:501-530)."""
+    calls = []
+    fake = SimpleNamespace(
+        _dispatch=lambda *a, **kw: calls.append(("dispatch", a, kw)),
+        _linear4=lambda *a, **kw: calls.append(("linear", a, kw)),
+    )
+    buffers = [object() for _ in range(9)]
+    HipRuntime._gated4(fake, buffers, rows=rows, cols=cols, k=k)
+    if rows in (16, 24, 128, 160, 256, 512) and (cols, k) == (3072, 1024):
+        assert len(calls) == (2 if rows == 24 else 1)
+        assert calls[0][1] == ("gated4_16x32_k64", buffers[:8])
+        assert calls[0][2] == dict(threads=rows // 16 * (cols // 32) * 256, group_size=256,
+                                   rows=rows, cols=cols, k=k)
+        if rows == 24:
+            assert calls[1][1] == ("gated4_8x32", buffers[:8])
+            assert calls[1][2] == dict(threads=(cols // 32) * 128, group_size=128, n=16,
+                                       rows=rows, cols=cols, k=k)
+    else:
+        assert [c[0] for c in calls] == ["linear", "linear", "dispatch"]
+        assert calls[0][1][0] == [*buffers[:4], buffers[7]]
+        assert calls[1][1][0] == [buffers[0], *buffers[4:7], buffers[8]]
+        assert calls[2][1] == ("silu_gate", buffers[7:])
+        assert calls[2][2] == dict(threads=rows * cols, n=rows * cols)
