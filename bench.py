@@ -16,6 +16,8 @@ HIP-event timings, and the float64 NumPy CPU oracle timed on the host on a bound
                     lengths U{2..512} (seed 2), 12 layers, route attention_tiled
   qwen_qkv4_16x256  uint4 QKV projection (x [4096,1024] fp16) -> k norm+RoPE -> fused attention,
                     lengths U{1..256} (seed 5), 8 layers
+  qwen_tail_16x256  the rest of the Qwen3 layer on 4096 tokens, fp32 activations: o_proj ->
+                    residual -> RMSNorm -> gate/up + SiLU -> down -> residual, 4 layers
 """
 
 from __future__ import annotations
@@ -412,6 +414,112 @@ def bench_qkv4_block(args) -> dict:
     }
 
 
+def qwen_tail_launch(rt: HipRuntime, s: dict, tokens: int, hidden: int, width: int,
+                     inter: int) -> None:
+    """qwen3.py:246-280: h = x + o_proj(attended); out = h + down(gated4(rms_norm(h)))."""
+    n = tokens * hidden
+    rt._linear4([s["att"], *s["o"], s["proj"]], rows=tokens, cols=hidden, k=width)
+    rt._dispatch("add", [s["x"], s["proj"], s["h"]], threads=n, n=n)
+    rt._dispatch("rms_norm", [s["h"], s["post_norm"], s["norm"]], threads=tokens * 32,
+                 group_size=32, cols=hidden, eps=workloads.EPS)
+    rt._gated4([s["norm"], *s["gate"], *s["up"], s["g"], s["u"]], rows=tokens, cols=inter,
+               k=hidden)
+    rt._linear4([s["g"], *s["down"], s["proj"]], rows=tokens, cols=hidden, k=inter)
+    rt._dispatch("add", [s["h"], s["proj"], s["out"]], threads=n, n=n)
+
+
+def bench_qwen_tail(args) -> dict:
+    """Qwen3 layer tail on 16x256 tokens (fp32 activations, uint4 bf16-affine weights), 4
+    independent layers: o_proj, residual, post-attention RMSNorm, gate/up + SiLU, down, residual."""
+    layers, tokens, hidden, width, inter = 4, 16 * 256, 1024, 2048, 3072
+    flop = workloads.tail_flop(tokens, hidden, width, inter)
+    log(f"workload qwen_tail_16x256: T={tokens} hidden={hidden} attn={width} inter={inter}")
+    with HipRuntime() as rt:
+        host = [workloads.qwen_tail_16x256(layer) for layer in range(layers)]
+        sets = []
+        for d in host:
+            s = {"x": rt.upload(d["x"]), "att": rt.upload(d["attended"]),
+                 "post_norm": rt.upload(d["post_norm"])}
+            for name in ("o", "gate", "up", "down"):
+                s[name] = [rt.upload(a) for a in d[name]]
+            for name, width_ in (("proj", hidden), ("h", hidden), ("norm", hidden), ("out", hidden),
+                                 ("g", inter), ("u", inter)):
+                s[name] = rt.buffer(tokens * width_ * 4)
+            sets.append(s)
+
+        def step():
+            for s in sets:
+                qwen_tail_launch(rt, s, tokens, hidden, width, inter)
+
+        launches = 8 * layers
+        t = run_timed(rt, step, args.steps, args.warmup, launches)
+        out0 = rt.read(sets[0]["out"], (tokens, hidden))
+    step_s = t["step"]
+    ks = t["kernel_s"]
+    # the four projections all run the linear4 kernel (route linear4_16x32_k64 at 4096 rows)
+    gemm_s = 4 * ks["linear4_16x32_k64"]
+    tflops = flop / gemm_s / 1e12
+    gemm_bytes = tokens * (width + hidden + hidden + 2 * inter + inter) * 4 + (
+        (hidden * width + 2 * inter * hidden + hidden * inter) // 2)
+    result = {
+        "metric": "Qwen3 layer tail (o_proj, RMSNorm, gated MLP) tokens/s, 16x256, 1 GPU",
+        "value": tokens * layers / step_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_s * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "qwen_tail_16x256: o_proj -> residual -> RMSNorm -> gate/up+SiLU "
+                               "-> down -> residual", "tokens": tokens, "hidden": hidden,
+                   "attention_width": width, "intermediate": inter, "layers": layers},
+        "tflops": flop * layers / step_s / 1e12,
+        "kernel_us": {k: v * 1e6 for k, v in ks.items()},
+        "roofline": {
+            "bound": "mfma",
+            "achieved": tflops,
+            "peak": PEAK_F32_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": tflops / PEAK_F32_TFLOPS,
+            "traffic": None,
+            "algorithmic_flop": flop,
+            "algorithmic_bytes": gemm_bytes,
+            "kernel": "linear4_16x32_k64",
+        },
+    }
+    if not args.no_cpu_baseline:
+        from oracle import qwen_block
+
+        sample = 512
+        d = host[0]
+
+        def layer():
+            return qwen_block.layer_tail(d["x"][:sample], d["attended"][:sample],
+                                         {n: d[n] for n in ("o", "gate", "up", "down")},
+                                         workloads.bf16_values(d["post_norm"]), eps=workloads.EPS)
+
+        expected, per_sample, runs = time_cpu(layer)
+        result["cpu_baseline"] = {
+            "value": sample / per_sample,
+            "unit": "tokens/s",
+            "cores": len(os.sched_getaffinity(0)),
+            "blas_threads": blas_threads(),
+            "kind": "port",
+            "sample": f"{sample} of {tokens} tokens of layer 0, float64 NumPy oracle, median of "
+                      f"{runs} runs; {per_sample * 1e3:.1f} ms",
+        }
+        err = np.abs(out0[:sample].astype(np.float64) - expected)
+        result["max_abs_err_layer0"] = float(err.max())
+        result["max_rel_err_layer0"] = float(err.max() / np.abs(expected).max())
+    else:
+        result["cpu_baseline"] = None
+    return result
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__,
                                      formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -420,7 +528,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--layers", type=int, default=LAYERS, help="headline workload only")
     parser.add_argument("--workload", default="qwen3_32x512",
-                        choices=["qwen3_32x512", "qwen3_8x512", "bge_32x512", "qwen_qkv4_16x256"])
+                        choices=["qwen3_32x512", "qwen3_8x512", "bge_32x512", "qwen_qkv4_16x256",
+                                 "qwen_tail_16x256"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="also launch one copy of this many MiB (traffic-counter calibration)")
@@ -443,6 +552,8 @@ def main() -> int:
                             headline=False)
     elif args.workload == "bge_32x512":
         result = bench_bge(args)
+    elif args.workload == "qwen_tail_16x256":
+        result = bench_qwen_tail(args)
     else:
         result = bench_qkv4_block(args)
     print(json.dumps(result), flush=True)

@@ -15,6 +15,8 @@ words (truncated, the encoding tessery's own tests use, test_kernels.py:22-23).
 
 from __future__ import annotations
 
+from typing import Any
+
 import math
 from dataclasses import dataclass
 
@@ -132,6 +134,42 @@ def qwen_qkv4_16x256(seed: int = 5) -> tuple[Shape, NDArray[np.uint32], dict[str
     gk = bf16_words(rng.uniform(0.5, 1.5, shape.dim))
     return shape, lengths, {"x": x, "w": packed, "s": scales, "b": biases,
                             "q_norm": gq, "k_norm": gk}
+
+
+def weight4_set(rng: np.random.Generator, n: int, k: int, scale: float) -> tuple[NDArray, ...]:
+    """weight4 words [n, k/8] with codes U{0..15}, bf16 group-64 scale s = U(0.5,1.5)*scale and
+    bias -(7.5 + U(-0.5,0.5))*s, so weights are near zero-mean like an affine-quantized layer (the
+    reference's bf16 storage, qwen3.py:70-73)."""
+    codes = rng.integers(0, 16, size=(n, k), dtype=np.uint32)
+    packed = np.zeros((n, k // 8), dtype=np.uint32)
+    for j in range(8):
+        packed |= codes[:, j::8] << np.uint32(4 * j)
+    s = rng.uniform(0.5, 1.5, size=(n, k // 64)) * scale
+    biases = bf16_words(-(7.5 + rng.uniform(-0.5, 0.5, size=s.shape)) * s)
+    return packed, bf16_words(s), biases
+
+
+def qwen_tail_16x256(layer: int, seed: int = 6) -> dict[str, Any]:
+    """Qwen3-0.6B layer tail (qwen3.py:246-280) on 16*256 tokens, fp32 activations: residual x
+    [4096, 1024] ~ N(0,1), attention output [4096, 2048] ~ N(0, 0.25), o_proj 2048->1024,
+    gate/up 1024->3072, down 3072->1024 as weight4 with bf16 scale/bias, post-attention
+    RMSNorm weight U(0.5,1.5) (bf16 words). One independent set per layer."""
+    rng = np.random.default_rng((seed, layer))
+    tokens, hidden, width, inter = 16 * 256, 1024, 2048, 3072
+    return {
+        "x": normal(rng, (tokens, hidden), np.float32),
+        "attended": (0.5 * normal(rng, (tokens, width), np.float32)).astype(np.float32),
+        "o": weight4_set(rng, hidden, width, 0.01),
+        "gate": weight4_set(rng, inter, hidden, 0.01),
+        "up": weight4_set(rng, inter, hidden, 0.01),
+        "down": weight4_set(rng, hidden, inter, 0.01),
+        "post_norm": bf16_words(rng.uniform(0.5, 1.5, hidden)),
+    }
+
+
+def tail_flop(tokens: int, hidden: int, width: int, inter: int) -> int:
+    """2*T*K*N over the four projections of the layer tail (o, gate, up, down)."""
+    return 2 * tokens * (width * hidden + 2 * hidden * inter + inter * hidden)
 
 
 def qkv4_flop(rows: int, k: int, n_total: int) -> int:
