@@ -20,5 +20,8 @@ Modules and what pins each one (the tests under tests/test_oracle_*.py run these
               (qwen3.py:194-245), pinned through the modules above, and the layer tail o_proj ->
               residual -> RMSNorm -> gate/up + SiLU -> down -> residual (qwen3.py:246-280), pinned
               against torch's rms_norm and transformers' Qwen3MLP.
+  bert_block  the BERT (BGE) encoder layer (bert.py:186-230): fp32 projections with bias, GELU,
+              LayerNorm and bidirectional attention. Pinned against torch's gelu / layer_norm,
+              math.erf and transformers' BertLayer in float64 with a key-padding mask.
 No function here is "parity unpinned".
 """

@@ -1,0 +1,178 @@
+// fp32 dense projections and elementwise kernels of tessery's BERT (BGE) layer on gfx950.
+//
+// matmul_f32<BIAS>: out[r][n] = sum_k a[r][k] * bt[n][k] (+ bias[n]) for rows [row0, row1), any
+// K and N: the matmul_f32 / matmul_f32_tiled / matmul_f32_chunk32 / matmul_bias_f32 /
+// matmul_bias_f32_chunk32 routes (kernels.metal:306-322, 396-487). Weights stay [N, K] as in the
+// reference ("transposed weight"). Products accumulate in K32 partial sums added to the total
+// (the chunk32 order, kernels.metal:416-436), every route runs this one kernel, and the bias is
+// added once after the last partial sum.
+// add_bias, gelu_f32 and layer_norm follow kernels.metal:362-394.
+#include "common.h"
+#include "kernels.h"
+
+namespace tessery {
+
+// 256 threads = 4 wavefronts; tile 32 rows x 128 columns (32 per wavefront); the K loop walks
+// 64 columns at a time. v_mfma_f32_32x32x2_f32 with lane (column n = l%32, k-slot h = l/32):
+// k-step t of a 32-wide half pairs k = 32h + t, so each lane holds 32 consecutive weights of its
+// row per 64-column chunk. Columns past K and rows / weight rows past their ends read as zero.
+template <bool BIAS>
+__global__ __launch_bounds__(256) void matmul_f32(const float* __restrict__ a,
+                                                  const float* __restrict__ bt,
+                                                  const float* __restrict__ bias,
+                                                  float* __restrict__ out, int row0, int row1,
+                                                  int cols, int k) {
+  constexpr int XROW = 64 + 4;
+  __shared__ __attribute__((aligned(16))) float xs[32 * XROW];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int rbase = row0 + blockIdx.x * 32;
+  const int n = blockIdx.y * 128 + wave * 32 + l32;
+  const bool nvalid = n < cols;
+  const bool vec = (k & 3) == 0;  // rows start 16-byte aligned: float4 loads
+  const int chunks = (k + 63) / 64;
+  floatx16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+  for (int ci = 0; ci < chunks; ++ci) {
+    const int k0 = ci * 64;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + 256 * i;  // 512 four-float chunks = 32 rows x 16
+      const int r = c / 16, kk = k0 + 4 * (c % 16);
+      floatx4 t = {0.f, 0.f, 0.f, 0.f};
+      if (rbase + r < row1) {
+        const float* src = a + static_cast<size_t>(rbase + r) * k + kk;
+        if (vec && kk + 4 <= k) {
+          t = *reinterpret_cast<const floatx4*>(src);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) t[j] = kk + j < k ? src[j] : 0.0f;
+        }
+      }
+      *reinterpret_cast<floatx4*>(&xs[r * XROW + 4 * (c % 16)]) = t;
+    }
+    __syncthreads();
+    float wv[32];
+    {
+      const int kw = k0 + 32 * hh;
+      const float* src = bt + static_cast<size_t>(n) * k + kw;
+      if (nvalid && vec && kw + 32 <= k) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const floatx4 t = *reinterpret_cast<const floatx4*>(src + 4 * j);
+          wv[4 * j] = t[0];
+          wv[4 * j + 1] = t[1];
+          wv[4 * j + 2] = t[2];
+          wv[4 * j + 3] = t[3];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) wv[j] = nvalid && kw + j < k ? src[j] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      floatx16 part;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) part[e] = 0.0f;
+#pragma unroll
+      for (int c4 = 4 * half; c4 < 4 * half + 4; ++c4) {
+        const floatx4 xa = *reinterpret_cast<const floatx4*>(&xs[l32 * XROW + 32 * hh + 4 * c4]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          part = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[t], wv[4 * c4 + t], part, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] += part[e];
+    }
+  }
+  if (!nvalid) return;
+  const float b = BIAS ? bias[n] : 0.0f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int r = rbase + 8 * (e >> 2) + 4 * hh + (e & 3);
+    if (r < row1) out[static_cast<size_t>(r) * cols + n] = BIAS ? acc[e] + b : acc[e];
+  }
+}
+
+// x[i] += bias[i % cols] (kernels.metal:376-379)
+__global__ __launch_bounds__(256) void add_bias_f32(float* __restrict__ x,
+                                                    const float* __restrict__ bias, uint32_t n,
+                                                    uint32_t cols) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i < n) x[i] += bias[i % cols];
+}
+
+// erf-form GELU, x * (1 + erf(x / sqrt 2)) / 2, with erf by Abramowitz & Stegun 7.1.26 (absolute
+// error below 1.5e-7), the approximation tessery's kernel uses (kernels.metal:381-394).
+__global__ __launch_bounds__(256) void gelu_f32(float* __restrict__ x, uint32_t n) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= n) return;
+  const float value = x[i], z = fabsf(value) * 0.70710678118654752f;
+  const float t = 1.0f / (1.0f + 0.3275911f * z);
+  const float poly =
+      ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t +
+       0.254829592f) * t;
+  const float tail = poly * expf(-z * z);  // 1 - erf(z)
+  x[i] = 0.5f * value * (value < 0.0f ? tail : 2.0f - tail);
+}
+
+// LayerNorm over rows of `cols` floats: (x - mean) / sqrt(var + eps) * w + bias, mean and variance
+// in fp32 (kernels.metal:362-374). One wavefront per row; out may alias x.
+__global__ __launch_bounds__(256) void layer_norm_f32(const float* x, const float* __restrict__ w,
+                                                      const float* __restrict__ bias, float* out,
+                                                      int rows, int cols, float eps) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float* xr = x + static_cast<size_t>(row) * cols;
+  float total = 0.0f;
+  for (int c = lane; c < cols; c += 64) total += xr[c];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) total += __shfl_xor(total, off);
+  const float mean = total / static_cast<float>(cols);
+  float squares = 0.0f;
+  for (int c = lane; c < cols; c += 64) {
+    const float d = xr[c] - mean;
+    squares += d * d;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) squares += __shfl_xor(squares, off);
+  const float inv = __frsqrt_rn(squares / static_cast<float>(cols) + eps);
+  float* orow = out + static_cast<size_t>(row) * cols;
+  for (int c = lane; c < cols; c += 64) orow[c] = (xr[c] - mean) * inv * w[c] + bias[c];
+}
+
+hipError_t launch_matmul_f32(const float* a, const float* bt, const float* bias, float* out,
+                             int row0, int row1, int cols, int k, hipStream_t st) {
+  if (row1 <= row0 || cols <= 0) return hipSuccess;
+  if (k <= 0) return hipErrorInvalidValue;
+  dim3 grid((row1 - row0 + 31) / 32, (cols + 127) / 128);
+  if (bias)
+    matmul_f32<true><<<grid, 256, 0, st>>>(a, bt, bias, out, row0, row1, cols, k);
+  else
+    matmul_f32<false><<<grid, 256, 0, st>>>(a, bt, nullptr, out, row0, row1, cols, k);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_bias_f32(float* x, const float* bias, uint32_t n, uint32_t cols,
+                               hipStream_t st) {
+  if (!n) return hipSuccess;
+  add_bias_f32<<<(n + 255) / 256, 256, 0, st>>>(x, bias, n, cols);
+  return hipGetLastError();
+}
+
+hipError_t launch_gelu_f32(float* x, uint32_t n, hipStream_t st) {
+  if (!n) return hipSuccess;
+  gelu_f32<<<(n + 255) / 256, 256, 0, st>>>(x, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_layer_norm_f32(const float* x, const float* w, const float* bias, float* out,
+                                 int rows, int cols, float eps, hipStream_t st) {
+  if (rows <= 0) return hipSuccess;
+  layer_norm_f32<<<(rows + 3) / 4, 256, 0, st>>>(x, w, bias, out, rows, cols, eps);
+  return hipGetLastError();
+}
+
+}  // namespace tessery

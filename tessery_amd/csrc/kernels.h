@@ -61,6 +61,21 @@ hipError_t launch_gated4_f32(const float* x, const uint32_t* w, const uint16_t* 
 // gate[i] = silu(gate[i]) * up[i] for i < n (tessery silu_gate, kernels.metal:334-337).
 hipError_t launch_silu_gate_f32(float* gate, const float* up, uint32_t n, hipStream_t st);
 
+// fp32 dense projection out[r][n] = sum_k a[r][k] * bt[n][k] (+ bias[n] when bias is non-null)
+// for rows [row0, row1), any K and N (tessery matmul_f32 / matmul_bias_f32 families,
+// kernels.metal:306-322, 396-487).
+hipError_t launch_matmul_f32(const float* a, const float* bt, const float* bias, float* out,
+                             int row0, int row1, int cols, int k, hipStream_t st);
+// x[i] += bias[i % cols] (kernels.metal:376-379).
+hipError_t launch_add_bias_f32(float* x, const float* bias, uint32_t n, uint32_t cols,
+                               hipStream_t st);
+// erf-form GELU in place (kernels.metal:381-394).
+hipError_t launch_gelu_f32(float* x, uint32_t n, hipStream_t st);
+// LayerNorm over rows of cols floats, fp32 weight and bias, out may alias x
+// (kernels.metal:362-374).
+hipError_t launch_layer_norm_f32(const float* x, const float* w, const float* bias, float* out,
+                                 int rows, int cols, float eps, hipStream_t st);
+
 // Fused uint4 QKV projection for fp16 activations: three weight sets, outputs written in the
 // attention layout. scale/bias words are fp16 (scale_bf16 = 0) or bf16 (scale_bf16 = 1).
 struct Qkv4Args {

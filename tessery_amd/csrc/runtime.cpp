@@ -50,6 +50,14 @@ enum Route : int {
   R_GATED4_16X32,
   R_GATED4_8X32,
   R_SILU_GATE,
+  R_MATMUL,
+  R_MATMUL_TILED,
+  R_MATMUL_CHUNK32,
+  R_MATMUL_BIAS,
+  R_MATMUL_BIAS_CHUNK32,
+  R_ADD_BIAS,
+  R_GELU,
+  R_LAYER_NORM,
   R_ADD,
   R_COPY,
   R_NONE
@@ -82,6 +90,14 @@ const RouteName kRoutes[] = {
     {"gated4_16x32_k64", R_GATED4_16X32, 8},
     {"gated4_8x32", R_GATED4_8X32, 8},
     {"silu_gate", R_SILU_GATE, 2},
+    {"matmul_f32", R_MATMUL, 3},
+    {"matmul_f32_tiled", R_MATMUL_TILED, 3},
+    {"matmul_f32_chunk32", R_MATMUL_CHUNK32, 3},
+    {"matmul_bias_f32", R_MATMUL_BIAS, 4},
+    {"matmul_bias_f32_chunk32", R_MATMUL_BIAS_CHUNK32, 4},
+    {"add_bias", R_ADD_BIAS, 2},
+    {"gelu_f32", R_GELU, 1},
+    {"layer_norm", R_LAYER_NORM, 4},
     {"add", R_ADD, 3},
     {"copy", R_COPY, 2},
 };
@@ -284,6 +300,26 @@ bool gated4_range(Route r, const Params& p, uint64_t threads, uint32_t group, Ro
   return out->r0 < out->r1 && out->r1 <= rows;
 }
 
+// Rows of an fp32 dense projection: the scalar routes cover rows n + 4 * (group / cols) + t
+// (kernels.metal:306-322, 438-455), the tiled ones 8-row tiles from row 0 (kernels.metal:396-436,
+// 457-487).
+bool matmul_range(Route r, const Params& p, uint64_t threads, uint32_t group, RowRange* out) {
+  const uint64_t rows = p.rows, cols = p.cols, k = p.k, n = p.n;
+  if (!rows || !cols || !k || rows > kMaxTokens || cols > 65536 || k > 65536) return false;
+  if (r == R_MATMUL || r == R_MATMUL_BIAS) {
+    if (group != 32 || threads % (cols * 32)) return false;
+    out->r0 = n;
+    out->r1 = std::min(n + 4 * (threads / (cols * 32)), rows);
+  } else {
+    const uint64_t per = (cols / 32) * 128;
+    if (group != 128 || cols % 32 || threads % per) return false;
+    out->r0 = 0;
+    out->r1 = 8 * (threads / per);
+    if (out->r1 > rows) return false;
+  }
+  return out->r0 < out->r1;
+}
+
 // Validates one launch against the buffer sizes it would touch. Pure: no allocation.
 bool validate(Route r, const Params& p, uint64_t threads, uint32_t group, const uint64_t* sz,
               uint32_t count, uint32_t nbuf) {
@@ -357,6 +393,35 @@ bool validate(Route r, const Params& p, uint64_t threads, uint32_t group, const 
       const uint64_t wb = cols * (k / 8) * 4, sb = cols * (k / 64) * 2;
       return sz[0] >= rr.r1 * k * 4 && sz[1] >= wb && sz[2] >= sb && sz[3] >= sb &&
              sz[4] >= wb && sz[5] >= sb && sz[6] >= sb && sz[7] >= rr.r1 * cols * 4;
+    }
+    case R_MATMUL:
+    case R_MATMUL_TILED:
+    case R_MATMUL_CHUNK32:
+    case R_MATMUL_BIAS:
+    case R_MATMUL_BIAS_CHUNK32: {  // buffers: a [rows, k], bt [cols, k], out [rows, cols], bias
+      RowRange rr;
+      if (!matmul_range(r, p, threads, group, &rr)) return false;
+      const uint64_t cols = p.cols, k = p.k;
+      const bool bias = r == R_MATMUL_BIAS || r == R_MATMUL_BIAS_CHUNK32;
+      return sz[0] >= rr.r1 * k * 4 && sz[1] >= cols * k * 4 && sz[2] >= rr.r1 * cols * 4 &&
+             (!bias || sz[3] >= cols * 4);
+    }
+    case R_ADD_BIAS: {  // kernels.metal:376-379: x, bias
+      const uint64_t n = p.n, cols = p.cols;
+      return n && cols && n <= (1ull << 32) - 256 && sz[0] >= n * 4 &&
+             sz[1] >= std::min(n, cols) * 4;
+    }
+    case R_GELU: {  // kernels.metal:381-394
+      const uint64_t n = p.n;
+      return n && n <= (1ull << 32) - 256 && sz[0] >= n * 4;
+    }
+    case R_LAYER_NORM: {  // kernels.metal:362-374: rows*32 threads, groups of 32; x, w, bias, out
+      const uint64_t cols = p.cols;
+      if (group != 32 || threads % 32 || !cols || cols > 65536) return false;
+      const uint64_t rows = threads / 32;
+      if (rows > kMaxTokens) return false;
+      return sz[0] >= rows * cols * 4 && sz[1] >= cols * 4 && sz[2] >= cols * 4 &&
+             sz[3] >= rows * cols * 4;
     }
     case R_SILU_GATE: {  // kernels.metal:334-337: gate, up
       const uint64_t n = p.n;
@@ -540,6 +605,30 @@ hipError_t launch(Runtime* rt, const Op& op) {
     case R_SILU_GATE:
       return tessery::launch_silu_gate_f32(static_cast<float*>(op.ptr[0]),
                                            static_cast<const float*>(op.ptr[1]), p.n, st);
+    case R_MATMUL:
+    case R_MATMUL_TILED:
+    case R_MATMUL_CHUNK32:
+    case R_MATMUL_BIAS:
+    case R_MATMUL_BIAS_CHUNK32: {
+      RowRange rr;
+      if (!matmul_range(op.route, p, op.threads, op.group, &rr)) return hipErrorInvalidValue;
+      const bool bias = op.route == R_MATMUL_BIAS || op.route == R_MATMUL_BIAS_CHUNK32;
+      return tessery::launch_matmul_f32(
+          static_cast<const float*>(op.ptr[0]), static_cast<const float*>(op.ptr[1]),
+          bias ? static_cast<const float*>(op.ptr[3]) : nullptr, static_cast<float*>(op.ptr[2]),
+          static_cast<int>(rr.r0), static_cast<int>(rr.r1), static_cast<int>(p.cols),
+          static_cast<int>(p.k), st);
+    }
+    case R_ADD_BIAS:
+      return tessery::launch_add_bias_f32(static_cast<float*>(op.ptr[0]),
+                                          static_cast<const float*>(op.ptr[1]), p.n, p.cols, st);
+    case R_GELU:
+      return tessery::launch_gelu_f32(static_cast<float*>(op.ptr[0]), p.n, st);
+    case R_LAYER_NORM:
+      return tessery::launch_layer_norm_f32(
+          static_cast<const float*>(op.ptr[0]), static_cast<const float*>(op.ptr[1]),
+          static_cast<const float*>(op.ptr[2]), static_cast<float*>(op.ptr[3]),
+          static_cast<int>(op.threads / 32), static_cast<int>(p.cols), p.eps, st);
     case R_ADD:
       return tessery::launch_add_f32(static_cast<const float*>(op.ptr[0]),
                                      static_cast<const float*>(op.ptr[1]),

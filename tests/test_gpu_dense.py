@@ -1,0 +1,201 @@
+"""fp32 projections and the elementwise kernels of tessery's BERT layer on the GPU
+(test_kernels.py:299-353, 404-420, 600-640): float64 accuracy, the route partition seen in the
+dispatch counts, rows outside a route's region untouched, and the BGE layer composed from these
+routes (bert.py:186-230) against the float64 oracle."""
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import bert_block as ref
+from tests.test_gpu_attention import run
+
+pytestmark = pytest.mark.gpu
+
+
+def test_layer_norm(runtime):
+    rng = np.random.default_rng(37)
+    x = rng.normal(size=(3, 67)).astype(np.float32)
+    scale = rng.normal(size=67).astype(np.float32)
+    bias = rng.normal(size=67).astype(np.float32)
+    out = run(runtime, "layer_norm", [x, scale, bias], x.shape, threads=3 * 32, group_size=32,
+              cols=67, eps=1e-12)
+    np.testing.assert_allclose(out, ref.layer_norm(x, scale, bias, 1e-12), atol=1e-6, rtol=1e-5)
+    # many rows, out aliasing x
+    x = rng.normal(size=(203, 384)).astype(np.float32)
+    w, b = rng.uniform(0.5, 1.5, 384).astype(np.float32), rng.normal(size=384).astype(np.float32)
+    bufs = [runtime.upload(a) for a in (x, w, b)]
+    try:
+        with runtime.command():
+            runtime._dispatch("layer_norm", [bufs[0], bufs[1], bufs[2], bufs[0]], threads=203 * 32,
+                              group_size=32, cols=384, eps=1e-12)
+        np.testing.assert_allclose(runtime.read(bufs[0], x.shape), ref.layer_norm(x, w, b, 1e-12),
+                                   atol=1e-5, rtol=1e-5)
+    finally:
+        for bb in bufs:
+            bb.close()
+
+
+def test_gelu_erf_form_and_bias(runtime):
+    x = np.linspace(-12, 12, 10001, dtype=np.float32)
+    buffer = runtime.upload(x)
+    try:
+        with runtime.command():
+            runtime._dispatch("gelu_f32", [buffer], threads=x.size, n=x.size)
+        expected = np.array([0.5 * float(v) * (1 + math.erf(float(v) / math.sqrt(2))) for v in x])
+        np.testing.assert_allclose(runtime.read(buffer, x.shape), expected, atol=2e-6, rtol=1e-6)
+    finally:
+        buffer.close()
+    x = np.arange(12, dtype=np.float32).reshape(3, 4)
+    bias = np.array([-2, -1, 1, 2], np.float32)
+    a, b = runtime.upload(x), runtime.upload(bias)
+    try:
+        with runtime.command():
+            runtime._dispatch("add_bias", [a, b], threads=x.size, n=x.size, cols=4)
+        np.testing.assert_array_equal(runtime.read(a, x.shape), x + bias)
+    finally:
+        a.close()
+        b.close()
+
+
+@pytest.mark.parametrize(
+    "shape", [(8, 8, 32), (16, 384, 384), (32, 512, 384), (32, 1536, 384), (8, 65, 32), (9, 64, 32),
+              (3, 7, 5), (40, 130, 200)])
+def test_tiled_matmul_and_unaligned_fallback(runtime, shape):
+    m, k, n = shape
+    rng = np.random.default_rng(33)
+    a = rng.normal(size=(m, k)).astype(np.float32)
+    b = rng.normal(size=(k, n)).astype(np.float32)
+    before = dict(runtime.diagnostics()["dispatches"])
+    got = runtime.matmul(a, b)
+    np.testing.assert_allclose(got, a.astype(np.float64) @ b.astype(np.float64), atol=5e-5, rtol=5e-5)
+    tiled = m >= 8 and m % 8 == 0 and n % 32 == 0 and k % 8 == 0 and k <= 512
+    name = "matmul_f32_tiled" if tiled else "matmul_f32"
+    if m >= 8 and (n, k) in ((384, 384), (1536, 384), (384, 1536)):
+        name = "matmul_f32_chunk32"
+    after = runtime.diagnostics()["dispatches"]
+    assert {key: after[key] - before.get(key, 0) for key in after if after[key] != before.get(key, 0)} == {name: 1}
+    assert runtime.active_bytes == 0
+
+
+@pytest.mark.parametrize("m", [8, 9, 10, 11, 12, 13, 14, 15, 128, 4096])
+@pytest.mark.parametrize("n,k", [(384, 384), (1536, 384), (384, 1536)])
+@pytest.mark.parametrize("pattern", ["random", "cancellation"])
+def test_f32_chunked_projections_and_bounded_tail(runtime, m, n, k, pattern):
+    rng = np.random.default_rng(2026 + m)
+    x = rng.normal(size=(m, k)).astype(np.float32)
+    w = rng.normal(size=(n, k)).astype(np.float32)
+    if pattern == "cancellation":
+        x[:, 1::2] = -x[:, ::2]
+        w[:, 1::2] = w[:, ::2] + np.float32(2**-16)
+    expected = x.astype(np.float64) @ w.astype(np.float64).T
+    np.testing.assert_allclose(runtime.matmul(x, np.ascontiguousarray(w.T)), expected, atol=5e-5,
+                               rtol=5e-5)
+
+
+def test_f32_scalar_tail_does_not_touch_complete_rows(runtime):
+    rng = np.random.default_rng(33)
+    x = rng.normal(size=(15, 1536)).astype(np.float32)
+    w = rng.normal(size=(384, 1536)).astype(np.float32)
+    sentinel = np.full((15, 384), np.nan, np.float32)
+    buffers = [runtime.upload(a) for a in (x, w, sentinel)]
+    try:
+        with runtime.command():
+            runtime._dispatch("matmul_f32", buffers, threads=2 * 384 * 32, group_size=32, n=8,
+                              rows=15, cols=384, k=1536)
+        out = runtime.read(buffers[-1], (15, 384))
+        assert np.isnan(out[:8]).all()
+        np.testing.assert_allclose(out[8:], x[8:].astype(np.float64) @ w.astype(np.float64).T,
+                                   atol=5e-5, rtol=5e-5)
+    finally:
+        for b in buffers:
+            b.close()
+
+
+@pytest.mark.parametrize("rows", [1, 7, 8, 13, 129])
+@pytest.mark.parametrize("cols,k", [(384, 384), (1536, 384), (384, 1536), (385, 384)])
+def test_affine_projection_routes(runtime, rows, cols, k):
+    """_matmul_bias_f32 on every branch of its partition, against x W^T + b in float64."""
+    rng = np.random.default_rng(rows + cols)
+    x = rng.normal(size=(rows, k)).astype(np.float32)
+    w = rng.normal(scale=k ** -0.5, size=(cols, k)).astype(np.float32)
+    bias = rng.normal(size=cols).astype(np.float32)
+    bufs = [runtime.upload(x), runtime.upload(w), runtime.buffer(rows * cols * 4), runtime.upload(bias)]
+    try:
+        with runtime.command():
+            runtime._matmul_bias_f32(bufs, rows=rows, cols=cols, k=k)
+        np.testing.assert_allclose(runtime.read(bufs[2], (rows, cols)), ref.linear(x, w, bias),
+                                   atol=5e-5, rtol=5e-5)
+    finally:
+        for b in bufs:
+            b.close()
+
+
+def bge_weights(rng, hidden, inter):
+    w = {}
+    for name, (n, k) in {"q": (hidden, hidden), "k": (hidden, hidden), "v": (hidden, hidden),
+                         "o": (hidden, hidden), "i": (inter, hidden), "out": (hidden, inter)}.items():
+        w[name] = rng.normal(scale=k ** -0.5, size=(n, k)).astype(np.float32)
+        w[name + "_b"] = rng.normal(scale=0.1, size=n).astype(np.float32)
+    for ln in ("ln1", "ln2"):
+        w[ln + "_w"] = rng.uniform(0.5, 1.5, hidden).astype(np.float32)
+        w[ln + "_b"] = rng.normal(scale=0.1, size=hidden).astype(np.float32)
+    return w
+
+
+def bge_layer(runtime, x, lengths, w, heads, eps):
+    """bert.py:186-230 on the runtime (one encoder layer, x updated in place)."""
+    b, s, hidden = x.shape
+    tokens, inter = b * s, w["i"].shape[0]
+    bufs = {name: runtime.upload(a) for name, a in w.items()}
+    bufs["x"] = runtime.upload(x.reshape(tokens, hidden))
+    bufs["len"] = runtime.upload(lengths.astype(np.uint32))
+    for name, width in (("q_", hidden), ("k_", hidden), ("v_", hidden), ("att", hidden),
+                        ("proj", hidden), ("act", inter)):
+        bufs[name] = runtime.buffer(tokens * width * 4)
+
+    def linear(src, dst, name, outputs, inputs):
+        runtime._matmul_bias_f32([bufs[src], bufs[name], bufs[dst], bufs[name + "_b"]], rows=tokens,
+                                 cols=outputs, k=inputs)
+
+    def norm(name):
+        runtime._dispatch("layer_norm", [bufs["x"], bufs[name + "_w"], bufs[name + "_b"], bufs["x"]],
+                          threads=tokens * 32, group_size=32, cols=hidden, eps=eps)
+
+    try:
+        with runtime.command():
+            for target, name in (("q_", "q"), ("k_", "k"), ("v_", "v")):
+                linear("x", target, name, hidden, hidden)
+            runtime._attention([bufs["q_"], bufs["k_"], bufs["v_"], bufs["len"], bufs["att"]],
+                               tokens=tokens, seq=s, heads=heads, kv_heads=heads,
+                               dim=hidden // heads, bidirectional=True)
+            linear("att", "proj", "o", hidden, hidden)
+            runtime._dispatch("add", [bufs["x"], bufs["proj"], bufs["x"]], threads=tokens * hidden,
+                              n=tokens * hidden)
+            norm("ln1")
+            linear("x", "act", "i", inter, hidden)
+            runtime._dispatch("gelu_f32", [bufs["act"]], threads=tokens * inter, n=tokens * inter)
+            linear("act", "proj", "out", hidden, inter)
+            runtime._dispatch("add", [bufs["x"], bufs["proj"], bufs["x"]], threads=tokens * hidden,
+                              n=tokens * hidden)
+            norm("ln2")
+        return runtime.read(bufs["x"], x.shape)
+    finally:
+        for bb in bufs.values():
+            bb.close()
+
+
+@pytest.mark.parametrize("batch,seq,lengths", [(2, 16, [16, 9]), (2, 64, [64, 23]),
+                                               (3, 96, [96, 2, 71]), (1, 129, [100])])
+def test_bge_layer_matches_oracle(runtime, batch, seq, lengths):
+    """BGE-small widths (hidden 384, 12 heads x 32, intermediate 1536); S = 16 takes the scalar
+    attention route, 64 and 96 the tiled one, 129 the tail route."""
+    rng = np.random.default_rng(seq + batch)
+    hidden, heads, inter, eps = 384, 12, 1536, 1e-12
+    x = rng.normal(size=(batch, seq, hidden)).astype(np.float32)
+    lengths = np.array(lengths, np.uint32)
+    w = bge_weights(rng, hidden, inter)
+    got = bge_layer(runtime, x, lengths, w, heads, eps)
+    expected = ref.layer(x, lengths, w, heads=heads, eps=eps)
+    np.testing.assert_allclose(got, expected, atol=5e-5, rtol=5e-5)

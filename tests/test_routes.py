@@ -115,3 +115,54 @@ def test_gated_projection_guard_and_buffer_binding(rows, cols, k):
         assert calls[1][1][0] == [buffers[0], *buffers[4:7], buffers[8]]
         assert calls[2][1] == ("silu_gate", buffers[7:])
         assert calls[2][2] == dict(threads=rows * cols, n=rows * cols)
+
+
+BGE_SHAPES = ((384, 384), (1536, 384), (384, 1536))
+
+
+@pytest.mark.parametrize("rows", [1, 7, 8, 9, 12, 15, 16, 129, 4096])
+@pytest.mark.parametrize("cols,k", [(384, 384), (1536, 384), (384, 1536), (385, 384), (384, 1535),
+                                    (384, 512), (384, 2048)])
+def test_f32_verified_shapes_and_tail_dispatch(rows, cols, k):
+    """_matmul_f32's partition (metal.py:664-700; test_runtime_loading.py:133-164)."""
+    calls, fake = recorder()
+    HipRuntime._matmul_f32(fake, [], rows=rows, cols=cols, k=k)
+    if rows >= 8 and (cols, k) in BGE_SHAPES:
+        assert calls[0][0][0] == "matmul_f32_chunk32"
+        assert calls[0][1] == dict(threads=(rows // 8) * (cols // 32) * 128, group_size=128,
+                                   rows=rows, cols=cols, k=k)
+        assert len(calls) == 1 + bool(rows % 8)
+        if rows % 8:
+            assert calls[1][0][0] == "matmul_f32"
+            assert calls[1][1] == dict(threads=((rows % 8 + 3) // 4) * cols * 32, group_size=32,
+                                       n=rows // 8 * 8, rows=rows, cols=cols, k=k)
+    else:
+        tiled = rows >= 8 and rows % 8 == 0 and cols % 32 == 0 and k % 8 == 0 and k <= 512
+        assert len(calls) == 1
+        assert calls[0][0][0] == ("matmul_f32_tiled" if tiled else "matmul_f32")
+        assert calls[0][1].get("n", 0) == 0
+
+
+@pytest.mark.parametrize("rows", [1, 7, 8, 9, 15, 16, 129, 4096])
+@pytest.mark.parametrize("cols,k", [(384, 384), (1536, 384), (384, 1536), (385, 384)])
+def test_bge_affine_guarded_dispatch(rows, cols, k):
+    """_matmul_bias_f32's partition and binding (metal.py:702-731;
+    test_runtime_loading.py:219-262)."""
+    calls = []
+    fake = SimpleNamespace(
+        _dispatch=lambda *a, **kw: calls.append((a, kw)),
+        _matmul_f32=lambda *a, **kw: calls.append((("old_matmul", *a), kw)),
+    )
+    buffers = [object() for _ in range(4)]
+    HipRuntime._matmul_bias_f32(fake, buffers, rows=rows, cols=cols, k=k)
+    if cols == 385 or rows < 8:
+        assert [c[0][0] for c in calls] == ["old_matmul", "add_bias"]
+        assert calls[0][0][1] == buffers[:3]
+        assert calls[1][0][1] == buffers[2:]
+        assert calls[1][1] == dict(threads=rows * cols, n=rows * cols, cols=cols)
+    else:
+        expected = ["matmul_bias_f32_chunk32"] + (["matmul_bias_f32"] if rows % 8 else [])
+        assert [c[0][0] for c in calls] == expected
+        assert all(c[0][1] == buffers for c in calls)
+        if rows % 8:
+            assert calls[-1][1]["n"] == rows // 8 * 8
