@@ -18,6 +18,8 @@ HIP-event timings, and the float64 NumPy CPU oracle timed on the host on a bound
                     lengths U{1..256} (seed 5), 8 layers
   qwen_tail_16x256  the rest of the Qwen3 layer on 4096 tokens, fp32 activations: o_proj ->
                     residual -> RMSNorm -> gate/up + SiLU -> down -> residual, 4 layers
+  bge_layer_32x512  whole BGE-small encoder layers (fp32) on 32x512 tokens, lengths U{2..512}
+                    (seed 2): projections + bias, attention, LayerNorms, GELU MLP, 4 layers
 """
 
 from __future__ import annotations
@@ -520,6 +522,124 @@ def bench_qwen_tail(args) -> dict:
     return result
 
 
+def bge_layer_launch(rt: HipRuntime, s: dict, lengths_buf, tokens: int, seq: int) -> None:
+    """bert.py:186-230: q/k/v projections with bias, bidirectional attention, output projection,
+    residual + LayerNorm, intermediate projection + GELU, output projection, residual +
+    LayerNorm (x updated in place, as the reference does)."""
+    hidden, inter, heads = 384, 1536, 12
+
+    def linear(src, dst, name, outputs, inputs):
+        rt._matmul_bias_f32([s[src], s[name], s[dst], s[name + "_b"]], rows=tokens, cols=outputs,
+                            k=inputs)
+
+    def norm(name):
+        rt._dispatch("layer_norm", [s["x"], s[name + "_w"], s[name + "_b"], s["x"]],
+                     threads=tokens * 32, group_size=32, cols=hidden, eps=1e-12)
+
+    for target, name in (("qb", "q"), ("kb", "k"), ("vb", "v")):
+        linear("x", target, name, hidden, hidden)
+    rt._attention([s["qb"], s["kb"], s["vb"], lengths_buf, s["att"]], tokens=tokens, seq=seq,
+                  heads=heads, kv_heads=heads, dim=hidden // heads, bidirectional=1)
+    linear("att", "proj", "o", hidden, hidden)
+    rt._dispatch("add", [s["x"], s["proj"], s["x"]], threads=tokens * hidden, n=tokens * hidden)
+    norm("ln1")
+    linear("x", "act", "i", inter, hidden)
+    rt._dispatch("gelu_f32", [s["act"]], threads=tokens * inter, n=tokens * inter)
+    linear("act", "proj", "out", hidden, inter)
+    rt._dispatch("add", [s["x"], s["proj"], s["x"]], threads=tokens * hidden, n=tokens * hidden)
+    norm("ln2")
+
+
+def bench_bge_layer(args) -> dict:
+    """BGE-small encoder layers on 32x512 tokens (fp32), 4 independent layers: projections with
+    bias, bidirectional attention, residual + LayerNorm, GELU MLP."""
+    layers, batch, seq, hidden, inter = 4, 32, 512, 384, 1536
+    tokens = batch * seq
+    shape, lengths = workloads.bge_small_32x512()
+    flop = workloads.bge_layer_gemm_flop(tokens)
+    log(f"workload bge_layer_32x512: T={tokens} hidden={hidden} inter={inter}")
+    with HipRuntime() as rt:
+        host = [workloads.bge_encoder_layer(layer) for layer in range(layers)]
+        lengths_buf = rt.upload(lengths)
+        sets = []
+        for d in host:
+            s = {name: rt.upload(a) for name, a in d.items()}
+            for name, width in (("qb", hidden), ("kb", hidden), ("vb", hidden), ("att", hidden),
+                                ("proj", hidden), ("act", inter)):
+                s[name] = rt.buffer(tokens * width * 4)
+            sets.append(s)
+
+        def step():
+            for s in sets:
+                bge_layer_launch(rt, s, lengths_buf, tokens, seq)
+
+        # one layer first, from the pristine input, for the parity check
+        with rt.command():
+            bge_layer_launch(rt, sets[0], lengths_buf, tokens, seq)
+        out0 = rt.read(sets[0]["x"], (tokens, hidden))
+        t = run_timed(rt, step, args.steps, args.warmup, 12 * layers)
+    step_s = t["step"]
+    ks = t["kernel_s"]
+    gemm_s = 6 * ks["matmul_bias_f32_chunk32"]  # the six projections of a layer
+    tflops = flop / gemm_s / 1e12
+    result = {
+        "metric": "BGE-small encoder layer tokens/s, 32x512, 1 GPU",
+        "value": tokens * layers / step_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_s * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "bge_layer_32x512: q/k/v projections -> bidirectional attention -> "
+                               "o projection + LayerNorm -> GELU MLP + LayerNorm",
+                   "batch": batch, "seq": seq, "hidden": hidden, "intermediate": inter,
+                   "layers": layers, "lengths": "uniform [2,512], seed 2"},
+        "tflops": flop * layers / step_s / 1e12,
+        "kernel_us": {k: v * 1e6 for k, v in ks.items()},
+        "roofline": {
+            "bound": "mfma",
+            "achieved": tflops,
+            "peak": PEAK_F32_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": tflops / PEAK_F32_TFLOPS,
+            "traffic": None,
+            "algorithmic_flop": flop,
+            "kernel": "matmul_bias_f32_chunk32",
+        },
+    }
+    if not args.no_cpu_baseline:
+        from oracle import bert_block
+
+        d = host[0]
+        rows = 2  # a bounded sample: the first 2 batch rows of layer 0
+        w = {k: v for k, v in d.items() if k != "x"}
+
+        def layer():
+            return bert_block.layer(d["x"][: rows * seq].reshape(rows, seq, hidden),
+                                    lengths[:rows], w, heads=12, eps=1e-12)
+
+        expected, per_sample, runs = time_cpu(layer)
+        result["cpu_baseline"] = {
+            "value": rows * seq / per_sample,
+            "unit": "tokens/s",
+            "cores": len(os.sched_getaffinity(0)),
+            "blas_threads": blas_threads(),
+            "kind": "port",
+            "sample": f"{rows} of {batch} batch rows of layer 0, float64 NumPy oracle, median of "
+                      f"{runs} runs; {per_sample * 1e3:.1f} ms",
+        }
+        got = out0[: rows * seq].reshape(rows, seq, hidden).astype(np.float64)
+        result["max_abs_err_layer0"] = float(np.abs(got - expected).max())
+    else:
+        result["cpu_baseline"] = None
+    return result
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__,
                                      formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -529,7 +649,7 @@ def main() -> int:
     parser.add_argument("--layers", type=int, default=LAYERS, help="headline workload only")
     parser.add_argument("--workload", default="qwen3_32x512",
                         choices=["qwen3_32x512", "qwen3_8x512", "bge_32x512", "qwen_qkv4_16x256",
-                                 "qwen_tail_16x256"])
+                                 "qwen_tail_16x256", "bge_layer_32x512"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="also launch one copy of this many MiB (traffic-counter calibration)")
@@ -554,6 +674,8 @@ def main() -> int:
         result = bench_bge(args)
     elif args.workload == "qwen_tail_16x256":
         result = bench_qwen_tail(args)
+    elif args.workload == "bge_layer_32x512":
+        result = bench_bge_layer(args)
     else:
         result = bench_qkv4_block(args)
     print(json.dumps(result), flush=True)

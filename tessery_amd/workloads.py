@@ -93,6 +93,28 @@ def bge_layer(shape: Shape, layer: int, seed: int = 2) -> dict[str, NDArray]:
     return {"q": q, "k": k, "v": v}
 
 
+def bge_encoder_layer(layer: int, seed: int = 7, batch: int = 32, seq: int = 512) -> dict[str, Any]:
+    """BGE-small encoder layer weights and input (bert.py:186-230): hidden 384, 12 heads x 32,
+    intermediate 1536; x ~ N(0,1) [batch*seq, 384]; projection weights N(0, 1/K) [N, K] with
+    biases N(0, 0.1^2); LayerNorm weights U(0.5,1.5), biases N(0, 0.1^2). fp32."""
+    rng = np.random.default_rng((seed, layer))
+    hidden, inter = 384, 1536
+    w: dict[str, Any] = {"x": normal(rng, (batch * seq, hidden), np.float32)}
+    for name, (n, k) in {"q": (hidden, hidden), "k": (hidden, hidden), "v": (hidden, hidden),
+                         "o": (hidden, hidden), "i": (inter, hidden), "out": (hidden, inter)}.items():
+        w[name] = (normal(rng, (n, k), np.float32) * np.float32(k ** -0.5)).astype(np.float32)
+        w[name + "_b"] = (0.1 * normal(rng, (n,), np.float32)).astype(np.float32)
+    for ln in ("ln1", "ln2"):
+        w[ln + "_w"] = rng.uniform(0.5, 1.5, hidden).astype(np.float32)
+        w[ln + "_b"] = (0.1 * normal(rng, (hidden,), np.float32)).astype(np.float32)
+    return w
+
+
+def bge_layer_gemm_flop(tokens: int, hidden: int = 384, inter: int = 1536) -> int:
+    """2*T*K*N over the six projections of a BERT layer (q, k, v, o, intermediate, output)."""
+    return 2 * tokens * (4 * hidden * hidden + 2 * hidden * inter)
+
+
 def qwen3_8x512() -> tuple[Shape, NDArray[np.uint32]]:
     return Shape(8, 512, 16, 8, 128, causal=True), lengths_uniform(3, 8, 64, 512)
 
