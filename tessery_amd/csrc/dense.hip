@@ -12,10 +12,13 @@
 
 namespace tessery {
 
-// 256 threads = 4 wavefronts; tile 32 rows x 128 columns (32 per wavefront); the K loop walks
+// 256 threads = 4 wavefronts; tile 64 rows x 128 columns: wavefront w owns columns 32w..32w+31
+// of both 32-row halves, so every weight it loads feeds two 32x32 MFMA tiles. The K loop walks
 // 64 columns at a time. v_mfma_f32_32x32x2_f32 with lane (column n = l%32, k-slot h = l/32):
 // k-step t of a 32-wide half pairs k = 32h + t, so each lane holds 32 consecutive weights of its
 // row per 64-column chunk. Columns past K and rows / weight rows past their ends read as zero.
+constexpr int kDenseRows = 64;
+
 template <bool BIAS>
 __global__ __launch_bounds__(256) void matmul_f32(const float* __restrict__ a,
                                                   const float* __restrict__ bt,
@@ -23,25 +26,29 @@ __global__ __launch_bounds__(256) void matmul_f32(const float* __restrict__ a,
                                                   float* __restrict__ out, int row0, int row1,
                                                   int cols, int k) {
   constexpr int XROW = 64 + 4;
-  __shared__ __attribute__((aligned(16))) float xs[32 * XROW];
+  __shared__ __attribute__((aligned(16))) float xs[kDenseRows * XROW];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  const int rbase = row0 + blockIdx.x * 32;
+  const int rbase = row0 + blockIdx.x * kDenseRows;
   const int n = blockIdx.y * 128 + wave * 32 + l32;
   const bool nvalid = n < cols;
   const bool vec = (k & 3) == 0;  // rows start 16-byte aligned: float4 loads
   const int chunks = (k + 63) / 64;
-  floatx16 acc;
+  floatx16 acc[2];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
-  for (int ci = 0; ci < chunks; ++ci) {
-    const int k0 = ci * 64;
-    __syncthreads();
+  for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + 256 * i;  // 512 four-float chunks = 32 rows x 16
+    for (int e = 0; e < 16; ++e) acc[rt][e] = 0.0f;
+  // x chunks are loaded into registers one chunk ahead and written to LDS after the barrier that
+  // retires the previous chunk's reads; the lane's weights are loaded before that barrier
+  constexpr int XV = kDenseRows * 16 / 256;  // four-float x pieces per thread per chunk
+  floatx4 xr[XV];
+  auto load_x = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+      const int c = tid + 256 * i;  // four-float pieces: 64 rows x 16
       const int r = c / 16, kk = k0 + 4 * (c % 16);
       floatx4 t = {0.f, 0.f, 0.f, 0.f};
-      if (rbase + r < row1) {
+      if (rbase + r < row1 && kk < k) {
         const float* src = a + static_cast<size_t>(rbase + r) * k + kk;
         if (vec && kk + 4 <= k) {
           t = *reinterpret_cast<const floatx4*>(src);
@@ -50,9 +57,12 @@ __global__ __launch_bounds__(256) void matmul_f32(const float* __restrict__ a,
           for (int j = 0; j < 4; ++j) t[j] = kk + j < k ? src[j] : 0.0f;
         }
       }
-      *reinterpret_cast<floatx4*>(&xs[r * XROW + 4 * (c % 16)]) = t;
+      xr[i] = t;
     }
-    __syncthreads();
+  };
+  load_x(0);
+  for (int ci = 0; ci < chunks; ++ci) {
+    const int k0 = ci * 64;
     float wv[32];
     {
       const int kw = k0 + 32 * hh;
@@ -71,29 +81,43 @@ __global__ __launch_bounds__(256) void matmul_f32(const float* __restrict__ a,
         for (int j = 0; j < 32; ++j) wv[j] = nvalid && kw + j < k ? src[j] : 0.0f;
       }
     }
+    __syncthreads();
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      floatx16 part;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) part[e] = 0.0f;
-#pragma unroll
-      for (int c4 = 4 * half; c4 < 4 * half + 4; ++c4) {
-        const floatx4 xa = *reinterpret_cast<const floatx4*>(&xs[l32 * XROW + 32 * hh + 4 * c4]);
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          part = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[t], wv[4 * c4 + t], part, 0, 0, 0);
-      }
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[e] += part[e];
+    for (int i = 0; i < XV; ++i) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<floatx4*>(&xs[(c / 16) * XROW + 4 * (c % 16)]) = xr[i];
     }
+    __syncthreads();
+    if (ci + 1 < chunks) load_x(k0 + 64);
+    // K32 partial sums per 32-row tile, each added to its total (the chunk32 order)
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        floatx16 part;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) part[e] = 0.0f;
+#pragma unroll
+        for (int c4 = 4 * half; c4 < 4 * half + 4; ++c4) {
+          const floatx4 xa =
+              *reinterpret_cast<const floatx4*>(&xs[(32 * rt + l32) * XROW + 32 * hh + 4 * c4]);
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            part = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[t], wv[4 * c4 + t], part, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[rt][e] += part[e];
+      }
   }
   if (!nvalid) return;
   const float b = BIAS ? bias[n] : 0.0f;
 #pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const int r = rbase + 8 * (e >> 2) + 4 * hh + (e & 3);
-    if (r < row1) out[static_cast<size_t>(r) * cols + n] = BIAS ? acc[e] + b : acc[e];
-  }
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int r = rbase + 32 * rt + 8 * (e >> 2) + 4 * hh + (e & 3);
+      if (r < row1) out[static_cast<size_t>(r) * cols + n] = BIAS ? acc[rt][e] + b : acc[rt][e];
+    }
 }
 
 // x[i] += bias[i % cols] (kernels.metal:376-379)
@@ -147,7 +171,7 @@ hipError_t launch_matmul_f32(const float* a, const float* bt, const float* bias,
                              int row0, int row1, int cols, int k, hipStream_t st) {
   if (row1 <= row0 || cols <= 0) return hipSuccess;
   if (k <= 0) return hipErrorInvalidValue;
-  dim3 grid((row1 - row0 + 31) / 32, (cols + 127) / 128);
+  dim3 grid((row1 - row0 + kDenseRows - 1) / kDenseRows, (cols + 127) / 128);
   if (bias)
     matmul_f32<true><<<grid, 256, 0, st>>>(a, bt, bias, out, row0, row1, cols, k);
   else
