@@ -44,7 +44,7 @@ __device__ __forceinline__ void decode_group(const uint32_t* __restrict__ w,
 // Two independent 32-product partial sums per group, added to the total: the K32 partial
 // accumulation of tessery's tiled kernels (kernels.metal:500-518), which bounds the rounding
 // growth over long K.
-__device__ __forceinline__ void group_product(const float* xs, int xrow, int l32, int hh,
+__device__ __forceinline__ void group_product(const float* xs, int xrow, int row, int hh,
                                               const float (&wv)[32], floatx16& acc) {
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
@@ -53,7 +53,7 @@ __device__ __forceinline__ void group_product(const float* xs, int xrow, int l32
     for (int e = 0; e < 16; ++e) part[e] = 0.0f;
 #pragma unroll
     for (int c4 = 4 * half; c4 < 4 * half + 4; ++c4) {
-      const floatx4 xa = *reinterpret_cast<const floatx4*>(&xs[l32 * xrow + 32 * hh + 4 * c4]);
+      const floatx4 xa = *reinterpret_cast<const floatx4*>(&xs[row * xrow + 32 * hh + 4 * c4]);
 #pragma unroll
       for (int t = 0; t < 4; ++t)
         part = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[t], wv[4 * c4 + t], part, 0, 0, 0);
@@ -63,11 +63,15 @@ __device__ __forceinline__ void group_product(const float* xs, int xrow, int l32
   }
 }
 
-// 256 threads = 4 wavefronts; tile 32 rows x 128 columns (32 columns per wavefront); the K loop
-// walks one quantization group (64) at a time. fp32 MFMA v_mfma_f32_32x32x2_f32 computes
-// Y = X * W^T with lane (column n = l%32, k-slot h = l/32); k-step t pairs k = 32h + t, so each
-// lane decodes 32 consecutive codes (four words) of its weight row per group.
+// 256 threads = 4 wavefronts; tile 64 rows x 128 columns: wavefront w owns columns 32w..32w+31 of
+// both 32-row halves, so the weights it decodes feed two 32x32 MFMA tiles. The K loop walks one
+// quantization group (64) at a time; the next group's x is loaded into registers while the
+// current one runs. fp32 MFMA v_mfma_f32_32x32x2_f32 computes Y = X * W^T with lane (column
+// n = l%32, k-slot h = l/32); k-step t pairs k = 32h + t, so each lane decodes 32 consecutive
+// codes (four words) of its weight row per group.
 // GATED: a second weight set (uw, us, ub) accumulates the up projection beside the gate.
+constexpr int kL4Rows = 64;
+
 template <bool GATED>
 __global__ __launch_bounds__(256) void linear4_f32(
     const float* __restrict__ x, const uint32_t* __restrict__ w,
@@ -76,44 +80,63 @@ __global__ __launch_bounds__(256) void linear4_f32(
     const uint16_t* __restrict__ ubiases, float* __restrict__ out, int row0, int row1, int cols,
     int k) {
   constexpr int XROW = 64 + 4;
-  __shared__ __attribute__((aligned(16))) float xs[32 * XROW];
+  constexpr int XV = kL4Rows * 16 / 256;  // four-float x pieces per thread per group
+  __shared__ __attribute__((aligned(16))) float xs[kL4Rows * XROW];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  const int rbase = row0 + blockIdx.x * 32;
+  const int rbase = row0 + blockIdx.x * kL4Rows;
   const int n = blockIdx.y * 128 + wave * 32 + l32;
   const bool nvalid = n < cols;
   const int groups = k / 64;
-  floatx16 acc, uacc;
+  floatx16 acc[2], uacc[2];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    acc[e] = 0.0f;
-    uacc[e] = 0.0f;
-  }
-  for (int gi = 0; gi < groups; ++gi) {
-    __syncthreads();
+  for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + 256 * i;  // 512 float4 chunks = 32 rows x 16
+    for (int e = 0; e < 16; ++e) {
+      acc[rt][e] = 0.0f;
+      uacc[rt][e] = 0.0f;
+    }
+  floatx4 xr[XV];
+  auto load_x = [&](int gi) {
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+      const int c = tid + 256 * i;  // four-float pieces: 64 rows x 16
       const int r = c / 16, ck = c % 16;
       floatx4 t = {0.f, 0.f, 0.f, 0.f};
       if (rbase + r < row1)
         t = *reinterpret_cast<const floatx4*>(x + static_cast<size_t>(rbase + r) * k + gi * 64 + 4 * ck);
-      *reinterpret_cast<floatx4*>(&xs[r * XROW + 4 * ck]) = t;
+      xr[i] = t;
     }
-    __syncthreads();
+  };
+  load_x(0);
+  for (int gi = 0; gi < groups; ++gi) {
     float wv[32];
     decode_group(w, scales, biases, n, nvalid, k, gi, hh, wv);
-    group_product(xs, XROW, l32, hh, wv, acc);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<floatx4*>(&xs[(c / 16) * XROW + 4 * (c % 16)]) = xr[i];
+    }
+    __syncthreads();
+    if (gi + 1 < groups) load_x(gi + 1);
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) group_product(xs, XROW, 32 * rt + l32, hh, wv, acc[rt]);
     if constexpr (GATED) {
       decode_group(uw, uscales, ubiases, n, nvalid, k, gi, hh, wv);
-      group_product(xs, XROW, l32, hh, wv, uacc);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) group_product(xs, XROW, 32 * rt + l32, hh, wv, uacc[rt]);
     }
   }
   if (!nvalid) return;
 #pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const int r = rbase + 8 * (e >> 2) + 4 * hh + (e & 3);
-    if (r < row1) out[static_cast<size_t>(r) * cols + n] = GATED ? silu_times(acc[e], uacc[e]) : acc[e];
-  }
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int r = rbase + 32 * rt + 8 * (e >> 2) + 4 * hh + (e & 3);
+      if (r < row1)
+        out[static_cast<size_t>(r) * cols + n] =
+            GATED ? silu_times(acc[rt][e], uacc[rt][e]) : acc[rt][e];
+    }
 }
 
 __global__ __launch_bounds__(256) void silu_gate_f32(float* __restrict__ gate,
@@ -127,7 +150,7 @@ hipError_t launch_linear4_f32(const float* x, const uint32_t* w, const uint16_t*
                               int k, hipStream_t st) {
   if (row1 <= row0 || cols <= 0) return hipSuccess;
   if (k % 64) return hipErrorInvalidValue;
-  dim3 grid((row1 - row0 + 31) / 32, (cols + 127) / 128);
+  dim3 grid((row1 - row0 + kL4Rows - 1) / kL4Rows, (cols + 127) / 128);
   linear4_f32<false><<<grid, 256, 0, st>>>(x, w, scales, biases, nullptr, nullptr, nullptr, out,
                                            row0, row1, cols, k);
   return hipGetLastError();
@@ -139,7 +162,7 @@ hipError_t launch_gated4_f32(const float* x, const uint32_t* w, const uint16_t* 
                              int k, hipStream_t st) {
   if (row1 <= row0 || cols <= 0) return hipSuccess;
   if (k % 64) return hipErrorInvalidValue;
-  dim3 grid((row1 - row0 + 31) / 32, (cols + 127) / 128);
+  dim3 grid((row1 - row0 + kL4Rows - 1) / kL4Rows, (cols + 127) / 128);
   linear4_f32<true><<<grid, 256, 0, st>>>(x, w, scales, biases, uw, uscales, ubiases, out, row0,
                                           row1, cols, k);
   return hipGetLastError();
