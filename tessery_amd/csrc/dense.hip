@@ -19,7 +19,20 @@ namespace tessery {
 // row per 64-column chunk. Columns past K and rows / weight rows past their ends read as zero.
 constexpr int kDenseRows = 64;
 
-template <bool BIAS>
+// erf-form GELU, x * (1 + erf(x / sqrt 2)) / 2, with erf by Abramowitz & Stegun 7.1.26 (absolute
+// error below 1.5e-7), the approximation tessery's kernel uses (kernels.metal:381-394). The
+// gelu_f32 route and the fused projection epilogue share it, so both give the same bits.
+__device__ __forceinline__ float gelu_value(float value) {
+  const float z = fabsf(value) * 0.70710678118654752f;
+  const float t = 1.0f / (1.0f + 0.3275911f * z);
+  const float poly =
+      ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t +
+       0.254829592f) * t;
+  const float tail = poly * expf(-z * z);  // 1 - erf(z)
+  return 0.5f * value * (value < 0.0f ? tail : 2.0f - tail);
+}
+
+template <bool BIAS, bool GELU>
 __global__ __launch_bounds__(256) void matmul_f32(const float* __restrict__ a,
                                                   const float* __restrict__ bt,
                                                   const float* __restrict__ bias,
@@ -116,7 +129,10 @@ __global__ __launch_bounds__(256) void matmul_f32(const float* __restrict__ a,
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int r = rbase + 32 * rt + 8 * (e >> 2) + 4 * hh + (e & 3);
-      if (r < row1) out[static_cast<size_t>(r) * cols + n] = BIAS ? acc[rt][e] + b : acc[rt][e];
+      if (r < row1) {
+        const float y = BIAS ? acc[rt][e] + b : acc[rt][e];
+        out[static_cast<size_t>(r) * cols + n] = GELU ? gelu_value(y) : y;
+      }
     }
 }
 
@@ -128,28 +144,27 @@ __global__ __launch_bounds__(256) void add_bias_f32(float* __restrict__ x,
   if (i < n) x[i] += bias[i % cols];
 }
 
-// erf-form GELU, x * (1 + erf(x / sqrt 2)) / 2, with erf by Abramowitz & Stegun 7.1.26 (absolute
-// error below 1.5e-7), the approximation tessery's kernel uses (kernels.metal:381-394).
 __global__ __launch_bounds__(256) void gelu_f32(float* __restrict__ x, uint32_t n) {
   const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-  if (i >= n) return;
-  const float value = x[i], z = fabsf(value) * 0.70710678118654752f;
-  const float t = 1.0f / (1.0f + 0.3275911f * z);
-  const float poly =
-      ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t +
-       0.254829592f) * t;
-  const float tail = poly * expf(-z * z);  // 1 - erf(z)
-  x[i] = 0.5f * value * (value < 0.0f ? tail : 2.0f - tail);
+  if (i < n) x[i] = gelu_value(x[i]);
 }
 
 // LayerNorm over rows of `cols` floats: (x - mean) / sqrt(var + eps) * w + bias, mean and variance
 // in fp32 (kernels.metal:362-374). One wavefront per row; out may alias x.
-__global__ __launch_bounds__(256) void layer_norm_f32(const float* x, const float* __restrict__ w,
+// RESIDUAL: x is first replaced by x + r (tessery's add, kernels.metal:300-304) and the row is
+// normalized in place, the pair add(x, r -> x), layer_norm(x -> x) in one pass.
+template <bool RESIDUAL>
+__global__ __launch_bounds__(256) void layer_norm_f32(float* x, const float* r,
+                                                      const float* __restrict__ w,
                                                       const float* __restrict__ bias, float* out,
                                                       int rows, int cols, float eps) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= rows) return;
-  const float* xr = x + static_cast<size_t>(row) * cols;
+  float* xr = x + static_cast<size_t>(row) * cols;
+  if constexpr (RESIDUAL) {
+    const float* rr = r + static_cast<size_t>(row) * cols;
+    for (int c = lane; c < cols; c += 64) xr[c] = xr[c] + rr[c];
+  }
   float total = 0.0f;
   for (int c = lane; c < cols; c += 64) total += xr[c];
 #pragma unroll
@@ -168,14 +183,18 @@ __global__ __launch_bounds__(256) void layer_norm_f32(const float* x, const floa
 }
 
 hipError_t launch_matmul_f32(const float* a, const float* bt, const float* bias, float* out,
-                             int row0, int row1, int cols, int k, hipStream_t st) {
+                             int row0, int row1, int cols, int k, bool gelu, hipStream_t st) {
   if (row1 <= row0 || cols <= 0) return hipSuccess;
   if (k <= 0) return hipErrorInvalidValue;
   dim3 grid((row1 - row0 + kDenseRows - 1) / kDenseRows, (cols + 127) / 128);
-  if (bias)
-    matmul_f32<true><<<grid, 256, 0, st>>>(a, bt, bias, out, row0, row1, cols, k);
+  if (bias && gelu)
+    matmul_f32<true, true><<<grid, 256, 0, st>>>(a, bt, bias, out, row0, row1, cols, k);
+  else if (bias)
+    matmul_f32<true, false><<<grid, 256, 0, st>>>(a, bt, bias, out, row0, row1, cols, k);
+  else if (gelu)
+    matmul_f32<false, true><<<grid, 256, 0, st>>>(a, bt, nullptr, out, row0, row1, cols, k);
   else
-    matmul_f32<false><<<grid, 256, 0, st>>>(a, bt, nullptr, out, row0, row1, cols, k);
+    matmul_f32<false, false><<<grid, 256, 0, st>>>(a, bt, nullptr, out, row0, row1, cols, k);
   return hipGetLastError();
 }
 
@@ -195,7 +214,15 @@ hipError_t launch_gelu_f32(float* x, uint32_t n, hipStream_t st) {
 hipError_t launch_layer_norm_f32(const float* x, const float* w, const float* bias, float* out,
                                  int rows, int cols, float eps, hipStream_t st) {
   if (rows <= 0) return hipSuccess;
-  layer_norm_f32<<<(rows + 3) / 4, 256, 0, st>>>(x, w, bias, out, rows, cols, eps);
+  layer_norm_f32<false><<<(rows + 3) / 4, 256, 0, st>>>(const_cast<float*>(x), nullptr, w, bias,
+                                                       out, rows, cols, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_layer_norm_f32(float* x, const float* r, const float* w, const float* bias,
+                                     int rows, int cols, float eps, hipStream_t st) {
+  if (rows <= 0) return hipSuccess;
+  layer_norm_f32<true><<<(rows + 3) / 4, 256, 0, st>>>(x, r, w, bias, x, rows, cols, eps);
   return hipGetLastError();
 }
 

@@ -63,9 +63,10 @@ hipError_t launch_silu_gate_f32(float* gate, const float* up, uint32_t n, hipStr
 
 // fp32 dense projection out[r][n] = sum_k a[r][k] * bt[n][k] (+ bias[n] when bias is non-null)
 // for rows [row0, row1), any K and N (tessery matmul_f32 / matmul_bias_f32 families,
-// kernels.metal:306-322, 396-487).
+// kernels.metal:306-322, 396-487); with gelu the stored value is gelu_f32 of it, bit-identical to
+// the projection followed by the gelu_f32 route.
 hipError_t launch_matmul_f32(const float* a, const float* bt, const float* bias, float* out,
-                             int row0, int row1, int cols, int k, hipStream_t st);
+                             int row0, int row1, int cols, int k, bool gelu, hipStream_t st);
 // x[i] += bias[i % cols] (kernels.metal:376-379).
 hipError_t launch_add_bias_f32(float* x, const float* bias, uint32_t n, uint32_t cols,
                                hipStream_t st);
@@ -75,6 +76,10 @@ hipError_t launch_gelu_f32(float* x, uint32_t n, hipStream_t st);
 // (kernels.metal:362-374).
 hipError_t launch_layer_norm_f32(const float* x, const float* w, const float* bias, float* out,
                                  int rows, int cols, float eps, hipStream_t st);
+// x = layer_norm(x + r) in place: the add route into x followed by an in-place layer_norm, in one
+// pass with the same bits.
+hipError_t launch_add_layer_norm_f32(float* x, const float* r, const float* w, const float* bias,
+                                     int rows, int cols, float eps, hipStream_t st);
 
 // Fused uint4 QKV projection for fp16 activations: three weight sets, outputs written in the
 // attention layout. scale/bias words are fp16 (scale_bf16 = 0) or bf16 (scale_bf16 = 1).

@@ -617,7 +617,7 @@ hipError_t launch(Runtime* rt, const Op& op) {
           static_cast<const float*>(op.ptr[0]), static_cast<const float*>(op.ptr[1]),
           bias ? static_cast<const float*>(op.ptr[3]) : nullptr, static_cast<float*>(op.ptr[2]),
           static_cast<int>(rr.r0), static_cast<int>(rr.r1), static_cast<int>(p.cols),
-          static_cast<int>(p.k), st);
+          static_cast<int>(p.k), false, st);
     }
     case R_ADD_BIAS:
       return tessery::launch_add_bias_f32(static_cast<float*>(op.ptr[0]),
@@ -780,6 +780,41 @@ int mi_dispatch(void* runtime, const char* name, void** buffers, uint32_t count,
   return queue_op(rt, op) ? 0 : 1;
 }
 
+// Pairs of queued launches that one kernel runs with the same bits (the second op of a pair is
+// then not launched on its own):
+//   a projection covering every row of its output, then gelu_f32 over exactly that output
+//     -> the projection with the GELU epilogue;
+//   add(a, b -> a), then layer_norm(a -> a) over the same rows
+//     -> one pass that adds and normalizes in place.
+// Returns the launch status, or hipErrorNotReady when ops[i], ops[i + 1] are not such a pair.
+hipError_t launch_fused_pair(Runtime* rt, const Op& a, const Op& b) {
+  hipStream_t st = rt->stream;
+  const bool projection = a.route == R_MATMUL || a.route == R_MATMUL_TILED ||
+                          a.route == R_MATMUL_CHUNK32 || a.route == R_MATMUL_BIAS ||
+                          a.route == R_MATMUL_BIAS_CHUNK32;
+  if (projection && b.route == R_GELU && b.ptr[0] == a.ptr[2]) {
+    RowRange rr;
+    if (!matmul_range(a.route, a.p, a.threads, a.group, &rr)) return hipErrorNotReady;
+    if (rr.r0 != 0 || rr.r1 != a.p.rows ||
+        static_cast<uint64_t>(b.p.n) != static_cast<uint64_t>(a.p.rows) * a.p.cols)
+      return hipErrorNotReady;
+    const bool bias = a.route == R_MATMUL_BIAS || a.route == R_MATMUL_BIAS_CHUNK32;
+    return tessery::launch_matmul_f32(
+        static_cast<const float*>(a.ptr[0]), static_cast<const float*>(a.ptr[1]),
+        bias ? static_cast<const float*>(a.ptr[3]) : nullptr, static_cast<float*>(a.ptr[2]),
+        0, static_cast<int>(rr.r1), static_cast<int>(a.p.cols), static_cast<int>(a.p.k), true, st);
+  }
+  if (a.route == R_ADD && b.route == R_LAYER_NORM && a.ptr[2] == a.ptr[0] &&
+      b.ptr[0] == a.ptr[0] && b.ptr[3] == a.ptr[0] && a.ptr[1] != a.ptr[0] &&
+      static_cast<uint64_t>(a.p.n) == (b.threads / 32) * b.p.cols) {
+    return tessery::launch_add_layer_norm_f32(
+        static_cast<float*>(a.ptr[0]), static_cast<const float*>(a.ptr[1]),
+        static_cast<const float*>(b.ptr[1]), static_cast<const float*>(b.ptr[2]),
+        static_cast<int>(b.threads / 32), static_cast<int>(b.p.cols), b.p.eps, st);
+  }
+  return hipErrorNotReady;
+}
+
 int mi_finish(void* runtime) {
   auto rt = static_cast<Runtime*>(runtime);
   if (!rt || !rt->recording) return 1;
@@ -796,10 +831,20 @@ int mi_finish(void* runtime) {
   if (hipEventRecord(rt->ev_start, rt->stream) != hipSuccess) failed = 1;
   for (size_t i = 0; i < n && !failed; ++i) {
     if (rt->profiling && hipEventRecord(rt->prof_events[2 * i], rt->stream) != hipSuccess) failed = 1;
-    if (!failed && launch(rt, rt->ops[i]) != hipSuccess) failed = 1;
+    // a fused pair runs inside the first op's events; the second op's events enclose no work
+    const hipError_t fused =
+        failed || i + 1 >= n ? hipErrorNotReady : launch_fused_pair(rt, rt->ops[i], rt->ops[i + 1]);
+    if (!failed && fused != hipErrorNotReady && fused != hipSuccess) failed = 1;
+    if (!failed && fused == hipErrorNotReady && launch(rt, rt->ops[i]) != hipSuccess) failed = 1;
     if (!failed && rt->profiling &&
         hipEventRecord(rt->prof_events[2 * i + 1], rt->stream) != hipSuccess)
       failed = 1;
+    if (!failed && fused == hipSuccess) {
+      ++i;
+      if (rt->profiling && (hipEventRecord(rt->prof_events[2 * i], rt->stream) != hipSuccess ||
+                            hipEventRecord(rt->prof_events[2 * i + 1], rt->stream) != hipSuccess))
+        failed = 1;
+    }
   }
   if (hipEventRecord(rt->ev_end, rt->stream) != hipSuccess) failed = 1;
   if (hipStreamSynchronize(rt->stream) != hipSuccess) failed = 1;

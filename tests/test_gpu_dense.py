@@ -199,3 +199,48 @@ def test_bge_layer_matches_oracle(runtime, batch, seq, lengths):
     got = bge_layer(runtime, x, lengths, w, heads, eps)
     expected = ref.layer(x, lengths, w, heads=heads, eps=eps)
     np.testing.assert_allclose(got, expected, atol=5e-5, rtol=5e-5)
+
+
+@pytest.mark.parametrize("rows,cols,k", [(64, 1536, 384), (200, 384, 1536), (13, 96, 40)])
+def test_fused_projection_gelu_and_residual_norm_are_bit_exact(runtime, rows, cols, k):
+    """Within one command the runtime runs projection + gelu_f32 and add + layer_norm (in place)
+    as single launches; split over two commands they run separately. Same bits either way."""
+    rng = np.random.default_rng(rows * 3 + k)
+    x = rng.normal(size=(rows, k)).astype(np.float32)
+    w = rng.normal(scale=k ** -0.5, size=(cols, k)).astype(np.float32)
+    bias = rng.normal(size=cols).astype(np.float32)
+    resid = rng.normal(size=(rows, cols)).astype(np.float32)
+    lw, lb = rng.uniform(0.5, 1.5, cols).astype(np.float32), rng.normal(size=cols).astype(np.float32)
+
+    def run_layer(split):
+        bufs = [runtime.upload(a) for a in (x, w, np.zeros((rows, cols), np.float32), bias, resid, lw, lb)]
+        xb, wb, yb, bb, rb, lwb, lbb = bufs
+        try:
+            steps = [
+                lambda: runtime._matmul_bias_f32([xb, wb, yb, bb], rows=rows, cols=cols, k=k),
+                lambda: runtime._dispatch("gelu_f32", [yb], threads=rows * cols, n=rows * cols),
+                lambda: runtime._dispatch("add", [rb, yb, rb], threads=rows * cols, n=rows * cols),
+                lambda: runtime._dispatch("layer_norm", [rb, lwb, lbb, rb], threads=rows * 32,
+                                          group_size=32, cols=cols, eps=1e-12),
+            ]
+            if split:
+                for s in steps:
+                    with runtime.command():
+                        s()
+            else:
+                with runtime.command():
+                    for s in steps:
+                        s()
+            return runtime.read(yb, (rows, cols)), runtime.read(rb, (rows, cols))
+        finally:
+            for b in bufs:
+                b.close()
+
+    fused_y, fused_r = run_layer(False)
+    split_y, split_r = run_layer(True)
+    np.testing.assert_array_equal(fused_y, split_y)
+    np.testing.assert_array_equal(fused_r, split_r)
+    expected_y = ref.gelu(ref.linear(x, w, bias))
+    np.testing.assert_allclose(fused_y, expected_y, atol=5e-5, rtol=5e-5)
+    np.testing.assert_allclose(fused_r, ref.layer_norm(resid + expected_y, lw, lb, 1e-12),
+                               atol=5e-5, rtol=5e-5)
