@@ -20,6 +20,8 @@ HIP-event timings, and the float64 NumPy CPU oracle timed on the host on a bound
                     residual -> RMSNorm -> gate/up + SiLU -> down -> residual, 4 layers
   bge_layer_32x512  whole BGE-small encoder layers (fp32) on 32x512 tokens, lengths U{2..512}
                     (seed 2): projections + bias, attention, LayerNorms, GELU MLP, 4 layers
+  bge_plan_1x128    a 12-layer BGE-small stack on one 128-token sequence replayed as a prepared
+                    plan, with plan replays as cached HIP graphs and launched one by one
 """
 
 from __future__ import annotations
@@ -640,6 +642,81 @@ def bench_bge_layer(args) -> dict:
     return result
 
 
+def bench_bge_plan(args) -> dict:
+    """A 12-layer BGE-small encoder stack on one 128-token sequence, replayed as a prepared plan
+    (the reference's _execution_plan path, bert.py:153-170): per-forward time with plan replays as
+    cached HIP graphs and, in a second runtime, launched one by one (TESSERY_HIP_GRAPHS=0)."""
+    layers, batch, seq, hidden, inter = 12, 1, 128, 384, 1536
+    tokens = batch * seq
+    lengths = np.array([seq], np.uint32)
+    host = [workloads.bge_encoder_layer(layer, batch=batch, seq=seq) for layer in range(layers)]
+    log(f"workload bge_plan_1x128: {layers} layers, T={tokens}")
+
+    def measure(graphs: bool) -> tuple[float, dict]:
+        previous = os.environ.get("TESSERY_HIP_GRAPHS")
+        os.environ["TESSERY_HIP_GRAPHS"] = "1" if graphs else "0"
+        try:
+            rt = HipRuntime()
+        finally:
+            if previous is None:
+                del os.environ["TESSERY_HIP_GRAPHS"]
+            else:
+                os.environ["TESSERY_HIP_GRAPHS"] = previous
+        with rt:
+            lengths_buf = rt.upload(lengths)
+            sets = []
+            for d in host:
+                s = {name: rt.upload(a) for name, a in d.items()}
+                for name, width in (("qb", hidden), ("kb", hidden), ("vb", hidden), ("att", hidden),
+                                    ("proj", hidden), ("act", inter)):
+                    s[name] = rt.buffer(tokens * width * 4)
+                sets.append(s)
+            bindings = [lengths_buf] + [s[n] for s in sets for n in sorted(s)]
+
+            def forward():
+                with rt.command():
+                    with rt._execution_plan(("bge_plan", layers, seq), bindings) as replayed:
+                        if not replayed:
+                            for s in sets:
+                                bge_layer_launch(rt, s, lengths_buf, tokens, seq)
+
+            with rt._workspace():
+                for _ in range(args.warmup + 2):
+                    forward()
+                start = time.perf_counter()
+                reps = max(args.steps, 50)
+                for _ in range(reps):
+                    forward()
+                per = (time.perf_counter() - start) / reps
+            return per, rt.diagnostics()
+
+    with_graphs, diag = measure(True)
+    without, _ = measure(False)
+    return {
+        "metric": "BGE-small 12-layer encoder forward on one 128-token sequence, plan replay, 1 GPU",
+        "value": tokens / with_graphs,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": max(args.steps, 50),
+        "warmup": args.warmup,
+        "ms_per_step": with_graphs * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "bge_plan_1x128: 12 encoder layers (144 launches) per forward, "
+                               "replayed as one prepared plan", "batch": batch, "seq": seq,
+                   "layers": layers},
+        "ms_per_forward_graphs": with_graphs * 1e3,
+        "ms_per_forward_launches": without * 1e3,
+        "graph_builds": diag["graph_builds"],
+        "graph_launches": diag["graph_launches"],
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__,
                                      formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -649,7 +726,7 @@ def main() -> int:
     parser.add_argument("--layers", type=int, default=LAYERS, help="headline workload only")
     parser.add_argument("--workload", default="qwen3_32x512",
                         choices=["qwen3_32x512", "qwen3_8x512", "bge_32x512", "qwen_qkv4_16x256",
-                                 "qwen_tail_16x256", "bge_layer_32x512"])
+                                 "qwen_tail_16x256", "bge_layer_32x512", "bge_plan_1x128"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="also launch one copy of this many MiB (traffic-counter calibration)")
@@ -676,6 +753,8 @@ def main() -> int:
         result = bench_qwen_tail(args)
     elif args.workload == "bge_layer_32x512":
         result = bench_bge_layer(args)
+    elif args.workload == "bge_plan_1x128":
+        result = bench_bge_plan(args)
     else:
         result = bench_qkv4_block(args)
     print(json.dumps(result), flush=True)

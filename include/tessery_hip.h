@@ -66,7 +66,14 @@ int mi_plan_add(void *plan, const char *name, const uint32_t *slots, uint32_t co
                 const void *params, uint64_t threads, uint32_t group);
 uint64_t mi_plan_bytes(void *plan);
 void mi_plan_free(void *plan);
+/* A replayed plan runs as one HIP graph launch: the graph of a plan for one binding of its slots
+ * (device pointers) is captured and instantiated on first use, cached with the plan (at most 4
+ * bindings) and freed by mi_plan_free. The environment variable TESSERY_HIP_GRAPHS=0, read by
+ * mi_create, turns this off (launches one by one, the same results). */
 int mi_plan_run(void *runtime, void *plan, void **buffers, uint32_t count);
+/* No counterpart in the reference: the number of graph launches and graph instantiations of plan
+ * replays since mi_create (diagnostics). */
+int mi_graph_counts(void *runtime, uint64_t *launches, uint64_t *builds);
 
 /* No counterpart in the reference (unified memory made it unnecessary there): copy `bytes`
  * host bytes into an existing device buffer, synchronously. */

@@ -11,6 +11,7 @@
 
 #include <array>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <tuple>
@@ -113,6 +114,7 @@ Route find_route(const char* name, uint32_t* nbuf) {
 }
 
 struct Runtime;
+struct Plan;
 
 struct Buffer {
   void* ptr;
@@ -135,8 +137,19 @@ struct RopeTable {
   float* sin;
 };
 
+// Ops [first, first + count) of the queued command came from one plan replay bound to `key` (the
+// device pointers of the plan's slots).
+struct Segment {
+  size_t first, count;
+  Plan* plan;
+  std::vector<void*> key;
+};
+
 struct Runtime {
   int device = 0;
+  bool graphs = true;  // replay plans through cached HIP graphs (TESSERY_HIP_GRAPHS=0 disables)
+  uint64_t graph_launches = 0, graph_builds = 0;
+  std::vector<Segment> segments;
   hipStream_t stream = nullptr;
   hipEvent_t ev_start = nullptr, ev_end = nullptr;
   bool recording = false;
@@ -157,11 +170,20 @@ struct PlanOp {
   std::array<uint32_t, kMaxBuffers> slots;
 };
 
+// An instantiated HIP graph of a plan's launches for one binding of its slots.
+struct CachedGraph {
+  std::vector<void*> key;
+  hipGraphExec_t exec;
+};
+
 struct Plan {
   Runtime* owner;
   std::vector<uint64_t> sizes;
   std::vector<PlanOp> ops;
+  std::vector<CachedGraph> graphs;  // most recently used last, at most kPlanGraphs
 };
+
+constexpr size_t kPlanGraphs = 4;
 
 inline uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
@@ -681,6 +703,8 @@ void* mi_create(const char* /*source*/) {
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return nullptr;
   auto rt = new Runtime();
   rt->device = device;
+  const char* graphs = std::getenv("TESSERY_HIP_GRAPHS");
+  rt->graphs = !(graphs && std::strcmp(graphs, "0") == 0);
   if (hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking) != hipSuccess ||
       hipEventCreate(&rt->ev_start) != hipSuccess || hipEventCreate(&rt->ev_end) != hipSuccess) {
     mi_destroy(rt);
@@ -815,6 +839,64 @@ hipError_t launch_fused_pair(Runtime* rt, const Op& a, const Op& b) {
   return hipErrorNotReady;
 }
 
+// Launches ops [first, last) in order, pairing what launch_fused_pair can run as one kernel.
+hipError_t launch_range(Runtime* rt, size_t first, size_t last) {
+  for (size_t i = first; i < last; ++i) {
+    const hipError_t fused =
+        i + 1 < last ? launch_fused_pair(rt, rt->ops[i], rt->ops[i + 1]) : hipErrorNotReady;
+    if (fused == hipSuccess) {
+      ++i;
+      continue;
+    }
+    if (fused != hipErrorNotReady) return fused;
+    const hipError_t e = launch(rt, rt->ops[i]);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+// A plan replay as one graph launch: the graph of this plan for this binding is instantiated the
+// first time (stream capture of launch_range, which records the same kernels with the same
+// arguments) and reused afterwards. Captured launches do not run, so on any capture error the
+// caller launches the segment directly. hipErrorNotReady: graphs are off for this runtime.
+hipError_t launch_segment_graph(Runtime* rt, const Segment& seg) {
+  if (!rt->graphs) return hipErrorNotReady;
+  auto& cache = seg.plan->graphs;
+  for (size_t j = 0; j < cache.size(); ++j)
+    if (cache[j].key == seg.key) {
+      CachedGraph hit = cache[j];
+      cache.erase(cache.begin() + static_cast<std::ptrdiff_t>(j));
+      cache.push_back(hit);
+      ++rt->graph_launches;
+      return hipGraphLaunch(hit.exec, rt->stream);
+    }
+  if (hipStreamBeginCapture(rt->stream, hipStreamCaptureModeThreadLocal) != hipSuccess)
+    return hipErrorNotReady;
+  const hipError_t recorded = launch_range(rt, seg.first, seg.first + seg.count);
+  hipGraph_t graph = nullptr;
+  const hipError_t ended = hipStreamEndCapture(rt->stream, &graph);
+  if (recorded != hipSuccess || ended != hipSuccess || !graph) {
+    if (graph) (void)hipGraphDestroy(graph);
+    (void)hipGetLastError();
+    return hipErrorNotReady;
+  }
+  hipGraphExec_t exec = nullptr;
+  const hipError_t made = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (made != hipSuccess || !exec) {
+    (void)hipGetLastError();
+    return hipErrorNotReady;
+  }
+  if (cache.size() >= kPlanGraphs) {
+    (void)hipGraphExecDestroy(cache.front().exec);
+    cache.erase(cache.begin());
+  }
+  cache.push_back(CachedGraph{seg.key, exec});
+  ++rt->graph_builds;
+  ++rt->graph_launches;
+  return hipGraphLaunch(exec, rt->stream);
+}
+
 int mi_finish(void* runtime) {
   auto rt = static_cast<Runtime*>(runtime);
   if (!rt || !rt->recording) return 1;
@@ -829,7 +911,25 @@ int mi_finish(void* runtime) {
     }
   }
   if (hipEventRecord(rt->ev_start, rt->stream) != hipSuccess) failed = 1;
-  for (size_t i = 0; i < n && !failed; ++i) {
+  if (!rt->profiling) {
+    // plan replays run as cached graphs (plans are never replayed while profiling); the rest,
+    // and any segment whose graph could not be made, launch one by one
+    size_t i = 0;
+    for (const Segment& seg : rt->segments) {
+      if (failed) break;
+      if (launch_range(rt, i, seg.first) != hipSuccess) failed = 1;
+      if (failed) break;
+      const hipError_t g = launch_segment_graph(rt, seg);
+      if (g == hipErrorNotReady) {
+        if (launch_range(rt, seg.first, seg.first + seg.count) != hipSuccess) failed = 1;
+      } else if (g != hipSuccess) {
+        failed = 1;
+      }
+      i = seg.first + seg.count;
+    }
+    if (!failed && launch_range(rt, i, n) != hipSuccess) failed = 1;
+  }
+  for (size_t i = 0; rt->profiling && i < n && !failed; ++i) {
     if (rt->profiling && hipEventRecord(rt->prof_events[2 * i], rt->stream) != hipSuccess) failed = 1;
     // a fused pair runs inside the first op's events; the second op's events enclose no work
     const hipError_t fused =
@@ -866,6 +966,7 @@ int mi_finish(void* runtime) {
     if (failed) rt->profile_seconds.clear();
   }
   rt->ops.clear();
+  rt->segments.clear();
   rt->recording = false;
   return failed;
 }
@@ -879,6 +980,7 @@ void mi_abort(void* runtime) {
   auto rt = static_cast<Runtime*>(runtime);
   if (!rt) return;
   rt->ops.clear();  // queued work was never launched
+  rt->segments.clear();
   rt->recording = false;
 }
 
@@ -946,7 +1048,20 @@ uint64_t mi_plan_bytes(void* plan) {
          pl->ops.capacity() * sizeof(PlanOp);
 }
 
-void mi_plan_free(void* plan) { delete static_cast<Plan*>(plan); }
+int mi_graph_counts(void* runtime, uint64_t* launches, uint64_t* builds) {
+  auto rt = static_cast<Runtime*>(runtime);
+  if (!rt || !launches || !builds) return 1;
+  *launches = rt->graph_launches;
+  *builds = rt->graph_builds;
+  return 0;
+}
+
+void mi_plan_free(void* plan) {
+  auto pl = static_cast<Plan*>(plan);
+  if (!pl) return;
+  for (auto& g : pl->graphs) (void)hipGraphExecDestroy(g.exec);
+  delete pl;
+}
 
 int mi_plan_run(void* runtime, void* plan, void** buffers, uint32_t count) {
   auto rt = static_cast<Runtime*>(runtime);
@@ -974,6 +1089,9 @@ int mi_plan_run(void* runtime, void* plan, void** buffers, uint32_t count) {
     make_op(po.route, po.p, po.threads, po.group, ptrs, sizes, po.count, &op);
     rt->ops.push_back(op);
   }
+  Segment seg{rt->ops.size() - pl->ops.size(), pl->ops.size(), pl, {}};
+  for (uint32_t i = 0; i < count; ++i) seg.key.push_back(static_cast<Buffer*>(buffers[i])->ptr);
+  rt->segments.push_back(std::move(seg));
   return 0;
 }
 

@@ -244,3 +244,80 @@ def test_fused_projection_gelu_and_residual_norm_are_bit_exact(runtime, rows, co
     np.testing.assert_allclose(fused_y, expected_y, atol=5e-5, rtol=5e-5)
     np.testing.assert_allclose(fused_r, ref.layer_norm(resid + expected_y, lw, lb, 1e-12),
                                atol=5e-5, rtol=5e-5)
+
+
+def plan_replays(runtime, x, lengths, w, heads, eps, replays):
+    """The BGE layer of bge_layer() captured once as a plan and replayed `replays` times over the
+    same buffers; x is rewritten from the host before every replay (eager work between them).
+    Returns the layer output of the capture run and of every replay."""
+    b, s, hidden = x.shape
+    tokens, inter = b * s, w["i"].shape[0]
+    bufs = {name: runtime.upload(a) for name, a in w.items()}
+    bufs["x"] = runtime.upload(x.reshape(tokens, hidden))
+    bufs["len"] = runtime.upload(lengths.astype(np.uint32))
+    for name, width in (("q_", hidden), ("k_", hidden), ("v_", hidden), ("att", hidden),
+                        ("proj", hidden), ("act", inter)):
+        bufs[name] = runtime.buffer(tokens * width * 4)
+    order = sorted(bufs)
+    outs = []
+
+    def linear(src, dst, name, outputs, inputs):
+        runtime._matmul_bias_f32([bufs[src], bufs[name], bufs[dst], bufs[name + "_b"]], rows=tokens,
+                                 cols=outputs, k=inputs)
+
+    def norm(name):
+        runtime._dispatch("layer_norm", [bufs["x"], bufs[name + "_w"], bufs[name + "_b"], bufs["x"]],
+                          threads=tokens * 32, group_size=32, cols=hidden, eps=eps)
+
+    try:
+        with runtime._workspace():
+            for _ in range(replays + 1):
+                runtime.write(bufs["x"], x.reshape(tokens, hidden))
+                with runtime.command():
+                    with runtime._execution_plan(("bge", b, s), [bufs[n] for n in order]) as replayed:
+                        if not replayed:
+                            for target, name in (("q_", "q"), ("k_", "k"), ("v_", "v")):
+                                linear("x", target, name, hidden, hidden)
+                            runtime._attention([bufs["q_"], bufs["k_"], bufs["v_"], bufs["len"],
+                                                bufs["att"]], tokens=tokens, seq=s, heads=heads,
+                                               kv_heads=heads, dim=hidden // heads, bidirectional=True)
+                            linear("att", "proj", "o", hidden, hidden)
+                            runtime._dispatch("add", [bufs["x"], bufs["proj"], bufs["x"]],
+                                              threads=tokens * hidden, n=tokens * hidden)
+                            norm("ln1")
+                            linear("x", "act", "i", inter, hidden)
+                            runtime._dispatch("gelu_f32", [bufs["act"]], threads=tokens * inter,
+                                              n=tokens * inter)
+                            linear("act", "proj", "out", hidden, inter)
+                            runtime._dispatch("add", [bufs["x"], bufs["proj"], bufs["x"]],
+                                              threads=tokens * hidden, n=tokens * hidden)
+                            norm("ln2")
+                outs.append(runtime.read(bufs["x"], x.shape))
+        return outs
+    finally:
+        for bb in bufs.values():
+            bb.close()
+
+
+@pytest.mark.parametrize("graphs", ["1", "0"])
+def test_plan_replay_graphs_match_eager(monkeypatch, graphs):
+    """Plan replays run as cached HIP graphs (TESSERY_HIP_GRAPHS=0: launched one by one); every
+    replay, with host writes and synchronizations between them, equals the eager capture run
+    bit for bit, and that run matches the float64 oracle."""
+    from tessery_amd import HipRuntime
+
+    monkeypatch.setenv("TESSERY_HIP_GRAPHS", graphs)
+    rng = np.random.default_rng(71)
+    hidden, heads, inter, eps = 384, 12, 1536, 1e-12
+    x = rng.normal(size=(2, 64, hidden)).astype(np.float32)
+    lengths = np.array([64, 23], np.uint32)
+    w = bge_weights(rng, hidden, inter)
+    with HipRuntime() as rt:
+        outs = plan_replays(rt, x, lengths, w, heads, eps, replays=5)
+        diag = rt.diagnostics()
+    assert diag["plan_builds"] == 1 and diag["plan_hits"] == 5
+    assert (diag["graph_builds"], diag["graph_launches"]) == ((1, 5) if graphs == "1" else (0, 0))
+    for out in outs[1:]:
+        np.testing.assert_array_equal(out, outs[0])
+    np.testing.assert_allclose(outs[0], ref.layer(x, lengths, w, heads=heads, eps=eps), atol=5e-5,
+                               rtol=5e-5)
