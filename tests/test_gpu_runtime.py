@@ -65,6 +65,57 @@ def test_invalid_shapes_are_rejected_before_launch(runtime):
             b.close()
 
 
+@pytest.mark.parametrize("case", ["gated_rows", "gated_threads", "gated_small_out", "matmul_small_w",
+                                  "tiled_cols", "layer_norm_group", "silu_small_up", "gelu_zero"])
+def test_layer_routes_reject_bad_launches(runtime, case):
+    """The projection, gated and elementwise routes refuse launches whose thread formula or
+    buffer sizes do not match Params, at dispatch time (nothing is queued)."""
+    f = lambda *shape: runtime.buffer(int(np.prod(shape)) * 4)  # noqa: E731
+    w32 = runtime.buffer(64 * (64 // 8) * 4)
+    sb = runtime.buffer(64 * (64 // 64) * 2)
+    bufs = [w32, sb]
+    try:
+        if case.startswith("gated"):
+            x, out = f(16, 64), f(16 if case != "gated_small_out" else 8, 64)
+            bufs += [x, out]
+            rows = 8 if case == "gated_rows" else 16
+            threads = 2 * 256 if case != "gated_threads" else 2 * 256 + 1
+            args = dict(threads=threads, group_size=256, rows=rows, cols=64, k=64)
+            with pytest.raises(InferenceError), runtime.command():
+                runtime._dispatch("gated4_16x32_k64", [x, w32, sb, sb, w32, sb, sb, out], **args)
+        elif case == "matmul_small_w":
+            x, w, out = f(8, 64), f(32, 64), f(8, 64)
+            bufs += [x, w, out]
+            with pytest.raises(InferenceError), runtime.command():
+                runtime._dispatch("matmul_f32_tiled", [x, w, out], threads=2 * 128, group_size=128,
+                                  rows=8, cols=64, k=64)
+        elif case == "tiled_cols":
+            x, w, out = f(8, 64), f(48, 64), f(8, 48)
+            bufs += [x, w, out]
+            with pytest.raises(InferenceError), runtime.command():
+                runtime._dispatch("matmul_f32_chunk32", [x, w, out], threads=128, group_size=128,
+                                  rows=8, cols=48, k=64)
+        elif case == "layer_norm_group":
+            x, v = f(4, 64), f(64)
+            bufs += [x, v]
+            with pytest.raises(InferenceError), runtime.command():
+                runtime._dispatch("layer_norm", [x, v, v, x], threads=4 * 64, group_size=64, cols=64)
+        elif case == "silu_small_up":
+            g, u = f(100), f(99)
+            bufs += [g, u]
+            with pytest.raises(InferenceError), runtime.command():
+                runtime._dispatch("silu_gate", [g, u], threads=100, n=100)
+        else:
+            x = f(10)
+            bufs += [x]
+            with pytest.raises(InferenceError), runtime.command():
+                runtime._dispatch("gelu_f32", [x], threads=1, n=0)
+    finally:
+        for b in bufs:
+            b.close()
+    assert runtime.active_bytes == 0
+
+
 def test_aborted_command_launches_nothing(runtime):
     x = np.arange(64, dtype=np.float32)
     a, out = runtime.upload(x), runtime.upload(np.full(64, -1.0, np.float32))
