@@ -1059,6 +1059,11 @@ int mi_graph_counts(void* runtime, uint64_t* launches, uint64_t* builds) {
 void mi_plan_free(void* plan) {
   auto pl = static_cast<Plan*>(plan);
   if (!pl) return;
+  // A replay of this plan may still be queued in the open command (a plan can be evicted while
+  // another one is captured): its launches stay queued and run one by one.
+  auto& segs = pl->owner->segments;
+  for (size_t i = segs.size(); i-- > 0;)
+    if (segs[i].plan == pl) segs.erase(segs.begin() + static_cast<std::ptrdiff_t>(i));
   for (auto& g : pl->graphs) (void)hipGraphExecDestroy(g.exec);
   delete pl;
 }

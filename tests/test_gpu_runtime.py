@@ -181,3 +181,35 @@ def test_plan_capture_and_replay(runtime):
     diag = runtime.diagnostics()
     assert diag["plan_builds"] == 1 and diag["plan_hits"] == 2
     assert diag["dispatches"] == {"attention_tiled": 3}
+
+
+def test_plan_evicted_while_its_replay_is_queued(runtime):
+    """A replayed plan evicted from the cache by later captures in the same command (the cache
+    holds 4 plans) still runs its queued launches."""
+    rng = np.random.default_rng(15)
+    q = rng.normal(size=(1, 64, 2, 32)).astype(np.float32)
+    k, v = [rng.normal(size=(1, 64, 2, 32)).astype(np.float32) for _ in range(2)]
+    lengths = np.array([40], np.uint32)
+    expected = ref.attention(q, k, v, lengths, bidirectional=False)
+    bufs = [runtime.upload(a) for a in (q, k, v, lengths)] + [runtime.buffer(q.nbytes)]
+    outs = [runtime.buffer(q.nbytes) for _ in range(5)]
+    try:
+        with runtime._workspace():
+            def plan(key, out):
+                binding = bufs[:4] + [out]
+                with runtime._execution_plan(key, binding) as replayed:
+                    if not replayed:
+                        runtime._attention(binding, tokens=64, seq=64, heads=2, kv_heads=2, dim=32)
+
+            with runtime.command():
+                plan(("a",), bufs[4])          # capture A
+            with runtime.command():
+                plan(("a",), bufs[4])          # replay A (queued) ...
+                for i in range(4):             # ... then four captures evict it
+                    plan(("b", i), outs[i])
+            assert runtime.diagnostics()["plan_hits"] == 1
+            for out in [bufs[4]] + outs[:4]:
+                check_f32(runtime.read(out, q.shape), expected)
+    finally:
+        for b in bufs + outs:
+            b.close()
