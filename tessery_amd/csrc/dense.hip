@@ -7,6 +7,8 @@
 // (the chunk32 order, kernels.metal:416-436), every route runs this one kernel, and the bias is
 // added once after the last partial sum.
 // add_bias, gelu_f32 and layer_norm follow kernels.metal:362-394.
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -32,12 +34,14 @@ __device__ __forceinline__ float gelu_value(float value) {
   return 0.5f * value * (value < 0.0f ? tail : 2.0f - tail);
 }
 
-template <bool BIAS, bool GELU>
+// PARTIAL: workgroup z sums chunks [z * per, (z + 1) * per) only and stores its raw sums to
+// out + z * (row1 - row0) * cols (rows relative to row0), for dense_reduce to add in z order.
+template <bool BIAS, bool GELU, bool PARTIAL>
 __global__ __launch_bounds__(256) void matmul_f32(const float* __restrict__ a,
                                                   const float* __restrict__ bt,
                                                   const float* __restrict__ bias,
                                                   float* __restrict__ out, int row0, int row1,
-                                                  int cols, int k) {
+                                                  int cols, int k, int per) {
   constexpr int XROW = 64 + 4;
   __shared__ __attribute__((aligned(16))) float xs[kDenseRows * XROW];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
@@ -45,7 +49,9 @@ __global__ __launch_bounds__(256) void matmul_f32(const float* __restrict__ a,
   const int n = blockIdx.y * 128 + wave * 32 + l32;
   const bool nvalid = n < cols;
   const bool vec = (k & 3) == 0;  // rows start 16-byte aligned: float4 loads
-  const int chunks = (k + 63) / 64;
+  const int all_chunks = (k + 63) / 64;
+  const int c_begin = PARTIAL ? static_cast<int>(blockIdx.z) * per : 0;
+  const int c_end = PARTIAL ? min(c_begin + per, all_chunks) : all_chunks;
   floatx16 acc[2];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
@@ -73,8 +79,8 @@ __global__ __launch_bounds__(256) void matmul_f32(const float* __restrict__ a,
       xr[i] = t;
     }
   };
-  load_x(0);
-  for (int ci = 0; ci < chunks; ++ci) {
+  load_x(c_begin * 64);
+  for (int ci = c_begin; ci < c_end; ++ci) {
     const int k0 = ci * 64;
     float wv[32];
     {
@@ -101,7 +107,7 @@ __global__ __launch_bounds__(256) void matmul_f32(const float* __restrict__ a,
       *reinterpret_cast<floatx4*>(&xs[(c / 16) * XROW + 4 * (c % 16)]) = xr[i];
     }
     __syncthreads();
-    if (ci + 1 < chunks) load_x(k0 + 64);
+    if (ci + 1 < c_end) load_x(k0 + 64);
     // K32 partial sums per 32-row tile, each added to its total (the chunk32 order)
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
@@ -124,16 +130,38 @@ __global__ __launch_bounds__(256) void matmul_f32(const float* __restrict__ a,
   }
   if (!nvalid) return;
   const float b = BIAS ? bias[n] : 0.0f;
+  // rows of a partial are counted from row0
+  float* const dst = PARTIAL ? out + static_cast<size_t>(blockIdx.z) * (row1 - row0) * cols : out;
+  const int rfirst = PARTIAL ? row0 : 0;
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int r = rbase + 32 * rt + 8 * (e >> 2) + 4 * hh + (e & 3);
       if (r < row1) {
-        const float y = BIAS ? acc[rt][e] + b : acc[rt][e];
-        out[static_cast<size_t>(r) * cols + n] = GELU ? gelu_value(y) : y;
+        const size_t at = static_cast<size_t>(r - rfirst) * cols + n;
+        if constexpr (PARTIAL) {
+          dst[at] = acc[rt][e];
+        } else {
+          const float y = BIAS ? acc[rt][e] + b : acc[rt][e];
+          dst[at] = GELU ? gelu_value(y) : y;
+        }
       }
     }
+}
+
+// Split-K epilogue: out[r][n] = sum over z in order of part[z][r - row0][n] (+ bias, GELU).
+template <bool BIAS, bool GELU>
+__global__ __launch_bounds__(256) void dense_reduce(const float* __restrict__ part,
+                                                    const float* __restrict__ bias,
+                                                    float* __restrict__ out, int row0, int rows,
+                                                    int cols, int splits) {
+  const size_t i = blockIdx.x * 256ull + threadIdx.x, total = static_cast<size_t>(rows) * cols;
+  if (i >= total) return;
+  float y = part[i];
+  for (int z = 1; z < splits; ++z) y += part[static_cast<size_t>(z) * total + i];
+  if (BIAS) y += bias[i % cols];
+  out[static_cast<size_t>(row0) * cols + i] = GELU ? gelu_value(y) : y;
 }
 
 // x[i] += bias[i % cols] (kernels.metal:376-379)
@@ -182,19 +210,50 @@ __global__ __launch_bounds__(256) void layer_norm_f32(float* x, const float* r,
   for (int c = lane; c < cols; c += 64) orow[c] = (xr[c] - mean) * inv * w[c] + bias[c];
 }
 
+int dense_splits(int rows, int cols, int k, size_t scratch_floats) {
+  const int tiles = ((rows + kDenseRows - 1) / kDenseRows) * ((cols + 127) / 128);
+  const int chunks = (k + 63) / 64;
+  if (tiles >= 128 || chunks < 4) return 1;
+  int splits = std::min(chunks, (256 + tiles - 1) / tiles);
+  const int per = (chunks + splits - 1) / splits;
+  splits = (chunks + per - 1) / per;  // no empty split
+  if (static_cast<size_t>(splits) * rows * cols > scratch_floats) return 1;
+  return splits;
+}
+
 hipError_t launch_matmul_f32(const float* a, const float* bt, const float* bias, float* out,
-                             int row0, int row1, int cols, int k, bool gelu, hipStream_t st) {
+                             int row0, int row1, int cols, int k, bool gelu, float* scratch,
+                             size_t scratch_floats, hipStream_t st) {
   if (row1 <= row0 || cols <= 0) return hipSuccess;
   if (k <= 0) return hipErrorInvalidValue;
-  dim3 grid((row1 - row0 + kDenseRows - 1) / kDenseRows, (cols + 127) / 128);
+  const int rows = row1 - row0, chunks = (k + 63) / 64;
+  const int splits = scratch ? dense_splits(rows, cols, k, scratch_floats) : 1;
+  if (splits > 1) {
+    // few output tiles (small batches): K split over workgroups, partial sums added in order
+    const int per = (chunks + splits - 1) / splits;
+    dim3 grid((rows + kDenseRows - 1) / kDenseRows, (cols + 127) / 128, splits);
+    matmul_f32<false, false, true><<<grid, 256, 0, st>>>(a, bt, nullptr, scratch, row0, row1,
+                                                         cols, k, per);
+    const unsigned blocks = static_cast<unsigned>((static_cast<size_t>(rows) * cols + 255) / 256);
+    if (bias && gelu)
+      dense_reduce<true, true><<<blocks, 256, 0, st>>>(scratch, bias, out, row0, rows, cols, splits);
+    else if (bias)
+      dense_reduce<true, false><<<blocks, 256, 0, st>>>(scratch, bias, out, row0, rows, cols, splits);
+    else if (gelu)
+      dense_reduce<false, true><<<blocks, 256, 0, st>>>(scratch, nullptr, out, row0, rows, cols, splits);
+    else
+      dense_reduce<false, false><<<blocks, 256, 0, st>>>(scratch, nullptr, out, row0, rows, cols, splits);
+    return hipGetLastError();
+  }
+  dim3 grid((rows + kDenseRows - 1) / kDenseRows, (cols + 127) / 128);
   if (bias && gelu)
-    matmul_f32<true, true><<<grid, 256, 0, st>>>(a, bt, bias, out, row0, row1, cols, k);
+    matmul_f32<true, true, false><<<grid, 256, 0, st>>>(a, bt, bias, out, row0, row1, cols, k, 0);
   else if (bias)
-    matmul_f32<true, false><<<grid, 256, 0, st>>>(a, bt, bias, out, row0, row1, cols, k);
+    matmul_f32<true, false, false><<<grid, 256, 0, st>>>(a, bt, bias, out, row0, row1, cols, k, 0);
   else if (gelu)
-    matmul_f32<false, true><<<grid, 256, 0, st>>>(a, bt, nullptr, out, row0, row1, cols, k);
+    matmul_f32<false, true, false><<<grid, 256, 0, st>>>(a, bt, nullptr, out, row0, row1, cols, k, 0);
   else
-    matmul_f32<false, false><<<grid, 256, 0, st>>>(a, bt, nullptr, out, row0, row1, cols, k);
+    matmul_f32<false, false, false><<<grid, 256, 0, st>>>(a, bt, nullptr, out, row0, row1, cols, k, 0);
   return hipGetLastError();
 }
 

@@ -65,8 +65,11 @@ hipError_t launch_silu_gate_f32(float* gate, const float* up, uint32_t n, hipStr
 // for rows [row0, row1), any K and N (tessery matmul_f32 / matmul_bias_f32 families,
 // kernels.metal:306-322, 396-487); with gelu the stored value is gelu_f32 of it, bit-identical to
 // the projection followed by the gelu_f32 route.
+// With few output tiles (small batches) and a scratch buffer of scratch_floats floats, K is
+// split over workgroups and the partial sums are added in a fixed order by a second kernel.
 hipError_t launch_matmul_f32(const float* a, const float* bt, const float* bias, float* out,
-                             int row0, int row1, int cols, int k, bool gelu, hipStream_t st);
+                             int row0, int row1, int cols, int k, bool gelu, float* scratch,
+                             size_t scratch_floats, hipStream_t st);
 // x[i] += bias[i % cols] (kernels.metal:376-379).
 hipError_t launch_add_bias_f32(float* x, const float* bias, uint32_t n, uint32_t cols,
                                hipStream_t st);

@@ -149,6 +149,7 @@ struct Runtime {
   int device = 0;
   bool graphs = true;  // replay plans through cached HIP graphs (TESSERY_HIP_GRAPHS=0 disables)
   uint64_t graph_launches = 0, graph_builds = 0;
+  float* dense_scratch = nullptr;  // split-K partial sums of small-batch projections
   std::vector<Segment> segments;
   hipStream_t stream = nullptr;
   hipEvent_t ev_start = nullptr, ev_end = nullptr;
@@ -498,12 +499,27 @@ bool ensure_rope(Runtime* rt, uint32_t seq, uint32_t dim, float theta) {
   return true;
 }
 
+// Scratch of the split-K projection path, allocated once per runtime on first use (its address
+// never changes, so a captured graph keeps pointing at it).
+constexpr size_t kDenseScratchFloats = size_t{8} << 20;  // 32 MiB
+
 bool prepare(Runtime* rt, Route r, const Params& p) {
   switch (r) {
     case R_ATTENTION_F16_NORM_ROPE:
     case R_NORM_ROPE_F16:
     case R_ROPE:
       return ensure_rope(rt, p.seq, p.dim, p.theta);
+    case R_MATMUL:
+    case R_MATMUL_TILED:
+    case R_MATMUL_CHUNK32:
+    case R_MATMUL_BIAS:
+    case R_MATMUL_BIAS_CHUNK32:
+      if (!rt->dense_scratch &&
+          hipMalloc(&rt->dense_scratch, kDenseScratchFloats * sizeof(float)) != hipSuccess) {
+        rt->dense_scratch = nullptr;
+        return false;
+      }
+      return true;
     default:
       return true;
   }
@@ -639,7 +655,7 @@ hipError_t launch(Runtime* rt, const Op& op) {
           static_cast<const float*>(op.ptr[0]), static_cast<const float*>(op.ptr[1]),
           bias ? static_cast<const float*>(op.ptr[3]) : nullptr, static_cast<float*>(op.ptr[2]),
           static_cast<int>(rr.r0), static_cast<int>(rr.r1), static_cast<int>(p.cols),
-          static_cast<int>(p.k), false, st);
+          static_cast<int>(p.k), false, rt->dense_scratch, kDenseScratchFloats, st);
     }
     case R_ADD_BIAS:
       return tessery::launch_add_bias_f32(static_cast<float*>(op.ptr[0]),
@@ -722,6 +738,7 @@ void mi_destroy(void* runtime) {
     (void)hipFree(kv.second.cos);
     (void)hipFree(kv.second.sin);
   }
+  if (rt->dense_scratch) (void)hipFree(rt->dense_scratch);
   release_profile_events(rt);
   if (rt->ev_start) (void)hipEventDestroy(rt->ev_start);
   if (rt->ev_end) (void)hipEventDestroy(rt->ev_end);
@@ -826,7 +843,8 @@ hipError_t launch_fused_pair(Runtime* rt, const Op& a, const Op& b) {
     return tessery::launch_matmul_f32(
         static_cast<const float*>(a.ptr[0]), static_cast<const float*>(a.ptr[1]),
         bias ? static_cast<const float*>(a.ptr[3]) : nullptr, static_cast<float*>(a.ptr[2]),
-        0, static_cast<int>(rr.r1), static_cast<int>(a.p.cols), static_cast<int>(a.p.k), true, st);
+        0, static_cast<int>(rr.r1), static_cast<int>(a.p.cols), static_cast<int>(a.p.k), true,
+        rt->dense_scratch, kDenseScratchFloats, st);
   }
   if (a.route == R_ADD && b.route == R_LAYER_NORM && a.ptr[2] == a.ptr[0] &&
       b.ptr[0] == a.ptr[0] && b.ptr[3] == a.ptr[0] && a.ptr[1] != a.ptr[0] &&
