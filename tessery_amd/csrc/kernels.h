@@ -49,15 +49,17 @@ hipError_t launch_norm_rope_f16(const _Float16* x, _Float16* y, const uint16_t* 
 
 // uint4 affine group-64 projection, fp32 activations, bf16 scale/bias (tessery linear4 family,
 // kernels.metal:11-19, 32-51, 489-605, 655-684, 733-773). Computes rows [row0, row1).
+// With few output tiles and a scratch buffer, K is split over workgroups (partial sums added in a
+// fixed order by a second kernel), as for the dense projections.
 hipError_t launch_linear4_f32(const float* x, const uint32_t* w, const uint16_t* scales,
                               const uint16_t* biases, float* out, int row0, int row1, int cols,
-                              int k, hipStream_t st);
+                              int k, float* scratch, size_t scratch_floats, hipStream_t st);
 // Gate and up projections of rows [row0, row1) with out = silu(gate) * up (tessery gated4,
 // kernels.metal:609-656, 687-731), bit-identical to linear4 + linear4 + silu_gate.
 hipError_t launch_gated4_f32(const float* x, const uint32_t* w, const uint16_t* scales,
                              const uint16_t* biases, const uint32_t* uw, const uint16_t* uscales,
                              const uint16_t* ubiases, float* out, int row0, int row1, int cols,
-                             int k, hipStream_t st);
+                             int k, float* scratch, size_t scratch_floats, hipStream_t st);
 // gate[i] = silu(gate[i]) * up[i] for i < n (tessery silu_gate, kernels.metal:334-337).
 hipError_t launch_silu_gate_f32(float* gate, const float* up, uint32_t n, hipStream_t st);
 

@@ -13,6 +13,8 @@
 // out = silu(gate) * up (kernels.metal:609-656, 687-731); each projection keeps the linear4
 // reduction order and the epilogue is silu_gate's expression, so the fused routes are
 // bit-identical to linear4 + linear4 + silu_gate over the same rows.
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -72,13 +74,16 @@ __device__ __forceinline__ void group_product(const float* xs, int xrow, int row
 // GATED: a second weight set (uw, us, ub) accumulates the up projection beside the gate.
 constexpr int kL4Rows = 64;
 
-template <bool GATED>
+// PARTIAL: workgroup z sums groups [z * per, (z + 1) * per) only and stores its raw sums (gate,
+// then up at + splits * rows * cols) to out + z * rows * cols, rows counted from row0, for
+// linear4_reduce to add in z order.
+template <bool GATED, bool PARTIAL>
 __global__ __launch_bounds__(256) void linear4_f32(
     const float* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     const uint32_t* __restrict__ uw, const uint16_t* __restrict__ uscales,
     const uint16_t* __restrict__ ubiases, float* __restrict__ out, int row0, int row1, int cols,
-    int k) {
+    int k, int per) {
   constexpr int XROW = 64 + 4;
   constexpr int XV = kL4Rows * 16 / 256;  // four-float x pieces per thread per group
   __shared__ __attribute__((aligned(16))) float xs[kL4Rows * XROW];
@@ -86,7 +91,9 @@ __global__ __launch_bounds__(256) void linear4_f32(
   const int rbase = row0 + blockIdx.x * kL4Rows;
   const int n = blockIdx.y * 128 + wave * 32 + l32;
   const bool nvalid = n < cols;
-  const int groups = k / 64;
+  const int all_groups = k / 64;
+  const int g_begin = PARTIAL ? static_cast<int>(blockIdx.z) * per : 0;
+  const int g_end = PARTIAL ? min(g_begin + per, all_groups) : all_groups;
   floatx16 acc[2], uacc[2];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
@@ -107,8 +114,8 @@ __global__ __launch_bounds__(256) void linear4_f32(
       xr[i] = t;
     }
   };
-  load_x(0);
-  for (int gi = 0; gi < groups; ++gi) {
+  load_x(g_begin);
+  for (int gi = g_begin; gi < g_end; ++gi) {
     float wv[32];
     decode_group(w, scales, biases, n, nvalid, k, gi, hh, wv);
     __syncthreads();
@@ -118,7 +125,7 @@ __global__ __launch_bounds__(256) void linear4_f32(
       *reinterpret_cast<floatx4*>(&xs[(c / 16) * XROW + 4 * (c % 16)]) = xr[i];
     }
     __syncthreads();
-    if (gi + 1 < groups) load_x(gi + 1);
+    if (gi + 1 < g_end) load_x(gi + 1);
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) group_product(xs, XROW, 32 * rt + l32, hh, wv, acc[rt]);
     if constexpr (GATED) {
@@ -128,15 +135,81 @@ __global__ __launch_bounds__(256) void linear4_f32(
     }
   }
   if (!nvalid) return;
+  const size_t plane = static_cast<size_t>(row1 - row0) * cols;
+  float* const dst = PARTIAL ? out + blockIdx.z * plane : out;
+  const int rfirst = PARTIAL ? row0 : 0;
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int r = rbase + 32 * rt + 8 * (e >> 2) + 4 * hh + (e & 3);
-      if (r < row1)
-        out[static_cast<size_t>(r) * cols + n] =
-            GATED ? silu_times(acc[rt][e], uacc[rt][e]) : acc[rt][e];
+      if (r < row1) {
+        const size_t at = static_cast<size_t>(r - rfirst) * cols + n;
+        if constexpr (PARTIAL) {
+          dst[at] = acc[rt][e];
+          if constexpr (GATED) dst[gridDim.z * plane + at] = uacc[rt][e];
+        } else {
+          dst[at] = GATED ? silu_times(acc[rt][e], uacc[rt][e]) : acc[rt][e];
+        }
+      }
     }
+}
+
+// Split-K epilogue: gate (and up) sums added in z order, then silu(gate) * up when GATED.
+template <bool GATED>
+__global__ __launch_bounds__(256) void linear4_reduce(const float* __restrict__ part,
+                                                      float* __restrict__ out, int row0, int rows,
+                                                      int cols, int splits) {
+  const size_t i = blockIdx.x * 256ull + threadIdx.x, total = static_cast<size_t>(rows) * cols;
+  if (i >= total) return;
+  float g = part[i];
+  for (int z = 1; z < splits; ++z) g += part[static_cast<size_t>(z) * total + i];
+  if constexpr (GATED) {
+    const float* up = part + static_cast<size_t>(splits) * total;
+    float u = up[i];
+    for (int z = 1; z < splits; ++z) u += up[static_cast<size_t>(z) * total + i];
+    g = silu_times(g, u);
+  }
+  out[static_cast<size_t>(row0) * cols + i] = g;
+}
+
+// Workgroups split over K when the output has few tiles (small batches); the linear4 and gated4
+// launches of one row range take the same split, so the fused and unfused routes stay
+// bit-identical.
+int linear4_splits(int rows, int cols, int k, size_t scratch_floats) {
+  const int tiles = ((rows + kL4Rows - 1) / kL4Rows) * ((cols + 127) / 128);
+  const int groups = k / 64;
+  if (tiles >= 128 || groups < 4) return 1;
+  int splits = std::min(groups, (256 + tiles - 1) / tiles);
+  const int per = (groups + splits - 1) / splits;
+  splits = (groups + per - 1) / per;
+  // room for two partial sets (gate and up), so linear4 and gated4 split alike
+  if (static_cast<size_t>(2) * splits * rows * cols > scratch_floats) return 1;
+  return splits;
+}
+
+template <bool GATED>
+hipError_t launch_l4(const float* x, const uint32_t* w, const uint16_t* scales,
+                     const uint16_t* biases, const uint32_t* uw, const uint16_t* uscales,
+                     const uint16_t* ubiases, float* out, int row0, int row1, int cols, int k,
+                     float* scratch, size_t scratch_floats, hipStream_t st) {
+  if (row1 <= row0 || cols <= 0) return hipSuccess;
+  if (k % 64) return hipErrorInvalidValue;
+  const int rows = row1 - row0;
+  const int splits = scratch ? linear4_splits(rows, cols, k, scratch_floats) : 1;
+  if (splits > 1) {
+    const int per = (k / 64 + splits - 1) / splits;
+    dim3 grid((rows + kL4Rows - 1) / kL4Rows, (cols + 127) / 128, splits);
+    linear4_f32<GATED, true><<<grid, 256, 0, st>>>(x, w, scales, biases, uw, uscales, ubiases,
+                                                   scratch, row0, row1, cols, k, per);
+    const unsigned blocks = static_cast<unsigned>((static_cast<size_t>(rows) * cols + 255) / 256);
+    linear4_reduce<GATED><<<blocks, 256, 0, st>>>(scratch, out, row0, rows, cols, splits);
+    return hipGetLastError();
+  }
+  dim3 grid((rows + kL4Rows - 1) / kL4Rows, (cols + 127) / 128);
+  linear4_f32<GATED, false><<<grid, 256, 0, st>>>(x, w, scales, biases, uw, uscales, ubiases, out,
+                                                  row0, row1, cols, k, 0);
+  return hipGetLastError();
 }
 
 __global__ __launch_bounds__(256) void silu_gate_f32(float* __restrict__ gate,
@@ -147,25 +220,17 @@ __global__ __launch_bounds__(256) void silu_gate_f32(float* __restrict__ gate,
 
 hipError_t launch_linear4_f32(const float* x, const uint32_t* w, const uint16_t* scales,
                               const uint16_t* biases, float* out, int row0, int row1, int cols,
-                              int k, hipStream_t st) {
-  if (row1 <= row0 || cols <= 0) return hipSuccess;
-  if (k % 64) return hipErrorInvalidValue;
-  dim3 grid((row1 - row0 + kL4Rows - 1) / kL4Rows, (cols + 127) / 128);
-  linear4_f32<false><<<grid, 256, 0, st>>>(x, w, scales, biases, nullptr, nullptr, nullptr, out,
-                                           row0, row1, cols, k);
-  return hipGetLastError();
+                              int k, float* scratch, size_t scratch_floats, hipStream_t st) {
+  return launch_l4<false>(x, w, scales, biases, nullptr, nullptr, nullptr, out, row0, row1, cols,
+                          k, scratch, scratch_floats, st);
 }
 
 hipError_t launch_gated4_f32(const float* x, const uint32_t* w, const uint16_t* scales,
                              const uint16_t* biases, const uint32_t* uw, const uint16_t* uscales,
                              const uint16_t* ubiases, float* out, int row0, int row1, int cols,
-                             int k, hipStream_t st) {
-  if (row1 <= row0 || cols <= 0) return hipSuccess;
-  if (k % 64) return hipErrorInvalidValue;
-  dim3 grid((row1 - row0 + kL4Rows - 1) / kL4Rows, (cols + 127) / 128);
-  linear4_f32<true><<<grid, 256, 0, st>>>(x, w, scales, biases, uw, uscales, ubiases, out, row0,
-                                          row1, cols, k);
-  return hipGetLastError();
+                             int k, float* scratch, size_t scratch_floats, hipStream_t st) {
+  return launch_l4<true>(x, w, scales, biases, uw, uscales, ubiases, out, row0, row1, cols, k,
+                         scratch, scratch_floats, st);
 }
 
 hipError_t launch_silu_gate_f32(float* gate, const float* up, uint32_t n, hipStream_t st) {

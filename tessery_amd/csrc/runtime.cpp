@@ -499,8 +499,8 @@ bool ensure_rope(Runtime* rt, uint32_t seq, uint32_t dim, float theta) {
   return true;
 }
 
-// Scratch of the split-K projection path, allocated once per runtime on first use (its address
-// never changes, so a captured graph keeps pointing at it).
+// Scratch of the split-K projection paths (dense and uint4), allocated once per runtime on first
+// use (its address never changes, so a captured graph keeps pointing at it).
 constexpr size_t kDenseScratchFloats = size_t{8} << 20;  // 32 MiB
 
 bool prepare(Runtime* rt, Route r, const Params& p) {
@@ -514,6 +514,14 @@ bool prepare(Runtime* rt, Route r, const Params& p) {
     case R_MATMUL_CHUNK32:
     case R_MATMUL_BIAS:
     case R_MATMUL_BIAS_CHUNK32:
+    case R_LINEAR4:
+    case R_LINEAR4_TILED:
+    case R_LINEAR4_TAIL:
+    case R_LINEAR4_16X32:
+    case R_LINEAR4_32X32:
+    case R_LINEAR4_SMALL3:
+    case R_GATED4_16X32:
+    case R_GATED4_8X32:
       if (!rt->dense_scratch &&
           hipMalloc(&rt->dense_scratch, kDenseScratchFloats * sizeof(float)) != hipSuccess) {
         rt->dense_scratch = nullptr;
@@ -608,7 +616,8 @@ hipError_t launch(Runtime* rt, const Op& op) {
           static_cast<const float*>(op.ptr[0]), static_cast<const uint32_t*>(op.ptr[1]),
           static_cast<const uint16_t*>(op.ptr[2]), static_cast<const uint16_t*>(op.ptr[3]),
           static_cast<float*>(op.ptr[4]), static_cast<int>(rr.r0), static_cast<int>(rr.r1),
-          static_cast<int>(p.cols), static_cast<int>(p.k), st);
+          static_cast<int>(p.cols), static_cast<int>(p.k), rt->dense_scratch, kDenseScratchFloats,
+          st);
     }
     case R_QKV4_F16: {
       tessery::Qkv4Args a{};
@@ -638,7 +647,7 @@ hipError_t launch(Runtime* rt, const Op& op) {
           static_cast<const uint32_t*>(op.ptr[4]), static_cast<const uint16_t*>(op.ptr[5]),
           static_cast<const uint16_t*>(op.ptr[6]), static_cast<float*>(op.ptr[7]),
           static_cast<int>(rr.r0), static_cast<int>(rr.r1), static_cast<int>(p.cols),
-          static_cast<int>(p.k), st);
+          static_cast<int>(p.k), rt->dense_scratch, kDenseScratchFloats, st);
     }
     case R_SILU_GATE:
       return tessery::launch_silu_gate_f32(static_cast<float*>(op.ptr[0]),
