@@ -18,6 +18,7 @@ HIP-event timings, and the float64 NumPy CPU oracle timed on the host on a bound
                     lengths U{1..256} (seed 5), 8 layers
   qwen_tail_16x256  the rest of the Qwen3 layer on 4096 tokens, fp32 activations: o_proj ->
                     residual -> RMSNorm -> gate/up + SiLU -> down -> residual, 4 layers
+  qwen_tail_1x128   the same tail on one 128-token sequence (fused gated4 route, split-K)
   bge_layer_32x512  whole BGE-small encoder layers (fp32) on 32x512 tokens, lengths U{2..512}
                     (seed 2): projections + bias, attention, LayerNorms, GELU MLP, 4 layers
   bge_plan_1x128    a 12-layer BGE-small stack on one 128-token sequence replayed as a prepared
@@ -432,14 +433,17 @@ def qwen_tail_launch(rt: HipRuntime, s: dict, tokens: int, hidden: int, width: i
     rt._dispatch("add", [s["h"], s["proj"], s["out"]], threads=n, n=n)
 
 
-def bench_qwen_tail(args) -> dict:
-    """Qwen3 layer tail on 16x256 tokens (fp32 activations, uint4 bf16-affine weights), 4
+def bench_qwen_tail(args, tokens: int = 16 * 256) -> dict:
+    """Qwen3 layer tail on `tokens` tokens (fp32 activations, uint4 bf16-affine weights), 4
     independent layers: o_proj, residual, post-attention RMSNorm, gate/up + SiLU, down, residual."""
-    layers, tokens, hidden, width, inter = 4, 16 * 256, 1024, 2048, 3072
+    layers, hidden, width, inter = 4, 1024, 2048, 3072
+    wname = "qwen_tail_16x256" if tokens == 16 * 256 else f"qwen_tail_1x{tokens}"
     flop = workloads.tail_flop(tokens, hidden, width, inter)
-    log(f"workload qwen_tail_16x256: T={tokens} hidden={hidden} attn={width} inter={inter}")
+    log(f"workload {wname}: T={tokens} hidden={hidden} attn={width} inter={inter}")
     with HipRuntime() as rt:
         host = [workloads.qwen_tail_16x256(layer) for layer in range(layers)]
+        for d in host:  # the first `tokens` rows
+            d["x"], d["attended"] = d["x"][:tokens].copy(), d["attended"][:tokens].copy()
         sets = []
         for d in host:
             s = {"x": rt.upload(d["x"]), "att": rt.upload(d["attended"]),
@@ -460,13 +464,19 @@ def bench_qwen_tail(args) -> dict:
         out0 = rt.read(sets[0]["out"], (tokens, hidden))
     step_s = t["step"]
     ks = t["kernel_s"]
-    # the four projections all run the linear4 kernel (route linear4_16x32_k64 at 4096 rows)
-    gemm_s = 4 * ks["linear4_16x32_k64"]
+    # the four projections run the linear4 kernel: route linear4_16x32_k64 at 4096 rows; at the
+    # measured Qwen3 heights linear4_32x32_k64 for o / down and the fused gated4 route
+    if "linear4_16x32_k64" in ks:
+        gemm_s = 4 * ks["linear4_16x32_k64"]
+        kernel = "linear4_16x32_k64"
+    else:
+        gemm_s = 2 * ks["linear4_32x32_k64"] + 2 * ks["gated4_16x32_k64"]
+        kernel = "linear4_32x32_k64 + gated4_16x32_k64"
     tflops = flop / gemm_s / 1e12
     gemm_bytes = tokens * (width + hidden + hidden + 2 * inter + inter) * 4 + (
         (hidden * width + 2 * inter * hidden + hidden * inter) // 2)
     result = {
-        "metric": "Qwen3 layer tail (o_proj, RMSNorm, gated MLP) tokens/s, 16x256, 1 GPU",
+        "metric": f"Qwen3 layer tail (o_proj, RMSNorm, gated MLP) tokens/s, {wname[10:]}, 1 GPU",
         "value": tokens * layers / step_s,
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -478,7 +488,7 @@ def bench_qwen_tail(args) -> dict:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "qwen_tail_16x256: o_proj -> residual -> RMSNorm -> gate/up+SiLU "
+        "config": {"workload": f"{wname}: o_proj -> residual -> RMSNorm -> gate/up+SiLU "
                                "-> down -> residual", "tokens": tokens, "hidden": hidden,
                    "attention_width": width, "intermediate": inter, "layers": layers},
         "tflops": flop * layers / step_s / 1e12,
@@ -492,13 +502,13 @@ def bench_qwen_tail(args) -> dict:
             "traffic": None,
             "algorithmic_flop": flop,
             "algorithmic_bytes": gemm_bytes,
-            "kernel": "linear4_16x32_k64",
+            "kernel": kernel,
         },
     }
     if not args.no_cpu_baseline:
         from oracle import qwen_block
 
-        sample = 512
+        sample = min(512, tokens)
         d = host[0]
 
         def layer():
@@ -726,7 +736,8 @@ def main() -> int:
     parser.add_argument("--layers", type=int, default=LAYERS, help="headline workload only")
     parser.add_argument("--workload", default="qwen3_32x512",
                         choices=["qwen3_32x512", "qwen3_8x512", "bge_32x512", "qwen_qkv4_16x256",
-                                 "qwen_tail_16x256", "bge_layer_32x512", "bge_plan_1x128"])
+                                 "qwen_tail_16x256", "qwen_tail_1x128", "bge_layer_32x512",
+                                 "bge_plan_1x128"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="also launch one copy of this many MiB (traffic-counter calibration)")
@@ -751,6 +762,8 @@ def main() -> int:
         result = bench_bge(args)
     elif args.workload == "qwen_tail_16x256":
         result = bench_qwen_tail(args)
+    elif args.workload == "qwen_tail_1x128":
+        result = bench_qwen_tail(args, tokens=128)
     elif args.workload == "bge_layer_32x512":
         result = bench_bge_layer(args)
     elif args.workload == "bge_plan_1x128":
