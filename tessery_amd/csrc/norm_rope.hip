@@ -13,20 +13,42 @@
 
 namespace tessery {
 
-// One wavefront per row, 4 rows per 256-thread workgroup. out may alias x.
+// One wavefront per row, 4 rows per 256-thread workgroup. out may alias x. With VEC (cols a
+// multiple of 4, x and out 16-byte aligned) rows are read and written as float4.
+template <bool VEC>
 __global__ __launch_bounds__(256) void rms_norm_f32(const float* x, const uint16_t* __restrict__ w,
                                                     float* out, int rows, int cols, float eps) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;  // row-uniform: the whole wavefront leaves together
   const float* xr = x + static_cast<size_t>(row) * cols;
+  float* yr = out + static_cast<size_t>(row) * cols;
   float squares = 0.0f;
+  if (VEC) {
+    const int c4n = cols >> 2;
+    const floatx4* x4 = reinterpret_cast<const floatx4*>(xr);
+#pragma unroll 4
+    for (int c = lane; c < c4n; c += 64) {
+      const floatx4 v = x4[c];
+      squares += (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(squares) / static_cast<float>(cols) + eps);
+    floatx4* y4 = reinterpret_cast<floatx4*>(yr);
+#pragma unroll 4
+    for (int c = lane; c < c4n; c += 64) {
+      const floatx4 v = x4[c];
+      floatx4 r;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r[j] = v[j] * inv * bf16_to_float(w[4 * c + j]);
+      y4[c] = r;
+    }
+    return;
+  }
   for (int c = lane; c < cols; c += 64) {
     const float val = xr[c];
     squares += val * val;
   }
   const float inv = 1.0f / sqrtf(wave_sum(squares) / static_cast<float>(cols) + eps);
-  float* yr = out + static_cast<size_t>(row) * cols;
   for (int c = lane; c < cols; c += 64) yr[c] = xr[c] * inv * bf16_to_float(w[c]);
 }
 
@@ -129,7 +151,12 @@ __global__ __launch_bounds__(256) void norm_rope_f16(const _Float16* __restrict_
 hipError_t launch_rms_norm_f32(const float* x, const uint16_t* w, float* out, int rows, int cols,
                                float eps, hipStream_t st) {
   if (rows <= 0) return hipSuccess;
-  rms_norm_f32<<<(rows + 3) / 4, 256, 0, st>>>(x, w, out, rows, cols, eps);
+  const bool vec = (cols & 3) == 0 &&
+                   ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+  if (vec)
+    rms_norm_f32<true><<<(rows + 3) / 4, 256, 0, st>>>(x, w, out, rows, cols, eps);
+  else
+    rms_norm_f32<false><<<(rows + 3) / 4, 256, 0, st>>>(x, w, out, rows, cols, eps);
   return hipGetLastError();
 }
 

@@ -39,7 +39,19 @@ def test_rms_norm_in_place(runtime):
     np.testing.assert_allclose(got, ref.rms_norm(x, bf16_values(w), 1e-6), atol=1e-6)
 
 
-@pytest.mark.parametrize("shape,theta", [((2, 3, 4, 64), 10000.0), ((2, 512, 2, 128), 1e6)])
+@pytest.mark.parametrize("rows,cols", [(9, 1030), (5, 66), (130, 1024), (3, 4)])
+def test_rms_norm_widths(runtime, rows, cols):
+    """Row widths that take the scalar path (cols % 4 != 0) and the float4 path (hidden 1024)."""
+    rng = np.random.default_rng(cols)
+    x = rng.normal(size=(rows, cols)).astype(np.float32)
+    w = bf16_words(rng.uniform(0.5, 1.5, cols))
+    got = run(runtime, "rms_norm", [x, w], x.shape, threads=rows * 32, group_size=32, cols=cols,
+              eps=1e-6)
+    np.testing.assert_allclose(got, ref.rms_norm(x, bf16_values(w), 1e-6), atol=1e-6,
+                               rtol=1e-6)
+
+
+@pytest.mark.parametrize("shape,theta",[((2, 3, 4, 64), 10000.0), ((2, 512, 2, 128), 1e6)])
 def test_rope(runtime, shape, theta):
     rng = np.random.default_rng(8)
     x = rng.normal(size=shape).astype(np.float32)
