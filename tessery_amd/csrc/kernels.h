@@ -103,6 +103,23 @@ hipError_t launch_qkv4_f16(const Qkv4Args& a, hipStream_t st);
 // tessery add (kernels.metal:300-304): out[i] = a[i] + b[i], i < n. out may alias a or b.
 hipError_t launch_add_f32(const float* a, const float* b, float* out, uint32_t n, hipStream_t st);
 
+// tessery embedding4 (kernels.metal:21-30): out[t][c] = weight4(table, ids[t], c) for the
+// n = tokens * cols outputs; cols % 64 == 0, out 16-byte aligned. ids >= vocab give zero rows.
+hipError_t launch_embedding4_f32(const uint32_t* ids, const uint32_t* w, const uint16_t* s,
+                                 const uint16_t* b, float* out, uint64_t n, uint32_t cols,
+                                 uint32_t vocab, hipStream_t st);
+// tessery embedding_position (kernels.metal:351-360):
+// out[t][c] = (words[ids[t]][c] + types[c]) + positions[t % seq][c]. ids >= vocab give zeros.
+hipError_t launch_embedding_position_f32(const uint32_t* ids, const float* words,
+                                         const float* positions, const float* types, float* out,
+                                         uint64_t n, uint32_t cols, uint32_t seq, uint32_t vocab,
+                                         hipStream_t st);
+// tessery pool_project (kernels.metal:339-349): out[b][0:dim] = x[b, pos] / |x[b, pos][0:dim]|,
+// pos = 0 with first, else lengths[b] - 1.
+hipError_t launch_pool_project_f32(const float* x, const uint32_t* lengths, float* out,
+                                   uint32_t batch, uint32_t seq, uint32_t cols, uint32_t dim,
+                                   bool first, hipStream_t st);
+
 // Plain device copy (bytes % 16 == 0), used to calibrate HBM traffic counters.
 hipError_t launch_copy(const void* src, void* dst, uint64_t bytes, hipStream_t st);
 

@@ -60,6 +60,9 @@ enum Route : int {
   R_GELU,
   R_LAYER_NORM,
   R_ADD,
+  R_EMBEDDING4,
+  R_EMBEDDING_POSITION,
+  R_POOL_PROJECT,
   R_COPY,
   R_NONE
 };
@@ -100,6 +103,9 @@ const RouteName kRoutes[] = {
     {"gelu_f32", R_GELU, 1},
     {"layer_norm", R_LAYER_NORM, 4},
     {"add", R_ADD, 3},
+    {"embedding4", R_EMBEDDING4, 5},
+    {"embedding_position", R_EMBEDDING_POSITION, 5},
+    {"pool_project", R_POOL_PROJECT, 3},
     {"copy", R_COPY, 2},
 };
 
@@ -454,6 +460,32 @@ bool validate(Route r, const Params& p, uint64_t threads, uint32_t group, const 
       const uint64_t n = p.n;
       return n && sz[0] >= n * 4 && sz[1] >= n * 4 && sz[2] >= n * 4;
     }
+    case R_EMBEDDING4: {  // kernels.metal:21-30: ids, w, scales, biases, out; n = tokens*cols
+      const uint64_t n = p.n, cols = p.cols;
+      if (!n || !cols || cols % 64 || cols > 65536 || n % cols || n / cols > kMaxTokens * 16)
+        return false;
+      const uint64_t vocab = sz[1] / (cols / 2);
+      return vocab && vocab <= 0xffffffffull && sz[0] >= n / cols * 4 &&
+             sz[2] >= vocab * (cols / 64) * 2 && sz[3] >= vocab * (cols / 64) * 2 &&
+             sz[4] >= n * 4;
+    }
+    case R_EMBEDDING_POSITION: {  // kernels.metal:351-360: ids, words, positions, types, out
+      const uint64_t n = p.n, cols = p.cols, seq = p.seq;
+      if (!n || !cols || cols > 65536 || n % cols || !seq || n / cols > kMaxTokens * 16)
+        return false;
+      const uint64_t vocab = sz[1] / (cols * 4);
+      return vocab && vocab <= 0xffffffffull && sz[0] >= n / cols * 4 &&
+             sz[2] >= seq * cols * 4 && sz[3] >= cols * 4 && sz[4] >= n * 4;
+    }
+    case R_POOL_PROJECT: {  // kernels.metal:339-349: x, lengths, out; batch*32 threads
+      const uint64_t cols = p.cols, seq = p.seq, dim = p.dim;
+      if (group != 32 || !threads || threads % 32 || !cols || !seq || !dim || dim > cols)
+        return false;
+      const uint64_t batch = threads / 32;
+      if (batch > kMaxTokens) return false;
+      return sz[0] >= batch * seq * cols * 4 && (p.u1 || sz[1] >= batch * 4) &&
+             sz[2] >= batch * dim * 4;
+    }
     case R_COPY:
       return threads % 16 == 0 && sz[0] >= threads && sz[1] >= threads;
     default:
@@ -680,6 +712,23 @@ hipError_t launch(Runtime* rt, const Op& op) {
       return tessery::launch_add_f32(static_cast<const float*>(op.ptr[0]),
                                      static_cast<const float*>(op.ptr[1]),
                                      static_cast<float*>(op.ptr[2]), p.n, st);
+    case R_EMBEDDING4:
+      return tessery::launch_embedding4_f32(
+          static_cast<const uint32_t*>(op.ptr[0]), static_cast<const uint32_t*>(op.ptr[1]),
+          static_cast<const uint16_t*>(op.ptr[2]), static_cast<const uint16_t*>(op.ptr[3]),
+          static_cast<float*>(op.ptr[4]), p.n, p.cols,
+          static_cast<uint32_t>(op.size[1] / (p.cols / 2)), st);
+    case R_EMBEDDING_POSITION:
+      return tessery::launch_embedding_position_f32(
+          static_cast<const uint32_t*>(op.ptr[0]), static_cast<const float*>(op.ptr[1]),
+          static_cast<const float*>(op.ptr[2]), static_cast<const float*>(op.ptr[3]),
+          static_cast<float*>(op.ptr[4]), p.n, p.cols, p.seq,
+          static_cast<uint32_t>(op.size[1] / (static_cast<uint64_t>(p.cols) * 4)), st);
+    case R_POOL_PROJECT:
+      return tessery::launch_pool_project_f32(
+          static_cast<const float*>(op.ptr[0]), static_cast<const uint32_t*>(op.ptr[1]),
+          static_cast<float*>(op.ptr[2]), static_cast<uint32_t>(op.threads / 32), p.seq, p.cols,
+          p.dim, p.u1 != 0, st);
     case R_COPY:
       return tessery::launch_copy(op.ptr[0], op.ptr[1], op.threads, st);
     default:

@@ -241,3 +241,128 @@ def attention_bytes(
     kv = 2 * valid * shape.kv_heads * shape.dim * in_bytes
     o = shape.batch * shape.seq * shape.heads * shape.dim * out_bytes
     return q + kv + o + 4 * shape.batch
+
+
+# ---- synthetic weight packs (model.safetensors + config.json of the real model shapes) --------
+
+QWEN3_0P6B = {"hidden": 1024, "intermediate": 3072, "layers": 28, "heads": 16, "kv_heads": 8,
+              "head_dim": 128, "vocab": 151669}
+BGE_SMALL = {"hidden": 384, "intermediate": 1536, "layers": 12, "heads": 12, "vocab": 30522,
+             "positions": 512, "types": 2}
+
+
+def qwen3_pack_tensors(seed: int, *, hidden: int, intermediate: int, layers: int, heads: int,
+                       kv_heads: int, head_dim: int, vocab: int
+                       ) -> tuple[dict[str, Any], dict[str, tuple[str, NDArray]]]:
+    """A Qwen3 config and its uint4 tensors (names and shapes of qwen3.py:65-92). Projection
+    scales 0.2/sqrt(inputs) keep the residual stream O(1) over many layers; embedding scale 0.2;
+    RMSNorm weights U(0.5, 1.5)."""
+    rng = np.random.default_rng(seed)
+    tensors: dict[str, tuple[str, NDArray]] = {}
+
+    def norm(prefix: str, dims: int) -> None:
+        tensors[prefix + ".weight"] = ("BF16", bf16_words(rng.uniform(0.5, 1.5, dims)))
+
+    def quant(prefix: str, outputs: int, inputs: int, scale: float) -> None:
+        packed, s, b = weight4_set(rng, outputs, inputs, scale)
+        tensors[prefix + ".weight"] = ("U32", packed)
+        tensors[prefix + ".scales"] = ("BF16", s)
+        tensors[prefix + ".biases"] = ("BF16", b)
+
+    qw, kvw = heads * head_dim, kv_heads * head_dim
+    quant("model.embed_tokens", vocab, hidden, 0.2)
+    norm("model.norm", hidden)
+    for layer in range(layers):
+        p = f"model.layers.{layer}"
+        norm(p + ".input_layernorm", hidden)
+        norm(p + ".post_attention_layernorm", hidden)
+        for name, outputs in (("q", qw), ("k", kvw), ("v", kvw)):
+            quant(p + f".self_attn.{name}_proj", outputs, hidden, 0.2 / math.sqrt(hidden))
+        quant(p + ".self_attn.o_proj", hidden, qw, 0.2 / math.sqrt(qw))
+        norm(p + ".self_attn.q_norm", head_dim)
+        norm(p + ".self_attn.k_norm", head_dim)
+        quant(p + ".mlp.gate_proj", intermediate, hidden, 0.2 / math.sqrt(hidden))
+        quant(p + ".mlp.up_proj", intermediate, hidden, 0.2 / math.sqrt(hidden))
+        quant(p + ".mlp.down_proj", hidden, intermediate, 0.2 / math.sqrt(intermediate))
+    config = {
+        "model_type": "qwen3", "architectures": ["Qwen3ForCausalLM"], "hidden_size": hidden,
+        "intermediate_size": intermediate, "num_hidden_layers": layers,
+        "num_attention_heads": heads, "num_key_value_heads": kv_heads, "head_dim": head_dim,
+        "vocab_size": vocab, "hidden_act": "silu", "attention_bias": False, "rope_scaling": None,
+        "use_sliding_window": False, "quantization": {"bits": 4, "group_size": 64},
+        "rms_norm_eps": EPS, "rope_theta": THETA, "max_position_embeddings": 32768,
+        "tie_word_embeddings": True,
+    }
+    return config, tensors
+
+
+def bert_pack_tensors(seed: int, *, hidden: int, intermediate: int, layers: int, heads: int,
+                      vocab: int, positions: int, types: int, extras: bool = True
+                      ) -> tuple[dict[str, Any], dict[str, tuple[str, NDArray]]]:
+    """A BERT config and its fp32 tensors (names and shapes of bert.py:50-84), with the optional
+    pooler and position_ids tensors when extras."""
+    rng = np.random.default_rng(seed)
+    tensors: dict[str, tuple[str, NDArray]] = {}
+
+    def f32(shape: tuple[int, ...], std: float) -> tuple[str, NDArray]:
+        return ("F32", (rng.standard_normal(shape) * std).astype(np.float32))
+
+    def norm(prefix: str) -> None:
+        tensors[prefix + ".weight"] = ("F32", rng.uniform(0.5, 1.5, hidden).astype(np.float32))
+        tensors[prefix + ".bias"] = f32((hidden,), 0.1)
+
+    def linear(prefix: str, outputs: int, inputs: int) -> None:
+        tensors[prefix + ".weight"] = f32((outputs, inputs), 1.0 / math.sqrt(inputs))
+        tensors[prefix + ".bias"] = f32((outputs,), 0.1)
+
+    for name, rows in (("word", vocab), ("position", positions), ("token_type", types)):
+        tensors[f"embeddings.{name}_embeddings.weight"] = f32((rows, hidden), 0.5)
+    norm("embeddings.LayerNorm")
+    for layer in range(layers):
+        p = f"encoder.layer.{layer}"
+        for name in ("query", "key", "value"):
+            linear(p + ".attention.self." + name, hidden, hidden)
+        linear(p + ".attention.output.dense", hidden, hidden)
+        norm(p + ".attention.output.LayerNorm")
+        linear(p + ".intermediate.dense", intermediate, hidden)
+        linear(p + ".output.dense", hidden, intermediate)
+        norm(p + ".output.LayerNorm")
+    if extras:
+        linear("pooler.dense", hidden, hidden)
+        tensors["embeddings.position_ids"] = ("I64", np.arange(positions, dtype=np.int64)[None])
+    config = {
+        "model_type": "bert", "architectures": ["BertModel"], "hidden_size": hidden,
+        "intermediate_size": intermediate, "num_hidden_layers": layers,
+        "num_attention_heads": heads, "vocab_size": vocab, "max_position_embeddings": positions,
+        "type_vocab_size": types, "hidden_act": "gelu", "layer_norm_eps": 1e-12,
+        "position_embedding_type": "absolute",
+    }
+    return config, tensors
+
+
+def write_pack(directory: str, config: dict[str, Any], tensors: dict[str, tuple[str, NDArray]],
+               *, architecture: str, max_length: int, min_dimensions: int | None = None):
+    """Write config.json and model.safetensors into directory; returns the ModelProfile that pins
+    both files (sizes and sha256)."""
+    import json
+    import os
+
+    from .backends import ModelProfile
+    from .weights import artifact_of, encode_safetensors
+
+    config_bytes = json.dumps(config).encode()
+    model_bytes = encode_safetensors(tensors)
+    for name, data in (("config.json", config_bytes), ("model.safetensors", model_bytes)):
+        with open(os.path.join(directory, name), "wb") as f:
+            f.write(data)
+    hidden = int(config["hidden_size"])
+    return ModelProfile(
+        architecture=architecture, native_dimensions=hidden,
+        min_dimensions=hidden if min_dimensions is None else min_dimensions,
+        max_length=max_length,
+        artifacts=(artifact_of("config.json", "config.json", config_bytes),
+                   artifact_of("model.safetensors", "model.safetensors", model_bytes)))
+
+
+def weights_of(tensors: dict[str, tuple[str, NDArray]]) -> dict[str, NDArray]:
+    return {name: array for name, (_, array) in tensors.items()}
