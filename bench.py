@@ -727,6 +727,136 @@ def bench_bge_plan(args) -> dict:
     }
 
 
+def bench_model(args, arch: str) -> dict:
+    """A whole embedding forward through the model backends: a synthetic weight pack of the real
+    model shapes written to disk (config.json + model.safetensors, pinned by sha256), loaded by
+    Qwen3Backend / BertBackend, and forward(ids, lengths) timed end to end (ids upload, every
+    layer, pooling, result read; plan replayed as a HIP graph after the first call)."""
+    import tempfile
+
+    from tessery_amd.backends import BertBackend, Qwen3Backend
+
+    batch, seq = 8, 512
+    rng = np.random.default_rng(3)
+    if arch == "qwen3":
+        shape = workloads.QWEN3_0P6B
+        config, tensors = workloads.qwen3_pack_tensors(21, **shape)
+        lengths = workloads.lengths_uniform(3, batch, 64, seq)
+        architecture, backend_cls, dims = "qwen3_uint4", Qwen3Backend, shape["hidden"]
+        wname = "qwen3_model_8x512"
+        what = "Qwen3-0.6B shapes (28 layers, hidden 1024, 16q/8kv x 128, MLP 3072, vocab 151669)"
+    else:
+        shape = workloads.BGE_SMALL
+        config, tensors = workloads.bert_pack_tensors(22, **shape)
+        lengths = workloads.lengths_uniform(2, batch, 2, seq)
+        architecture, backend_cls, dims = "bert_f32", BertBackend, shape["hidden"]
+        wname = "bge_model_8x512"
+        what = "BGE-small shapes (12 layers, hidden 384, 12 heads x 32, MLP 1536, vocab 30522)"
+    ids = rng.integers(0, shape["vocab"], (batch, seq)).astype(np.uint32)
+    log(f"workload {wname}: {what}, lengths uniform, {int(lengths.sum())} valid tokens")
+    with tempfile.TemporaryDirectory(dir="/tmp") as pack_dir:
+        t0 = time.perf_counter()
+        profile = workloads.write_pack(pack_dir, config, tensors, architecture=architecture,
+                                       max_length=seq,
+                                       min_dimensions=64 if arch == "qwen3" else dims)
+        pack_bytes = profile.artifact("model.safetensors").size
+        log(f"pack written: {pack_bytes / 2**20:.1f} MiB in {time.perf_counter() - t0:.1f} s")
+        t0 = time.perf_counter()
+        backend = backend_cls(pack_dir, profile, workspace_limit_bytes=1 << 30)
+        load_s = time.perf_counter() - t0
+        log(f"pack verified and uploaded in {load_s:.2f} s")
+    try:
+        rt = backend.runtime
+        for _ in range(max(2, args.warmup)):
+            out = backend.forward(ids, lengths, dimensions=dims)
+        start = time.perf_counter()
+        for _ in range(args.steps):
+            out = backend.forward(ids, lengths, dimensions=dims)
+        per = (time.perf_counter() - start) / args.steps
+        log(f"timed {args.steps} forwards: {per * 1e3:.3f} ms each")
+        diag = rt.diagnostics()
+        rt._clear_plans()  # re-record once with events around every launch
+        with rt.profile_kernels() as records:
+            backend.forward(ids, lengths, dimensions=dims)
+    finally:
+        backend.close()
+    kernel_s: dict[str, float] = {}
+    proj_flop, proj_s = 0, 0.0
+    for r in records:
+        kernel_s[r["kernel"]] = kernel_s.get(r["kernel"], 0.0) + r["gpu_seconds"]
+        # at 4096 rows every projection is a single launch over all rows
+        if r["kernel"].startswith(("linear4", "gated4", "matmul")):
+            mult = 2 if r["kernel"].startswith("gated4") else 1
+            proj_flop += mult * 2 * r["rows"] * r["cols"] * r["k"]
+            proj_s += r["gpu_seconds"]
+    tokens = batch * seq
+    proj_tflops = proj_flop / proj_s / 1e12
+    result = {
+        "metric": f"{'Qwen3-0.6B' if arch == 'qwen3' else 'BGE-small'} embedding forward "
+                  f"tokens/s (padded), {batch}x{seq}, 1 GPU",
+        "value": tokens / per,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": max(2, args.warmup),
+        "ms_per_step": per * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"{wname}: {what}, forward(ids, lengths) -> unit vectors",
+                   "batch": batch, "seq": seq, "valid_tokens": int(lengths.sum()),
+                   "dimensions": dims},
+        "sequences_per_s": batch / per,
+        "pack_mib": pack_bytes / 2**20,
+        "load_s": load_s,
+        "graph_builds": diag["graph_builds"],
+        "graph_launches": diag["graph_launches"],
+        "kernel_ms_per_forward": {k: v * 1e3 for k, v in sorted(kernel_s.items())},
+        "roofline": {
+            "bound": "mfma",
+            "achieved": proj_tflops,
+            "peak": PEAK_F32_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": proj_tflops / PEAK_F32_TFLOPS,
+            "traffic": None,
+            "algorithmic_flop": proj_flop,
+            "kernel": "all projection launches of one forward (summed FLOP / summed duration)",
+        },
+    }
+    if not args.no_cpu_baseline:
+        from oracle import models as oracle_models
+
+        w = workloads.weights_of(tensors)
+        sample = int(lengths[0])
+        ids0, len0 = ids[:1, :sample], lengths[:1].copy()
+
+        def forward_cpu():
+            if arch == "qwen3":
+                return oracle_models.qwen3_forward(
+                    w, ids0, len0, layers=shape["layers"], heads=shape["heads"],
+                    kv_heads=shape["kv_heads"], head_dim=shape["head_dim"],
+                    eps=config["rms_norm_eps"], theta=config["rope_theta"], dimensions=dims)
+            return oracle_models.bert_forward(w, ids0, len0, layers=shape["layers"],
+                                              heads=shape["heads"], eps=config["layer_norm_eps"])
+
+        expected, per_sample, runs = time_cpu(forward_cpu, budget_s=20.0)
+        result["cpu_baseline"] = {
+            "value": sample / per_sample,
+            "unit": "tokens/s",
+            "cores": len(os.sched_getaffinity(0)),
+            "blas_threads": blas_threads(),
+            "kind": "port",
+            "sample": f"sequence 0 ({sample} tokens, all layers), float64 NumPy oracle, median of "
+                      f"{runs}; {per_sample * 1e3:.0f} ms",
+        }
+        result["max_abs_err_seq0"] = float(np.abs(out[0] - expected[0]).max())
+    else:
+        result["cpu_baseline"] = None
+    return result
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__,
                                      formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -737,7 +867,7 @@ def main() -> int:
     parser.add_argument("--workload", default="qwen3_32x512",
                         choices=["qwen3_32x512", "qwen3_8x512", "bge_32x512", "qwen_qkv4_16x256",
                                  "qwen_tail_16x256", "qwen_tail_1x128", "bge_layer_32x512",
-                                 "bge_plan_1x128"])
+                                 "bge_plan_1x128", "qwen3_model_8x512", "bge_model_8x512"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="also launch one copy of this many MiB (traffic-counter calibration)")
@@ -768,6 +898,10 @@ def main() -> int:
         result = bench_bge_layer(args)
     elif args.workload == "bge_plan_1x128":
         result = bench_bge_plan(args)
+    elif args.workload == "qwen3_model_8x512":
+        result = bench_model(args, "qwen3")
+    elif args.workload == "bge_model_8x512":
+        result = bench_model(args, "bge")
     else:
         result = bench_qkv4_block(args)
     print(json.dumps(result), flush=True)

@@ -213,8 +213,12 @@ __global__ __launch_bounds__(256) void layer_norm_f32(float* x, const float* r,
 int dense_splits(int rows, int cols, int k, size_t scratch_floats) {
   const int tiles = ((rows + kDenseRows - 1) / kDenseRows) * ((cols + 127) / 128);
   const int chunks = (k + 63) / 64;
-  if (tiles >= 128 || chunks < 4) return 1;
-  int splits = std::min(chunks, (256 + tiles - 1) / tiles);
+  // Under one tile per CU (256 CUs) the CUs that hold a tile run it with one wavefront per SIMD,
+  // too few to cover the MFMA chains' latency: split K so every CU holds several workgroups
+  // (about 256 in all below 128 tiles, about 768 from 128 to 255 tiles, e.g. 4096 x 384 outputs).
+  if (tiles >= 256 || chunks < 4) return 1;
+  const int target = tiles < 128 ? 256 : 768;
+  int splits = std::min(chunks, (target + tiles - 1) / tiles);
   const int per = (chunks + splits - 1) / splits;
   splits = (chunks + per - 1) / per;  // no empty split
   if (static_cast<size_t>(splits) * rows * cols > scratch_floats) return 1;
