@@ -60,6 +60,13 @@ hipError_t launch_gated4_f32(const float* x, const uint32_t* w, const uint16_t* 
                              const uint16_t* biases, const uint32_t* uw, const uint16_t* uscales,
                              const uint16_t* ubiases, float* out, int row0, int row1, int cols,
                              int k, float* scratch, size_t scratch_floats, hipStream_t st);
+// The same projection for M >= kLinear4HiloRows rows on fp16 MFMA: rows scaled by powers of two
+// and split into hi + lo fp16 halves (about 22 bits), exact codes, fp32 sums. scratch holds the M
+// row scales. x and y start at row 0 of the range; N % 128 == 0, K % 64 == 0.
+constexpr int kLinear4HiloRows = 2048;
+hipError_t launch_linear4_hilo_f32(const float* x, const uint32_t* w, const uint16_t* scales,
+                                   const uint16_t* biases, float* y, int M, int N, int K,
+                                   float* scratch, size_t scratch_floats, hipStream_t st);
 // gate[i] = silu(gate[i]) * up[i] for i < n (tessery silu_gate, kernels.metal:334-337).
 hipError_t launch_silu_gate_f32(float* gate, const float* up, uint32_t n, hipStream_t st);
 

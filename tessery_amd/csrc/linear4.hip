@@ -196,6 +196,15 @@ hipError_t launch_l4(const float* x, const uint32_t* w, const uint16_t* scales,
   if (row1 <= row0 || cols <= 0) return hipSuccess;
   if (k % 64) return hipErrorInvalidValue;
   const int rows = row1 - row0;
+  if constexpr (!GATED) {
+    // large batches: fp16 MFMA on row-scaled hi + lo activations (fp32-grade, several times the
+    // fp32 MFMA rate)
+    if (rows >= kLinear4HiloRows && cols % 128 == 0 && scratch &&
+        static_cast<size_t>(rows) <= scratch_floats)
+      return launch_linear4_hilo_f32(x + static_cast<size_t>(row0) * k, w, scales, biases,
+                                     out + static_cast<size_t>(row0) * cols, rows, cols, k,
+                                     scratch, scratch_floats, st);
+  }
   const int splits = scratch ? linear4_splits(rows, cols, k, scratch_floats) : 1;
   if (splits > 1) {
     const int per = (k / 64 + splits - 1) / splits;

@@ -221,7 +221,215 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
     }
 }
 
+
+// ---- uint4 projection of fp32 activations on fp16 MFMA (large batches) ----------------------
+//
+// Each row m of x is scaled by an exact power of two 2^e_m so that its largest magnitude lies in
+// [2^13, 2^14), then split into two fp16 values: hi = fp16(xs), lo = fp16(xs - hi). hi + lo
+// carries xs to about 22 significant bits; what lo drops is below 2^-25 in absolute terms, far
+// under fp32 rounding on the row's largest value. The codes are exact in fp16, so
+//     y[m][n] = 2^-e_m * sum_g (scale[n][g] * A_g[m][n] + bias[n][g] * X_g[m])
+//     A_g[m][n] = sum_{k in g} (hi[m][k] + lo[m][k]) * code[n][k]   (fp16 MFMA, fp32 sums)
+//     X_g[m]    = sum_{k in g} xs[m][k]                              (fp32, while staging x)
+// gives fp32-grade results at the fp16 MFMA rate (two MFMAs per product, one per half).
+
+// One wavefront per row: rs[m] = 2^e_m (1 for all-zero or non-finite rows).
+__global__ __launch_bounds__(256) void row_scales_f32(const float* __restrict__ x, int M, int K,
+                                                      float* __restrict__ rs) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const floatx4* xr = reinterpret_cast<const floatx4*>(x + static_cast<size_t>(row) * K);
+  float mx = 0.0f;
+  for (int c = lane; c < K / 4; c += 64) {
+    const floatx4 v = xr[c];
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+  }
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  float scale = 1.0f;
+  if (mx > 0.0f && mx <= 3.402823466e38f) {
+    int ex;
+    frexpf(mx, &ex);  // mx = f * 2^ex, f in [0.5, 1): mx * 2^(14 - ex) in [2^13, 2^14)
+    scale = ldexpf(1.0f, min(max(14 - ex, -126), 126));
+  }
+  if (lane == 0) rs[row] = scale;
+}
+
+// 128 x 128 output tile per workgroup, 4 wavefronts in a 2 x 2 grid of 64 x 64 (2 x 2 MFMA
+// tiles of 32 x 32, v_mfma_f32_32x32x16_f16), the A / B k-mapping of qkv4_f16. Two LDS stages of
+// the hi and lo planes (swizzled as in qkv4_f16) and of X_g; group g + 1's x (fp32, 8 float4 per
+// thread), weight words, scales and biases are loaded into registers while group g runs.
+__global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__ x,
+                                                      const float* __restrict__ rs,
+                                                      const uint32_t* __restrict__ w,
+                                                      const uint16_t* __restrict__ sc,
+                                                      const uint16_t* __restrict__ bi,
+                                                      float* __restrict__ y, int M, int N, int K) {
+  __shared__ __attribute__((aligned(1024))) _Float16 xs[2][2][128 * 64];  // [stage][hi, lo]
+  __shared__ __attribute__((aligned(16))) float xsum[2][128];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int groups = K / 64;
+  const int m0 = blockIdx.x * 128;
+  const int nw = blockIdx.y * 128 + wn * 64;
+
+  // staging role: row srow of the tile, floats 32 * skh .. +31 of each group
+  const int srow = tid >> 1, skh = tid & 1;
+  const int grow = min(m0 + srow, M - 1);  // rows past M repeat row M - 1, never stored
+  const float* xsrc = x + static_cast<size_t>(grow) * K + 32 * skh;
+  const float rscale = rs[grow];
+  floatx4 xr[8];
+  auto load_x = [&](int g) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xr[j] = *reinterpret_cast<const floatx4*>(xsrc + 64 * g + 4 * j);
+  };
+  // MFMA role: the lane's two columns nw + 32 j + l32, words 4 hh .. 4 hh + 3 of each group
+  const uint32_t* wp[2];
+  const uint16_t* sp[2];
+  const uint16_t* bp[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const size_t n = static_cast<size_t>(nw + 32 * j + l32);
+    wp[j] = w + n * (K / 8) + 4 * hh;
+    sp[j] = sc + n * groups;
+    bp[j] = bi + n * groups;
+  }
+  uint4v wd[2], wdn[2];
+  uint16_t sv[2], bv[2], svn[2], bvn[2];
+  auto load_w = [&](int g, uint4v* wo, uint16_t* so, uint16_t* bo) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      wo[j] = *reinterpret_cast<const uint4v*>(wp[j] + 8 * g);
+      so[j] = sp[j][g];
+      bo[j] = bp[j][g];
+    }
+  };
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  load_x(0);
+  load_w(0, wd, sv, bv);
+  for (int g = 0; g < groups; ++g) {
+    const int stage = g & 1;
+    // ---- scale, split and stage group g's x; its row sum X_g ----
+    {
+      float sum = 0.0f;
+      half8 hv[4], lv[4];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float v = xr[j][t] * rscale;
+          const _Float16 h = static_cast<_Float16>(v);
+          sum += v;
+          hv[j >> 1][4 * (j & 1) + t] = h;
+          lv[j >> 1][4 * (j & 1) + t] = static_cast<_Float16>(v - static_cast<float>(h));
+        }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int pos = srow * 64 + 8 * ((4 * skh + c) ^ xsw(srow));
+        *reinterpret_cast<half8*>(&xs[stage][0][pos]) = hv[c];
+        *reinterpret_cast<half8*>(&xs[stage][1][pos]) = lv[c];
+      }
+      sum += __shfl_xor(sum, 1);
+      if (!skh) xsum[stage][srow] = sum;
+    }
+    if (g + 1 < groups) {
+      load_x(g + 1);
+      load_w(g + 1, wdn, svn, bvn);
+    }
+    __syncthreads();
+
+    // ---- A_g for the wavefront's 2 x 2 tiles, both halves into one sum ----
+    floatx16 part[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) part[i][j][e] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      half8 bq[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bq[j] = decode_codes(wd[j][s]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int row = wm * 64 + 32 * i + l32;
+        const int off = row * 64 + 8 * ((4 * hh + s) ^ xsw(row));
+        const half8 ah = *reinterpret_cast<const half8*>(&xs[stage][0][off]);
+        const half8 al = *reinterpret_cast<const half8*>(&xs[stage][1][off]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bq[j], part[i][j], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bq[j], part[i][j], 0, 0, 0);
+      }
+    }
+
+    // ---- fold: acc += scale * A_g + bias * X_g ----
+    float gs[2], gb[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      gs[j] = bf16_to_float(sv[j]);
+      gb[j] = bf16_to_float(bv[j]);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      floatx4 xg[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        xg[q] = *reinterpret_cast<const floatx4*>(&xsum[stage][wm * 64 + 32 * i + 8 * q + 4 * hh]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          acc[i][j][e] = fmaf(gs[j], part[i][j][e], fmaf(gb[j], xg[e >> 2][e & 3], acc[i][j][e]));
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      wd[j] = wdn[j];
+      sv[j] = svn[j];
+      bv[j] = bvn[j];
+    }
+  }
+
+  // ---- y = acc / 2^e_m, fp32, row-major ----
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int m = m0 + wm * 64 + 32 * i + 8 * (e >> 2) + 4 * hh + (e & 3);
+      if (m < M) {
+        const float inv = 1.0f / rs[m];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          y[static_cast<size_t>(m) * N + nw + 32 * j + l32] = acc[i][j][e] * inv;
+      }
+    }
+}
+
 }  // namespace
+
+hipError_t launch_linear4_hilo_f32(const float* x, const uint32_t* w, const uint16_t* scales,
+                                   const uint16_t* biases, float* y, int M, int N, int K,
+                                   float* scratch, size_t scratch_floats, hipStream_t st) {
+  if (M <= 0) return hipSuccess;
+  if (K <= 0 || K % 64 || N <= 0 || N % 128 || !scratch ||
+      static_cast<size_t>(M) > scratch_floats || (reinterpret_cast<uintptr_t>(x) & 15))
+    return hipErrorInvalidValue;
+  row_scales_f32<<<(M + 3) / 4, 256, 0, st>>>(x, M, K, scratch);
+  dim3 grid((M + 127) / 128, N / 128);
+  linear4_hilo<<<grid, 256, 0, st>>>(x, scratch, w, scales, biases, y, M, N, K);
+  return hipGetLastError();
+}
 
 hipError_t launch_qkv4_f16(const Qkv4Args& a, hipStream_t st) {
   if (a.M <= 0) return hipSuccess;

@@ -130,3 +130,27 @@ def test_eight_row_offset_preserves_surrounding_rows(runtime):
             b.close()
     assert np.isnan(out[:16]).all() and np.isnan(out[24:]).all()
     np.testing.assert_array_equal(out[16:24], 64)
+
+
+@pytest.mark.parametrize("m,n,k", [(2048, 1024, 1024), (4096, 3072, 1024), (2050, 1024, 3072),
+                                   (2176, 128, 64), (4097, 2048, 1024)])
+def test_large_batch_fp16_mfma_path(runtime, m, n, k):
+    """From 2048 rows the projection runs on fp16 MFMA over row-scaled hi + lo halves of x. Row
+    magnitudes spread over 2^-20 .. 2^20, a zero row, rows near fp32's smallest and largest
+    normal values (beyond fp16's range): every output stays within fp32-grade error of the
+    float64 product, measured against sum_k |x| |w| of the same element."""
+    x, packed, scales, biases = make(907 + m + n, m, n, k)
+    rng = np.random.default_rng(m)
+    x[5:] *= np.exp2(rng.integers(-20, 21, m - 5)).astype(np.float32)[:, None]
+    x[0] = 0.0
+    x[1] *= np.float32(1e-36)
+    x[2] *= np.float32(1e6)
+    x[3] *= np.float32(1e34)
+    got = project(runtime, [x, packed, scales, biases], m, n, k)
+    w = ref.dequantize(packed, scales, biases, k)
+    want = x.astype(np.float64) @ w.T
+    bound = np.abs(x).astype(np.float64) @ np.abs(w).T
+    assert np.isfinite(got).all()
+    err = np.abs(got - want)
+    assert np.all(err <= 2e-6 * bound + 1e-37), float((err / (bound + 1e-300)).max())
+    assert not np.any(got[0])
