@@ -39,6 +39,12 @@ hipError_t launch_rms_norm_f32(const float* x, const uint16_t* w, float* out, in
 // tessery rope (kernels.metal:65-74): in place, split-half pairs, pos = (row / heads) % seq.
 hipError_t launch_rope_f32(float* x, const float* cos_tab, const float* sin_tab, uint32_t n,
                            int heads, int seq, int dim, hipStream_t st);
+// launch_rms_norm_f32 in place (x == out) followed by launch_rope_f32 on the same rows, as one
+// kernel with the same bits; hipErrorNotReady when the shape is not covered (8 | dim <= 256, x
+// 16-byte aligned) and the two launches must run instead.
+hipError_t launch_rms_norm_rope_f32(float* x, const uint16_t* w, const float* cos_tab,
+                                   const float* sin_tab, int rows, int dim, float eps, int heads,
+                                   int seq, hipStream_t st);
 // Fused per-head RMSNorm + RoPE on fp16 rows [B,S,heads,D] -> fp16 rows, rows with
 // position >= lengths[b] skipped (they are padding that attention never reads). With split the
 // output holds two planes: y[0 : rows*D] = fp16(r), y[rows*D : 2*rows*D] = fp16(r - fp16(r)).

@@ -13,6 +13,22 @@
 
 namespace tessery {
 
+// The float4 pieces of the norm and the rotation, shared by the separate kernels and the fused
+// one so both round the same way: sum of squares of a piece, the row's 1 / rms, and the rotated
+// pair (explicit fmaf, no contraction left to the compiler).
+__device__ __forceinline__ float squares4(const floatx4 v) {
+  return (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+}
+__device__ __forceinline__ float inv_rms(float squares, int cols, float eps) {
+  return 1.0f / sqrtf(wave_sum(squares) / static_cast<float>(cols) + eps);
+}
+__device__ __forceinline__ float rope_first(float a, float b, float cv, float sv) {
+  return fmaf(a, cv, -(b * sv));
+}
+__device__ __forceinline__ float rope_second(float a, float b, float cv, float sv) {
+  return fmaf(a, sv, b * cv);
+}
+
 // One wavefront per row, 4 rows per 256-thread workgroup. out may alias x. With VEC (cols a
 // multiple of 4, x and out 16-byte aligned) rows are read and written as float4.
 template <bool VEC>
@@ -29,10 +45,9 @@ __global__ __launch_bounds__(256) void rms_norm_f32(const float* x, const uint16
     const floatx4* x4 = reinterpret_cast<const floatx4*>(xr);
 #pragma unroll 4
     for (int c = lane; c < c4n; c += 64) {
-      const floatx4 v = x4[c];
-      squares += (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+      squares += squares4(x4[c]);
     }
-    const float inv = 1.0f / sqrtf(wave_sum(squares) / static_cast<float>(cols) + eps);
+    const float inv = inv_rms(squares, cols, eps);
     floatx4* y4 = reinterpret_cast<floatx4*>(yr);
 #pragma unroll 4
     for (int c = lane; c < c4n; c += 64) {
@@ -63,8 +78,49 @@ __global__ __launch_bounds__(256) void rope_f32(float* x, const float* __restric
   const float cv = cos_tab[pos * halfdim + c], sv = sin_tab[pos * halfdim + c];
   float* r = x + static_cast<size_t>(row) * dim;
   const float a = r[c], b = r[c + halfdim];
-  r[c] = a * cv - b * sv;
-  r[c + halfdim] = a * sv + b * cv;
+  r[c] = rope_first(a, b, cv, sv);
+  r[c + halfdim] = rope_second(a, b, cv, sv);
+}
+
+// rms_norm in place followed by rope on the same rows, in one pass with the same bits: one
+// wavefront per row of dim (8 | dim, dim <= 256) floats, lane l holds floats 4l .. 4l + 3; the
+// lanes of the two halves swap their pieces for the rotation.
+__global__ __launch_bounds__(256) void rms_norm_rope_f32(float* x, const uint16_t* __restrict__ w,
+                                                         const float* __restrict__ cos_tab,
+                                                         const float* __restrict__ sin_tab,
+                                                         int rows, int dim, float eps, int heads,
+                                                         int seq) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const int c4n = dim >> 2, half4 = dim >> 3;
+  floatx4* xr = reinterpret_cast<floatx4*>(x + static_cast<size_t>(row) * dim);
+  floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+  float squares = 0.0f;
+  if (lane < c4n) {
+    v = xr[lane];
+    squares += squares4(v);
+  }
+  const float inv = inv_rms(squares, dim, eps);
+  floatx4 y;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) y[j] = lane < c4n ? v[j] * inv * bf16_to_float(w[4 * lane + j]) : 0.0f;
+  const bool first = lane < half4;
+  const int partner = first ? lane + half4 : lane - half4;
+  floatx4 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o[j] = __shfl(y[j], partner < 64 && partner >= 0 ? partner : lane);
+  if (lane >= c4n) return;
+  const int halfdim = dim >> 1;
+  const int pos = (row / heads) % seq;
+  const int c = 4 * (first ? lane : lane - half4);
+  floatx4 r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float cv = cos_tab[pos * halfdim + c + j], sv = sin_tab[pos * halfdim + c + j];
+    r[j] = first ? rope_first(y[j], o[j], cv, sv) : rope_second(o[j], y[j], cv, sv);
+  }
+  xr[lane] = r;
 }
 
 // fp16 rows [B,S,heads,D]; T = D/16 lanes per row, lane j owns channels 8j..8j+7 and their
@@ -157,6 +213,18 @@ hipError_t launch_rms_norm_f32(const float* x, const uint16_t* w, float* out, in
     rms_norm_f32<true><<<(rows + 3) / 4, 256, 0, st>>>(x, w, out, rows, cols, eps);
   else
     rms_norm_f32<false><<<(rows + 3) / 4, 256, 0, st>>>(x, w, out, rows, cols, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_rms_norm_rope_f32(float* x, const uint16_t* w, const float* cos_tab,
+                                   const float* sin_tab, int rows, int dim, float eps, int heads,
+                                   int seq, hipStream_t st) {
+  if (rows <= 0) return hipSuccess;
+  if (dim <= 0 || dim % 8 || dim > 256 || heads <= 0 || seq <= 0 ||
+      (reinterpret_cast<uintptr_t>(x) & 15))
+    return hipErrorNotReady;  // the separate kernels run instead
+  rms_norm_rope_f32<<<(rows + 3) / 4, 256, 0, st>>>(x, w, cos_tab, sin_tab, rows, dim, eps, heads,
+                                                   seq);
   return hipGetLastError();
 }
 

@@ -912,6 +912,16 @@ hipError_t launch_fused_pair(Runtime* rt, const Op& a, const Op& b) {
         static_cast<const float*>(b.ptr[1]), static_cast<const float*>(b.ptr[2]),
         static_cast<int>(b.threads / 32), static_cast<int>(b.p.cols), b.p.eps, st);
   }
+  if (a.route == R_RMS_NORM && b.route == R_ROPE && a.ptr[2] == a.ptr[0] &&
+      b.ptr[0] == a.ptr[0] && b.p.dim == a.p.cols &&
+      static_cast<uint64_t>(b.p.n) == (a.threads / 32) * (a.p.cols / 2)) {
+    const RopeTable* t = rope_of(rt, b.p);
+    if (!t) return hipErrorNotReady;
+    return tessery::launch_rms_norm_rope_f32(
+        static_cast<float*>(a.ptr[0]), static_cast<const uint16_t*>(a.ptr[1]), t->cos, t->sin,
+        static_cast<int>(a.threads / 32), static_cast<int>(a.p.cols), a.p.eps,
+        static_cast<int>(b.p.heads), static_cast<int>(b.p.seq), st);
+  }
   return hipErrorNotReady;
 }
 

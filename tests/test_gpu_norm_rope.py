@@ -133,3 +133,45 @@ def test_fp32_unfused_qwen_block(runtime):
     qn = ref.norm_rope(q, bf16_values(gq), 1e-6, 1e6)
     kn = ref.norm_rope(k, bf16_values(gk), 1e-6, 1e6)
     check_f32(got, ref_attention.attention(qn, kn, v, lengths, bidirectional=False))
+
+
+@pytest.mark.parametrize("tokens,heads,seq,dim", [(64, 16, 32, 128), (24, 8, 12, 64),
+                                                  (10, 2, 5, 256), (9, 3, 3, 8), (6, 2, 3, 12)])
+def test_rms_norm_then_rope_fused_in_one_command(runtime, tokens, heads, seq, dim):
+    """rms_norm in place followed by rope on the same rows (qwen3.py:216-237) runs as one kernel
+    when both sit in one command; the bits equal the two launches run in separate commands."""
+    rng = np.random.default_rng(dim + heads)
+    x = (3.0 * rng.normal(size=(tokens * heads, dim))).astype(np.float32)
+    w = bf16_words(rng.uniform(0.5, 1.5, dim))
+    theta, eps = 1e6, 1e-6
+    count = tokens * heads * dim // 2
+
+    def norm(buf, wb):
+        runtime._dispatch("rms_norm", [buf, wb, buf], threads=tokens * heads * 32, group_size=32,
+                          cols=dim, eps=eps)
+
+    def rope(buf):
+        runtime._dispatch("rope", [buf], threads=count, n=count, heads=heads, seq=seq, dim=dim,
+                          theta=theta)
+
+    results = []
+    for fused in (True, False):
+        xb, wb = runtime.upload(x), runtime.upload(w)
+        try:
+            if fused:
+                with runtime.command():
+                    norm(xb, wb)
+                    rope(xb)
+            else:
+                with runtime.command():
+                    norm(xb, wb)
+                with runtime.command():
+                    rope(xb)
+            results.append(runtime.read(xb, x.shape))
+        finally:
+            xb.close()
+            wb.close()
+    np.testing.assert_array_equal(results[0], results[1])
+    # rows are [batch, seq, heads] in order (tokens is a multiple of seq in every case)
+    want = ref.norm_rope(x.reshape(-1, seq, heads, dim), bf16_values(w), eps, theta)
+    np.testing.assert_allclose(results[0], want.reshape(x.shape), atol=2e-5, rtol=1e-5)
