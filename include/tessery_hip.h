@@ -44,7 +44,13 @@ int mi_begin(void *runtime);
 /* runtime.mm:109-146. `name` selects a route (kernel), `buffers` are mi_buffer handles bound in
  * order, `parameters` is the 64-byte Params block (kernels.metal:5-8), `threads`/`group` follow
  * the reference thread formulas (metal.py:532-569, 416-499) and are validated against them.
- * Shapes implied by Params/threads are checked against buffer sizes before anything launches. */
+ * Shapes implied by Params/threads are checked against buffer sizes before anything launches.
+ * Routes (kernels.metal names): attention, attention_tiled, attention_tail_32,
+ * attention_tail_128, rms_norm, rope, linear4, linear4_tiled, linear4_tail, linear4_16x32_k64,
+ * linear4_32x32_k64, linear4_small3, gated4_16x32_k64, gated4_8x32, silu_gate, matmul_f32,
+ * matmul_f32_tiled, matmul_f32_chunk32, matmul_bias_f32, matmul_bias_f32_chunk32, add_bias,
+ * gelu_f32, layer_norm, add, embedding4, embedding_position, pool_project; additions:
+ * attention_f16, attention_f16_scalar, attention_f16_norm_rope, norm_rope_f16, qkv4_f16, copy. */
 int mi_dispatch(void *runtime, const char *name, void **buffers, uint32_t count,
                 const void *parameters, uint32_t size, uint64_t threads, uint32_t group);
 /* runtime.mm:217-253 */
