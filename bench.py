@@ -473,9 +473,9 @@ def bench_qwen_tail(args, tokens: int = 16 * 256) -> dict:
         gemm_s = 2 * ks["linear4_32x32_k64"] + 2 * ks["gated4_16x32_k64"]
         kernel = "linear4_32x32_k64 + gated4_16x32_k64"
     tflops = flop / gemm_s / 1e12
-    # from 2048 rows linear4 runs on fp16 MFMA (row-scaled hi + lo halves of x, two MFMAs per
+    # from 1024 rows linear4 runs on fp16 MFMA (row-scaled hi + lo halves of x, two MFMAs per
     # product): priced against the fp16 peak; below that on fp32 MFMA
-    hilo = tokens >= 2048
+    hilo = tokens >= 1024
     peak = PEAK_F16_TFLOPS if hilo else PEAK_F32_TFLOPS
     gemm_bytes = tokens * (width + hidden + hidden + 2 * inter + inter) * 4 + (
         (hidden * width + 2 * inter * hidden + hidden * inter) // 2)

@@ -69,7 +69,7 @@ hipError_t launch_gated4_f32(const float* x, const uint32_t* w, const uint16_t* 
 // The same projection for M >= kLinear4HiloRows rows on fp16 MFMA: rows scaled by powers of two
 // and split into hi + lo fp16 halves (about 22 bits), exact codes, fp32 sums. scratch holds the M
 // row scales. x and y start at row 0 of the range; N % 128 == 0, K % 64 == 0.
-constexpr int kLinear4HiloRows = 2048;
+constexpr int kLinear4HiloRows = 1024;
 hipError_t launch_linear4_hilo_f32(const float* x, const uint32_t* w, const uint16_t* scales,
                                    const uint16_t* biases, float* y, int M, int N, int K,
                                    float* scratch, size_t scratch_floats, hipStream_t st);

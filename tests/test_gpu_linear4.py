@@ -132,10 +132,11 @@ def test_eight_row_offset_preserves_surrounding_rows(runtime):
     np.testing.assert_array_equal(out[16:24], 64)
 
 
-@pytest.mark.parametrize("m,n,k", [(2048, 1024, 1024), (4096, 3072, 1024), (2050, 1024, 3072),
+@pytest.mark.parametrize("m,n,k", [(1024, 2048, 1024), (1100, 1024, 2048), (2048, 1024, 1024),
+                                   (4096, 3072, 1024), (2050, 1024, 3072),
                                    (2176, 128, 64), (4097, 2048, 1024)])
 def test_large_batch_fp16_mfma_path(runtime, m, n, k):
-    """From 2048 rows the projection runs on fp16 MFMA over row-scaled hi + lo halves of x. Row
+    """From 1024 rows the projection runs on fp16 MFMA over row-scaled hi + lo halves of x. Row
     magnitudes spread over 2^-20 .. 2^20, a zero row, rows near fp32's smallest and largest
     normal values (beyond fp16's range): every output stays within fp32-grade error of the
     float64 product, measured against sum_k |x| |w| of the same element."""
