@@ -213,3 +213,47 @@ def test_plan_evicted_while_its_replay_is_queued(runtime):
     finally:
         for b in bufs + outs:
             b.close()
+
+
+@pytest.mark.parametrize("case", ["emb4_cols", "emb4_short_out", "emb4_short_ids", "emb4_scales",
+                                  "embpos_positions", "embpos_types", "pool_dim", "pool_lengths",
+                                  "pool_group", "pool_short_x"])
+def test_model_end_routes_reject_bad_launches(runtime, case):
+    """embedding4, embedding_position and pool_project refuse launches whose Params or thread
+    counts do not fit their buffers (kernels.metal:21-30, 339-360), at dispatch time."""
+    f = lambda *shape: runtime.buffer(int(np.prod(shape)) * 4)  # noqa: E731
+    bufs = []
+    try:
+        if case.startswith("emb4"):
+            cols, tokens, vocab = 64 if case != "emb4_cols" else 40, 4, 10
+            ids = f(tokens if case != "emb4_short_ids" else tokens - 1)
+            w = runtime.buffer(vocab * (64 // 8) * 4)
+            s = runtime.buffer(vocab * 2 * (1 if case != "emb4_scales" else 0) or 2)
+            out = f(tokens * cols - (8 if case == "emb4_short_out" else 0))
+            bufs += [ids, w, s, out]
+            with pytest.raises(InferenceError), runtime.command():
+                runtime._dispatch("embedding4", [ids, w, s, s, out], threads=tokens * cols,
+                                  n=tokens * cols, cols=cols)
+        elif case.startswith("embpos"):
+            cols, seq, tokens = 32, 8, 16
+            ids, words = f(tokens), f(5, cols)
+            positions = f(seq - 1 if case == "embpos_positions" else seq, cols)
+            types = f(cols - 1 if case == "embpos_types" else cols)
+            out = f(tokens, cols)
+            bufs += [ids, words, positions, types, out]
+            with pytest.raises(InferenceError), runtime.command():
+                runtime._dispatch("embedding_position", [ids, words, positions, types, out],
+                                  threads=tokens * cols, n=tokens * cols, cols=cols, seq=seq)
+        else:
+            batch, seq, cols = 3, 4, 64
+            x = f(batch * seq * cols - (1 if case == "pool_short_x" else 0))
+            lengths = runtime.buffer((batch - 1 if case == "pool_lengths" else batch) * 4)
+            out = f(batch, cols)
+            bufs += [x, lengths, out]
+            with pytest.raises(InferenceError), runtime.command():
+                runtime._dispatch("pool_project", [x, lengths, out], threads=batch * 32,
+                                  group_size=64 if case == "pool_group" else 32, seq=seq,
+                                  cols=cols, dim=cols + 1 if case == "pool_dim" else cols)
+    finally:
+        for b in bufs:
+            b.close()
