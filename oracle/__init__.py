@@ -23,5 +23,10 @@ Modules and what pins each one (the tests under tests/test_oracle_*.py run these
   bert_block  the BERT (BGE) encoder layer (bert.py:186-230): fp32 projections with bias, GELU,
               LayerNorm and bidirectional attention. Pinned against torch's gelu / layer_norm,
               math.erf and transformers' BertLayer in float64 with a key-padding mask.
+  models      whole forwards: embedding4 / embedding_position gathers (kernels.metal:21-30,
+              351-360), pool_project (kernels.metal:339-349), the Qwen3 forward (qwen3.py:112-296)
+              and the BERT forward (bert.py:103-251). Pinned by the scalar weight4 indexing, the
+              pooling definition, and transformers' Qwen3Model and BertModel in float64 on the same
+              weights (1e-10), with planted mistakes (wrong pooled token, a dropped layer).
 No function here is "parity unpinned".
 """
