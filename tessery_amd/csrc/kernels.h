@@ -39,6 +39,10 @@ hipError_t launch_rms_norm_f32(const float* x, const uint16_t* w, float* out, in
 // tessery rope (kernels.metal:65-74): in place, split-half pairs, pos = (row / heads) % seq.
 hipError_t launch_rope_f32(float* x, const float* cos_tab, const float* sin_tab, uint32_t n,
                            int heads, int seq, int dim, hipStream_t st);
+// launch_add_f32(x, r, x) followed by launch_rms_norm_f32(x, w, y) as one pass with the same bits;
+// hipErrorNotReady unless cols % 4 == 0 and x, r, y are 16-byte aligned.
+hipError_t launch_add_rms_norm_f32(float* x, const float* r, const uint16_t* w, float* y,
+                                   int rows, int cols, float eps, hipStream_t st);
 // launch_rms_norm_f32 in place (x == out) followed by launch_rope_f32 on the same rows, as one
 // kernel with the same bits; hipErrorNotReady when the shape is not covered (8 | dim <= 256, x
 // 16-byte aligned) and the two launches must run instead.

@@ -216,6 +216,50 @@ hipError_t launch_rms_norm_f32(const float* x, const uint16_t* w, float* out, in
   return hipGetLastError();
 }
 
+// add(x, r -> x) followed by rms_norm(x -> y), one wavefront per row, float4 pieces: the sum
+// is stored to x, and y takes the bits of the separate float4 rms_norm (same order of squares).
+__global__ __launch_bounds__(256) void add_rms_norm_f32(float* x, const float* __restrict__ r,
+                                                        const uint16_t* __restrict__ w, float* y,
+                                                        int rows, int cols, float eps) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const int c4n = cols >> 2;
+  floatx4* x4 = reinterpret_cast<floatx4*>(x + static_cast<size_t>(row) * cols);
+  const floatx4* r4 = reinterpret_cast<const floatx4*>(r + static_cast<size_t>(row) * cols);
+  float squares = 0.0f;
+#pragma unroll 4
+  for (int c = lane; c < c4n; c += 64) {
+    const floatx4 a = x4[c], b = r4[c];
+    floatx4 v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = a[j] + b[j];
+    x4[c] = v;
+    squares += squares4(v);
+  }
+  const float inv = inv_rms(squares, cols, eps);
+  floatx4* y4 = reinterpret_cast<floatx4*>(y + static_cast<size_t>(row) * cols);
+#pragma unroll 4
+  for (int c = lane; c < c4n; c += 64) {
+    const floatx4 v = x4[c];  // this lane's own store above
+    floatx4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = v[j] * inv * bf16_to_float(w[4 * c + j]);
+    y4[c] = o;
+  }
+}
+
+hipError_t launch_add_rms_norm_f32(float* x, const float* r, const uint16_t* w, float* y,
+                                   int rows, int cols, float eps, hipStream_t st) {
+  if (rows <= 0) return hipSuccess;
+  if (cols <= 0 || cols % 4 ||
+      ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(r) |
+        reinterpret_cast<uintptr_t>(y)) & 15))
+    return hipErrorNotReady;  // the separate launches run instead
+  add_rms_norm_f32<<<(rows + 3) / 4, 256, 0, st>>>(x, r, w, y, rows, cols, eps);
+  return hipGetLastError();
+}
+
 hipError_t launch_rms_norm_rope_f32(float* x, const uint16_t* w, const float* cos_tab,
                                    const float* sin_tab, int rows, int dim, float eps, int heads,
                                    int seq, hipStream_t st) {

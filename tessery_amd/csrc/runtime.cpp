@@ -912,6 +912,14 @@ hipError_t launch_fused_pair(Runtime* rt, const Op& a, const Op& b) {
         static_cast<const float*>(b.ptr[1]), static_cast<const float*>(b.ptr[2]),
         static_cast<int>(b.threads / 32), static_cast<int>(b.p.cols), b.p.eps, st);
   }
+  if (a.route == R_ADD && b.route == R_RMS_NORM && a.ptr[2] == a.ptr[0] &&
+      a.ptr[1] != a.ptr[0] && b.ptr[0] == a.ptr[0] && b.ptr[2] != a.ptr[1] &&
+      static_cast<uint64_t>(a.p.n) == (b.threads / 32) * b.p.cols) {
+    return tessery::launch_add_rms_norm_f32(
+        static_cast<float*>(a.ptr[0]), static_cast<const float*>(a.ptr[1]),
+        static_cast<const uint16_t*>(b.ptr[1]), static_cast<float*>(b.ptr[2]),
+        static_cast<int>(b.threads / 32), static_cast<int>(b.p.cols), b.p.eps, st);
+  }
   if (a.route == R_RMS_NORM && b.route == R_ROPE && a.ptr[2] == a.ptr[0] &&
       b.ptr[0] == a.ptr[0] && b.p.dim == a.p.cols &&
       static_cast<uint64_t>(b.p.n) == (a.threads / 32) * (a.p.cols / 2)) {

@@ -175,3 +175,39 @@ def test_rms_norm_then_rope_fused_in_one_command(runtime, tokens, heads, seq, di
     # rows are [batch, seq, heads] in order (tokens is a multiple of seq in every case)
     want = ref.norm_rope(x.reshape(-1, seq, heads, dim), bf16_values(w), eps, theta)
     np.testing.assert_allclose(results[0], want.reshape(x.shape), atol=2e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("rows,cols,in_place", [(130, 1024, False), (7, 64, False), (5, 1030, False),
+                                                (33, 1024, True)])
+def test_add_then_rms_norm_fused_in_one_command(runtime, rows, cols, in_place):
+    """add(x, r -> x) followed by rms_norm(x -> y) (the residual and the next norm of
+    qwen3.py:246-280) runs as one pass inside one command; x and y equal, bit for bit, the two
+    launches run in separate commands (cols % 4 != 0 is not fused and must match too)."""
+    rng = np.random.default_rng(rows + cols)
+    x = rng.normal(size=(rows, cols)).astype(np.float32)
+    r = (0.5 * rng.normal(size=(rows, cols))).astype(np.float32)
+    w = bf16_words(rng.uniform(0.5, 1.5, cols))
+    outs = []
+    for fused in (True, False):
+        xb, rb, wb = runtime.upload(x), runtime.upload(r), runtime.upload(w)
+        yb = xb if in_place else runtime.buffer(x.nbytes)
+        try:
+            add = dict(threads=rows * cols, n=rows * cols)
+            norm = dict(threads=rows * 32, group_size=32, cols=cols, eps=1e-6)
+            if fused:
+                with runtime.command():
+                    runtime._dispatch("add", [xb, rb, xb], **add)
+                    runtime._dispatch("rms_norm", [xb, wb, yb], **norm)
+            else:
+                with runtime.command():
+                    runtime._dispatch("add", [xb, rb, xb], **add)
+                with runtime.command():
+                    runtime._dispatch("rms_norm", [xb, wb, yb], **norm)
+            outs.append((runtime.read(xb, x.shape), runtime.read(yb, x.shape)))
+        finally:
+            for b in {id(b): b for b in (xb, rb, wb, yb)}.values():
+                b.close()
+    np.testing.assert_array_equal(outs[0][0], outs[1][0])
+    np.testing.assert_array_equal(outs[0][1], outs[1][1])
+    want = ref.rms_norm(x.astype(np.float64) + r, bf16_values(w), 1e-6)
+    np.testing.assert_allclose(outs[0][1], want, atol=2e-6, rtol=2e-6)
