@@ -82,35 +82,49 @@ __global__ __launch_bounds__(256) void rope_f32(float* x, const float* __restric
   r[c + halfdim] = rope_second(a, b, cv, sv);
 }
 
-// rms_norm in place followed by rope on the same rows, in one pass with the same bits: one
-// wavefront per row of dim (8 | dim, dim <= 256) floats, lane l holds floats 4l .. 4l + 3; the
-// lanes of the two halves swap their pieces for the rotation.
+// rms_norm in place followed by rope on the same rows, in one pass with the same bits: lane l of
+// a row holds floats 4l .. 4l + 3 (8 | dim, dim <= 256); the lanes of the two halves swap their
+// pieces for the rotation. PAIR (dim <= 128): two rows per wavefront, one per 32-lane half; the
+// half-wave butterfly gives the bits of wave_sum with the other half zero (its first step adds
+// exact zeros).
+template <bool PAIR>
 __global__ __launch_bounds__(256) void rms_norm_rope_f32(float* x, const uint16_t* __restrict__ w,
                                                          const float* __restrict__ cos_tab,
                                                          const float* __restrict__ sin_tab,
                                                          int rows, int dim, float eps, int heads,
                                                          int seq) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= rows) return;
+  const int slot = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = PAIR ? (threadIdx.x & 31) : (threadIdx.x & 63);
+  const int row = PAIR ? 2 * slot + ((threadIdx.x >> 5) & 1) : slot;
+  const bool live = row < rows;
+  if (PAIR ? 2 * slot >= rows : !live) return;  // wavefront-uniform
   const int c4n = dim >> 2, half4 = dim >> 3;
-  floatx4* xr = reinterpret_cast<floatx4*>(x + static_cast<size_t>(row) * dim);
+  floatx4* xr = reinterpret_cast<floatx4*>(x + static_cast<size_t>(live ? row : 0) * dim);
   floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
   float squares = 0.0f;
-  if (lane < c4n) {
+  if (live && lane < c4n) {
     v = xr[lane];
     squares += squares4(v);
   }
-  const float inv = inv_rms(squares, dim, eps);
+  float inv;
+  if constexpr (PAIR) {
+    float total = squares;
+    for (int off = 16; off >= 1; off >>= 1) total += __shfl_xor(total, off);
+    inv = 1.0f / sqrtf(total / static_cast<float>(dim) + eps);
+  } else {
+    inv = inv_rms(squares, dim, eps);
+  }
   floatx4 y;
 #pragma unroll
   for (int j = 0; j < 4; ++j) y[j] = lane < c4n ? v[j] * inv * bf16_to_float(w[4 * lane + j]) : 0.0f;
   const bool first = lane < half4;
   const int partner = first ? lane + half4 : lane - half4;
+  const int base = PAIR ? (threadIdx.x & 32) : 0;
   floatx4 o;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) o[j] = __shfl(y[j], partner < 64 && partner >= 0 ? partner : lane);
-  if (lane >= c4n) return;
+  for (int j = 0; j < 4; ++j)
+    o[j] = __shfl(y[j], base + (partner >= 0 && partner < (PAIR ? 32 : 64) ? partner : lane));
+  if (!live || lane >= c4n) return;
   const int halfdim = dim >> 1;
   const int pos = (row / heads) % seq;
   const int c = 4 * (first ? lane : lane - half4);
@@ -267,8 +281,14 @@ hipError_t launch_rms_norm_rope_f32(float* x, const uint16_t* w, const float* co
   if (dim <= 0 || dim % 8 || dim > 256 || heads <= 0 || seq <= 0 ||
       (reinterpret_cast<uintptr_t>(x) & 15))
     return hipErrorNotReady;  // the separate kernels run instead
-  rms_norm_rope_f32<<<(rows + 3) / 4, 256, 0, st>>>(x, w, cos_tab, sin_tab, rows, dim, eps, heads,
-                                                   seq);
+  if (dim <= 128) {
+    const int pairs = (rows + 1) / 2;
+    rms_norm_rope_f32<true><<<(pairs + 3) / 4, 256, 0, st>>>(x, w, cos_tab, sin_tab, rows, dim,
+                                                             eps, heads, seq);
+  } else {
+    rms_norm_rope_f32<false><<<(rows + 3) / 4, 256, 0, st>>>(x, w, cos_tab, sin_tab, rows, dim,
+                                                             eps, heads, seq);
+  }
   return hipGetLastError();
 }
 
