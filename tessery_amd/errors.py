@@ -1,9 +1,12 @@
 """Stable error types of the drop-in boundary.
 
-Same class names, codes and base class as tessery's errors (src/metal_inference/errors.py:1-59;
-re-exported by src/tessery/errors.py:1-33), so callers that catch them keep working. Messages
-carry only the stable code, never payloads. HipUnavailableError is the HIP-side reason for the
-reference's MetalUnavailableError and subclasses it.
+The classes raised by this path keep the class names, `code` strings and base class of tessery's
+errors (src/metal_inference/errors.py:1-59, re-exported by src/tessery/errors.py:1-33), so a
+caller that catches them keeps working. Messages carry only the stable code, never payloads.
+HipUnavailableError is the HIP-side reason for the reference's MetalUnavailableError and
+subclasses it. Only the classes something in this package raises are defined here; the
+reference's API/HTTP-layer classes (overload, deadline, cancellation, ...) belong to its service
+layer, which this package does not include.
 """
 
 
@@ -15,46 +18,28 @@ class EmbeddingError(Exception):
         super().__init__(self.code)
 
 
-class ConfigurationError(EmbeddingError):
-    code = "configuration_error"
-
-
-class InvalidInputError(EmbeddingError):
-    code = "invalid_input"
-    http_status = 400
-
-
 class ManifestError(EmbeddingError):
+    """A weight pack or its metadata failed verification (weights.py, backends.py)."""
+
     code = "invalid_manifest"
 
 
 class UnsupportedProfileError(EmbeddingError):
+    """A model config outside the shapes a backend serves."""
+
     code = "unsupported_profile"
 
 
-class OverloadError(EmbeddingError):
-    code = "overloaded"
-    http_status = 429
-
-
-class CanceledError(EmbeddingError):
-    code = "canceled"
-
-
-class DeadlineExceededError(EmbeddingError):
-    code = "deadline_exceeded"
-
-
 class InferenceError(EmbeddingError):
+    """A native call failed or the runtime was used outside its contract."""
+
     code = "inference_failed"
 
 
 class ClosedError(EmbeddingError):
+    """The runtime or backend was already closed."""
+
     code = "closed"
-
-
-class PrerequisiteError(EmbeddingError):
-    code = "baseline_required"
 
 
 class MetalUnavailableError(EmbeddingError):
@@ -68,21 +53,17 @@ class HipUnavailableError(MetalUnavailableError):
 
 
 class NativeBuildError(EmbeddingError):
+    """libtessery_hip.so is missing, unreadable or built for another ABI version."""
+
     code = "native_engine_not_built"
 
 
 __all__ = [
     "EmbeddingError",
-    "ConfigurationError",
-    "InvalidInputError",
     "ManifestError",
     "UnsupportedProfileError",
-    "OverloadError",
-    "CanceledError",
-    "DeadlineExceededError",
     "InferenceError",
     "ClosedError",
-    "PrerequisiteError",
     "MetalUnavailableError",
     "HipUnavailableError",
     "NativeBuildError",

@@ -5,10 +5,11 @@ qwen3.py:194-245 on the seeded 16x256 workload (x [4096, 1024], W_q 1024->2048, 
 
 Each stage is held to its own bar against float64:
   * projection: every output within fp16 rounding of the exact product (2^-11 |y| + 1e-4);
-  * attention: max-abs <= 2e-3 against the float64 oracle evaluated on the projection's fp16
-    outputs (the attention operands of this path are fp16 by definition).
+  * attention: max-abs <= 1e-4 (the fp32 bar) against the float64 oracle evaluated on the
+    projection's fp16 outputs (the attention operands of this path are fp16 by definition; the
+    fused route carries normalized q, k and P as hi + lo fp16 pairs and writes fp32).
 The projection outputs reach |y| ~ 6, where one fp16 ulp is 2^-8, so the chain as a whole is
-compared with an all-float64 chain only for the record (printed), not against 2e-3."""
+compared with an all-float64 chain only for the record (printed), not against a bar."""
 
 import numpy as np
 import pytest
@@ -20,7 +21,7 @@ from tessery_amd import workloads
 
 pytestmark = pytest.mark.gpu
 
-F16_MAX = 2e-3
+FUSED_F32_MAX = 1e-4
 
 
 def test_qkv4_norm_rope_attention_16x256(runtime):
@@ -67,6 +68,6 @@ def test_qkv4_norm_rope_attention_16x256(runtime):
 
     expected = chain(*(t.astype(np.float64) for t in y))
     err = float(np.max(np.abs(got.astype(np.float64) - expected)))
-    assert err <= F16_MAX, err
+    assert err <= FUSED_F32_MAX, err
     end_to_end = float(np.max(np.abs(got.astype(np.float64) - chain(*exact))))
     print(f"attention stage max-abs {err:.3e}; against the all-float64 chain {end_to_end:.3e}")
