@@ -646,6 +646,19 @@ __device__ __forceinline__ float dot_ones(half4 p, float acc) {
   return __builtin_amdgcn_fdot2(h2{p[2], p[3]}, one, acc, false);
 }
 
+// The score accumulators of a QK^T chain are read by VALU (row max, masking) right after the last
+// v_mfma_f32_16x16x32_f16 of the chain, and the hardware does not interlock that read: it needs 8
+// wait states after the MFMA. The compiler counts them inside a basic block but not across the
+// branch that skips the causal masking, where the row max then read a partly accumulated score
+// (the softmax still came out right, being shift-invariant, but its rounding depended on timing).
+// The fence is 8 wait states after the chain, ordered after it through the operand.
+__device__ __forceinline__ void mfma_result_fence(floatx4& acc) {
+  asm volatile("s_nop 7" : "+v"(acc));
+}
+__device__ __forceinline__ void mfma_result_fence(floatx4& a, floatx4& b) {
+  asm volatile("s_nop 7" : "+v"(a), "+v"(b));
+}
+
 // reduce over the four lanes r, r+16, r+32, r+48 that hold one query's scores
 __device__ __forceinline__ float rowmax4(float x) { return pair32(pair16(x, true), true); }
 __device__ __forceinline__ float rowsum4(float x) { return pair32(pair16(x, false), false); }
@@ -883,6 +896,7 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
 
     if constexpr (KT == 16) {
       floatx4 sc = qk_block(kst, 0);
+      mfma_result_fence(sc);
       // element j is key 4g + j of this tile
       if (kt * KT + KT > g.limit_min) {
 #pragma unroll
@@ -949,6 +963,7 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
       floatx4 sc[2];
       sc[0] = qk_block(kst, 0);
       sc[1] = qk_block(kst, 16);
+      mfma_result_fence(sc[0], sc[1]);
       // element (blk, j) is key 8g + 4blk + j of this tile
       if (kt * KT + KT > g.limit_min) {
 #pragma unroll
@@ -1095,7 +1110,13 @@ static bool geometry_fits(int B, int KV, int nblocks, int blockdiv) {
   return static_cast<uint64_t>(nblocks) * static_cast<uint64_t>(blockdiv) < (1ull << 32);
 }
 
+bool attention_scalar_fits(uint64_t B, uint64_t S, uint64_t H) {
+  // one 64-lane workgroup per (token, head) on a 1-D grid: at most 2^32 - 1 threads
+  return B * S * H * 64 < (1ull << 32);
+}
+
 hipError_t launch_attention_scalar(const AttnArgs& a, hipStream_t st) {
+  if (!attention_scalar_fits(a.B, a.S, a.H)) return hipErrorInvalidValue;
   const unsigned grid = static_cast<unsigned>(a.B * a.S * a.H);
   if (!grid) return hipSuccess;
   const float scale = a.scale;
@@ -1119,14 +1140,20 @@ hipError_t launch_attention_scalar(const AttnArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+bool attention_f32_fits(int B, int S, int H, int KV) {
+  if (B <= 0 || S <= 0 || H <= 0 || KV <= 0 || H % KV) return false;
+  const int G = H / KV;
+  return geometry_fits(B, KV, G * ((S + 31) / 32), G);
+}
+
 hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st) {
   if (!a.B || !a.S || !a.H) return hipSuccess;
+  if (!attention_f32_fits(a.B, a.S, a.H, a.KV)) return hipErrorInvalidValue;
   const dim3 grid = mfma_grid(a.B, a.S, a.H, a.KV);
   F32Shape shp;
   shp.G = a.H / a.KV;
   shp.g = make_div(static_cast<uint32_t>(shp.G));
   shp.kv = make_div(static_cast<uint32_t>(a.KV));
-  if (!geometry_fits(a.B, a.KV, shp.G * ((a.S + 31) / 32), shp.G)) return hipErrorInvalidValue;
   const float sl2 = a.scale * kLog2e;
   auto q = static_cast<const float*>(a.q), k = static_cast<const float*>(a.k),
        v = static_cast<const float*>(a.v);
@@ -1162,21 +1189,27 @@ static void launch_f16_d(const AttnArgs& a, dim3 grid, F16Shape shp, float sl2, 
         a.gamma_q, a.rope_cos, a.rope_sin, a.eps, plane, shp);
 }
 
+bool attention_f16_fits(int B, int S, int H, int KV, int D) {
+  if (B <= 0 || S <= 0 || H <= 0 || KV <= 0 || H % KV || (D != 64 && D != 128)) return false;
+  const int G = H / KV;
+  const int hsh = __builtin_ctz(static_cast<unsigned>(f16_heads_per_wave(G)));
+  if (!geometry_fits(B, KV, f16_wave_blocks(S, G), G >> hsh)) return false;
+  // K/V DMA offsets are 32-bit bytes inside one (batch row, kv head) plane, row * rowbytes by
+  // __umul24
+  const uint64_t rowbytes = static_cast<uint64_t>(KV) * D * 2;
+  return static_cast<uint64_t>(S) * rowbytes < (1ull << 32) && S < (1 << 24) &&
+         rowbytes < (1u << 24);
+}
+
 hipError_t launch_attention_f16(const AttnArgs& a, hipStream_t st) {
   if (!a.B || !a.S || !a.H) return hipSuccess;
+  if (!attention_f16_fits(a.B, a.S, a.H, a.KV, a.D)) return hipErrorInvalidValue;
   F16Shape shp;
   shp.G = a.H / a.KV;
   shp.hsh = __builtin_ctz(static_cast<unsigned>(f16_heads_per_wave(shp.G)));
   shp.nwb = f16_wave_blocks(a.S, shp.G);
   shp.kv = make_div(static_cast<uint32_t>(a.KV));
   shp.hbn = make_div(static_cast<uint32_t>(shp.G >> shp.hsh));
-  if (!geometry_fits(a.B, a.KV, shp.nwb, shp.G >> shp.hsh)) return hipErrorInvalidValue;
-  // K/V DMA offsets are 32-bit bytes inside one (batch row, kv head) plane, row * rowbytes by
-  // __umul24
-  const uint64_t rowbytes = static_cast<uint64_t>(a.KV) * a.D * 2;
-  if (static_cast<uint64_t>(a.S) * rowbytes >= (1ull << 32) || a.S >= (1 << 24) ||
-      rowbytes >= (1u << 24))
-    return hipErrorInvalidValue;
   const dim3 grid = sched_grid(a.B, a.KV, (shp.nwb + 3) / 4);
 
   const float sl2 = a.scale * kLog2e;

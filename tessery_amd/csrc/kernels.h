@@ -29,6 +29,12 @@ struct AttnArgs {
   float eps;
 };
 
+// Shape limits of the attention launchers (grid sizes, 32-bit offsets, exact reciprocal
+// division), also checked by the runtime before a launch is queued.
+bool attention_scalar_fits(uint64_t B, uint64_t S, uint64_t H);
+bool attention_f32_fits(int B, int S, int H, int KV);
+bool attention_f16_fits(int B, int S, int H, int KV, int D);
+
 hipError_t launch_attention_scalar(const AttnArgs& a, hipStream_t st);
 hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st);
 hipError_t launch_attention_f16(const AttnArgs& a, hipStream_t st);
@@ -36,6 +42,11 @@ hipError_t launch_attention_f16(const AttnArgs& a, hipStream_t st);
 // tessery rms_norm (kernels.metal:53-63): rows x cols fp32, bf16 weight, out may alias x.
 hipError_t launch_rms_norm_f32(const float* x, const uint16_t* w, float* out, int rows, int cols,
                                float eps, hipStream_t st);
+// RoPE tables [S, D/2] of cos / sin(pos * theta^(-2j/D)), evaluated in float64 on the device
+// and rounded once to float32.
+bool rope_tables_fit(int S, int D);
+hipError_t launch_rope_tables(float* cos_tab, float* sin_tab, int S, int D, float theta,
+                              hipStream_t st);
 // tessery rope (kernels.metal:65-74): in place, split-half pairs, pos = (row / heads) % seq.
 hipError_t launch_rope_f32(float* x, const float* cos_tab, const float* sin_tab, uint32_t n,
                            int heads, int seq, int dim, hipStream_t st);
@@ -52,6 +63,7 @@ hipError_t launch_rms_norm_rope_f32(float* x, const uint16_t* w, const float* co
 // Fused per-head RMSNorm + RoPE on fp16 rows [B,S,heads,D] -> fp16 rows, rows with
 // position >= lengths[b] skipped (they are padding that attention never reads). With split the
 // output holds two planes: y[0 : rows*D] = fp16(r), y[rows*D : 2*rows*D] = fp16(r - fp16(r)).
+bool norm_rope_f16_fits(int B, int S, int heads, int D);
 hipError_t launch_norm_rope_f16(const _Float16* x, _Float16* y, const uint16_t* gamma,
                                 const float* cos_tab, const float* sin_tab,
                                 const uint32_t* lengths, int B, int S, int heads, int D,
@@ -115,6 +127,7 @@ struct Qkv4Args {
   int M, K;
   int scale_bf16;
 };
+bool qkv4_f16_fits(int M, int K, const int n[3]);
 hipError_t launch_qkv4_f16(const Qkv4Args& a, hipStream_t st);
 
 // tessery add (kernels.metal:300-304): out[i] = a[i] + b[i], i < n. out may alias a or b.

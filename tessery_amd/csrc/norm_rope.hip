@@ -6,8 +6,9 @@
 // The Qwen3 attention block applies both, in place, to q ([tokens*H, D] rows) and to k
 // ([tokens*KV, D] rows) before attention (src/metal_inference/qwen3.py:216-237).
 //
-// cos/sin come from a [seq, D/2] table that the runtime computes once per (seq, D, theta) in
-// float64 on the host and rounds to float32, so the rotation is as accurate as a float64 angle.
+// cos/sin come from a [seq, D/2] table computed by rope_tables in float64 and rounded once to
+// float32, so the rotation is as accurate as a float64 angle. The runtime builds it once per
+// (seq, D, theta); the allocation-free entry point rebuilds it in its scratch on every call.
 #include "common.h"
 #include "kernels.h"
 
@@ -292,11 +293,45 @@ hipError_t launch_rms_norm_rope_f32(float* x, const uint16_t* w, const float* co
   return hipGetLastError();
 }
 
+// cos_tab / sin_tab[pos][j] = cos / sin(pos * theta^(-2j / D)), j < D / 2, the angle and both
+// functions evaluated in float64 (kernels.metal:65-74 evaluates the angle with f32 pow; the
+// float64 angle is the closed form the f32 one approximates).
+__global__ __launch_bounds__(256) void rope_tables(float* __restrict__ cos_tab,
+                                                  float* __restrict__ sin_tab, uint32_t n,
+                                                  uint32_t half, double theta, double dim) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t pos = i / half, j = i - pos * half;
+  const double angle = static_cast<double>(pos) * pow(theta, -2.0 * j / dim);
+  cos_tab[i] = static_cast<float>(cos(angle));
+  sin_tab[i] = static_cast<float>(sin(angle));
+}
+
+bool rope_tables_fit(int S, int D) {
+  return S > 0 && D > 0 && D % 2 == 0 && static_cast<uint64_t>(S) * (D / 2) < (1ull << 31);
+}
+
+hipError_t launch_rope_tables(float* cos_tab, float* sin_tab, int S, int D, float theta,
+                              hipStream_t st) {
+  if (!rope_tables_fit(S, D) || !(theta > 0.0f)) return hipErrorInvalidValue;
+  const uint32_t n = static_cast<uint32_t>(S) * static_cast<uint32_t>(D / 2);
+  rope_tables<<<(n + 255) / 256, 256, 0, st>>>(cos_tab, sin_tab, n,
+                                               static_cast<uint32_t>(D / 2),
+                                               static_cast<double>(theta), static_cast<double>(D));
+  return hipGetLastError();
+}
+
 hipError_t launch_rope_f32(float* x, const float* cos_tab, const float* sin_tab, uint32_t n,
                            int heads, int seq, int dim, hipStream_t st) {
   if (!n) return hipSuccess;
   rope_f32<<<(n + 255) / 256, 256, 0, st>>>(x, cos_tab, sin_tab, n, heads, seq, dim);
   return hipGetLastError();
+}
+
+bool norm_rope_f16_fits(int B, int S, int heads, int D) {
+  // at least one position per 256-lane pass (D / 16 lanes per row); the grid's y is the batch
+  return B > 0 && B <= 65535 && S > 0 && heads > 0 && (D == 32 || D == 64 || D == 128) &&
+         (D / 16) * heads <= 256;
 }
 
 hipError_t launch_norm_rope_f16(const _Float16* x, _Float16* y, const uint16_t* gamma,
@@ -305,7 +340,7 @@ hipError_t launch_norm_rope_f16(const _Float16* x, _Float16* y, const uint16_t* 
                                 float eps, bool split, hipStream_t st) {
   const int64_t rows = static_cast<int64_t>(B) * S * heads;
   if (!rows) return hipSuccess;
-  if ((D / 16) * heads > 256) return hipErrorInvalidValue;  // one position per pass at least
+  if (!norm_rope_f16_fits(B, S, heads, D)) return hipErrorInvalidValue;
   // one pass per thread: as many workgroups in flight as there are position blocks
   const int block = 256 / ((D / 16) * heads);
   const dim3 grid(static_cast<unsigned>((S + block - 1) / block), static_cast<unsigned>(B));

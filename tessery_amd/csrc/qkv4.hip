@@ -431,19 +431,24 @@ hipError_t launch_linear4_hilo_f32(const float* x, const uint32_t* w, const uint
   return hipGetLastError();
 }
 
+// scale and bias words of a column tile, all groups: 2 * 128 * groups halves (8 KiB at K = 1024);
+// with the 60 KiB of x and weight stages, two workgroups fit a CU up to K = 2048
+static size_t qkv4_sb_bytes(int K) { return static_cast<size_t>(2 * 128 * 2) * (K / 64); }
+
+bool qkv4_f16_fits(int M, int K, const int n[3]) {
+  if (M <= 0 || K <= 0 || K % 64 || qkv4_sb_bytes(K) > 64 * 1024) return false;  // K <= 8192
+  for (int p = 0; p < 3; ++p)
+    if (n[p] <= 0 || n[p] % 128) return false;
+  return true;
+}
+
 hipError_t launch_qkv4_f16(const Qkv4Args& a, hipStream_t st) {
   if (a.M <= 0) return hipSuccess;
-  if (a.K % 64 || a.K <= 0) return hipErrorInvalidValue;
+  if (!qkv4_f16_fits(a.M, a.K, a.n)) return hipErrorInvalidValue;
   int tiles = 0;
-  for (int p = 0; p < 3; ++p) {
-    if (a.n[p] <= 0 || a.n[p] % 128) return hipErrorInvalidValue;
-    tiles += a.n[p] / 128;
-  }
+  for (int p = 0; p < 3; ++p) tiles += a.n[p] / 128;
   dim3 grid((a.M + 127) / 128, tiles);
-  // scale and bias words of a column tile, all groups: 2 * 128 * groups halves (8 KiB at K = 1024);
-  // with the 60 KiB of x and weight stages, two workgroups fit a CU up to K = 2048
-  const size_t sb_bytes = static_cast<size_t>(2 * 128 * 2) * (a.K / 64);
-  if (sb_bytes > 64 * 1024) return hipErrorInvalidValue;  // K > 8192
+  const size_t sb_bytes = qkv4_sb_bytes(a.K);
   if (a.scale_bf16)
     qkv4_f16<true><<<grid, 256, sb_bytes, st>>>(a);
   else

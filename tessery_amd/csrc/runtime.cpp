@@ -166,6 +166,9 @@ struct Runtime {
   std::vector<hipEvent_t> prof_events;
   std::vector<double> profile_seconds;
   std::map<std::tuple<uint32_t, uint32_t, uint32_t>, RopeTable> rope;
+  // Device allocations whose buffers were freed while a command was open: queued launches may
+  // still name them, so they are released only after the command has finished or aborted.
+  std::vector<void*> pending_free;
 };
 
 struct PlanOp {
@@ -201,7 +204,11 @@ struct AttnShape {
   int in_f16, out_f16;
 };
 
-constexpr uint64_t kMaxTokens = 1ull << 31;
+constexpr uint64_t kMaxTokens = 0x7fffffffull;  // launchers take row counts as int
+// Row-per-wavefront kernels (rms_norm, layer_norm, pool_project) launch 64 lanes per row on a
+// 1-D grid, and elementwise kernels round n up to whole 256-lane workgroups in 32-bit arithmetic.
+constexpr uint64_t kMaxWaveRows = (1ull << 26) - 4;
+constexpr uint64_t kMaxElements = (1ull << 32) - 256;
 
 bool attn_shape(Route r, const Params& p, uint64_t threads, uint32_t group, AttnShape* s) {
   const uint64_t H = p.heads, KV = p.kv_heads, S = p.seq, D = p.dim;
@@ -363,15 +370,28 @@ bool validate(Route r, const Params& p, uint64_t threads, uint32_t group, const 
     case R_ATTENTION_F16_NORM_ROPE: {
       AttnShape s;
       if (!attn_shape(r, p, threads, group, &s) || !attn_sizes(s, sz)) return false;
+      const int B = static_cast<int>(s.B), S = static_cast<int>(s.S), H = static_cast<int>(s.H),
+                KV = static_cast<int>(s.KV), D = static_cast<int>(s.D);
+      if (r == R_ATTENTION || r == R_ATTENTION_F16_SCALAR) {
+        if (!tessery::attention_scalar_fits(s.B, s.S, s.H)) return false;
+      } else if (r == R_ATTENTION_F16 || r == R_ATTENTION_F16_NORM_ROPE) {
+        if (!tessery::attention_f16_fits(B, S, H, KV, D)) return false;
+      } else if (!tessery::attention_f32_fits(B, S, H, KV)) {
+        return false;
+      }
       if (r == R_ATTENTION_F16_NORM_ROPE)  // k holds hi and lo planes
-        return sz[1] >= 2 * s.B * s.S * s.KV * s.D * 2 && sz[5] >= s.D * 2 && p.theta > 0.0f &&
-               p.eps >= 0.0f && std::isfinite(p.theta);
+          return sz[1] >= 2 * s.B * s.S * s.KV * s.D * 2 && sz[5] >= s.D * 2 && p.theta > 0.0f &&
+               p.eps >= 0.0f && std::isfinite(p.theta) && tessery::rope_tables_fit(S, D);
       return true;
     }
     case R_NORM_ROPE_F16: {  // buffers: x, gamma, lengths, y; u1 bit 0: y gets hi + lo planes
       const uint64_t heads = p.heads, S = p.seq, D = p.dim, tokens = threads;
       if (group != 256 || !heads || heads > 1024 || !S || tokens % S || tokens > kMaxTokens ||
           (D != 32 && D != 64 && D != 128) || !(p.theta > 0.0f) || !std::isfinite(p.theta))
+        return false;
+      if (!tessery::norm_rope_f16_fits(static_cast<int>(tokens / S), static_cast<int>(S),
+                                       static_cast<int>(heads), static_cast<int>(D)) ||
+          !tessery::rope_tables_fit(static_cast<int>(S), static_cast<int>(D)))
         return false;
       const uint64_t bytes = tokens * heads * D * 2;
       const uint64_t planes = (p.u1 & 1u) ? 2 : 1;
@@ -382,13 +402,14 @@ bool validate(Route r, const Params& p, uint64_t threads, uint32_t group, const 
       const uint64_t cols = p.cols;
       if (group != 32 || threads % 32 || !cols || cols > 65536) return false;
       const uint64_t rows = threads / 32;
-      if (rows > kMaxTokens * 16) return false;
+      if (rows > kMaxWaveRows) return false;
       return sz[0] >= rows * cols * 4 && sz[1] >= cols * 2 && sz[2] >= rows * cols * 4;
     }
     case R_ROPE: {  // kernels.metal:65-74: n threads, n = tokens*heads*dim/2
       const uint64_t n = p.n, D = p.dim;
       if (!n || !D || D % 2 || D > 1024 || !p.heads || !p.seq || n % (D / 2) ||
-          !(p.theta > 0.0f) || !std::isfinite(p.theta))
+          n > kMaxElements || !(p.theta > 0.0f) || !std::isfinite(p.theta) ||
+          !tessery::rope_tables_fit(static_cast<int>(p.seq), static_cast<int>(D)))
         return false;
       return sz[0] >= n * 2 * 4;
     }
@@ -410,6 +431,8 @@ bool validate(Route r, const Params& p, uint64_t threads, uint32_t group, const 
       if (group != 256 || threads != M || !M || M > kMaxTokens || !K || K % 64 || K > 65536 ||
           !nq || nq % 128 || !nkv || nkv % 128 || ntot > 65536)
         return false;
+      const int widths[3] = {static_cast<int>(nq), static_cast<int>(nkv), static_cast<int>(nkv)};
+      if (!tessery::qkv4_f16_fits(static_cast<int>(M), static_cast<int>(K), widths)) return false;
       return sz[0] >= M * K * 2 && sz[1] >= ntot * (K / 8) * 4 && sz[2] >= ntot * (K / 64) * 2 &&
              sz[3] >= ntot * (K / 64) * 2 && sz[4] >= M * nq * 2 && sz[5] >= M * nkv * 2 &&
              sz[6] >= M * nkv * 2;
@@ -448,7 +471,7 @@ bool validate(Route r, const Params& p, uint64_t threads, uint32_t group, const 
       const uint64_t cols = p.cols;
       if (group != 32 || threads % 32 || !cols || cols > 65536) return false;
       const uint64_t rows = threads / 32;
-      if (rows > kMaxTokens) return false;
+      if (rows > kMaxWaveRows) return false;
       return sz[0] >= rows * cols * 4 && sz[1] >= cols * 4 && sz[2] >= cols * 4 &&
              sz[3] >= rows * cols * 4;
     }
@@ -458,7 +481,7 @@ bool validate(Route r, const Params& p, uint64_t threads, uint32_t group, const 
     }
     case R_ADD: {  // kernels.metal:300-304
       const uint64_t n = p.n;
-      return n && sz[0] >= n * 4 && sz[1] >= n * 4 && sz[2] >= n * 4;
+      return n && n <= kMaxElements && sz[0] >= n * 4 && sz[1] >= n * 4 && sz[2] >= n * 4;
     }
     case R_EMBEDDING4: {  // kernels.metal:21-30: ids, w, scales, biases, out; n = tokens*cols
       const uint64_t n = p.n, cols = p.cols;
@@ -482,7 +505,7 @@ bool validate(Route r, const Params& p, uint64_t threads, uint32_t group, const 
       if (group != 32 || !threads || threads % 32 || !cols || !seq || !dim || dim > cols)
         return false;
       const uint64_t batch = threads / 32;
-      if (batch > kMaxTokens) return false;
+      if (batch > kMaxWaveRows) return false;
       return sz[0] >= batch * seq * cols * 4 && (p.u1 || sz[1] >= batch * 4) &&
              sz[2] >= batch * dim * 4;
     }
@@ -501,28 +524,21 @@ uint32_t float_bits(float f) {
   return u;
 }
 
-// cos/sin[pos][c] = cos/sin(pos * theta^(-2c/D)), evaluated in float64 and rounded once.
+// cos/sin[pos][c] = cos/sin(pos * theta^(-2c/D)), evaluated in float64 and rounded once, by a
+// kernel on the runtime stream: queued launches of the open command run after it.
 bool ensure_rope(Runtime* rt, uint32_t seq, uint32_t dim, float theta) {
   const auto key = std::make_tuple(seq, dim, float_bits(theta));
   if (rt->rope.count(key)) return true;
-  const uint32_t half = dim / 2;
-  std::vector<float> c(static_cast<size_t>(seq) * half), s(c.size());
-  for (uint32_t pos = 0; pos < seq; ++pos)
-    for (uint32_t j = 0; j < half; ++j) {
-      const double angle =
-          static_cast<double>(pos) * std::pow(static_cast<double>(theta), -2.0 * j / dim);
-      c[static_cast<size_t>(pos) * half + j] = static_cast<float>(std::cos(angle));
-      s[static_cast<size_t>(pos) * half + j] = static_cast<float>(std::sin(angle));
-    }
+  const size_t bytes = static_cast<size_t>(seq) * (dim / 2) * sizeof(float);
   RopeTable t{nullptr, nullptr};
-  const size_t bytes = c.size() * sizeof(float);
   if (hipMalloc(&t.cos, bytes) != hipSuccess) return false;
   if (hipMalloc(&t.sin, bytes) != hipSuccess) {
     (void)hipFree(t.cos);
     return false;
   }
-  if (hipMemcpy(t.cos, c.data(), bytes, hipMemcpyHostToDevice) != hipSuccess ||
-      hipMemcpy(t.sin, s.data(), bytes, hipMemcpyHostToDevice) != hipSuccess) {
+  if (tessery::launch_rope_tables(t.cos, t.sin, static_cast<int>(seq), static_cast<int>(dim),
+                                  theta, rt->stream) != hipSuccess) {
+    (void)hipStreamSynchronize(rt->stream);
     (void)hipFree(t.cos);
     (void)hipFree(t.sin);
     return false;
@@ -761,6 +777,15 @@ void release_profile_events(Runtime* rt) {
   rt->prof_events.clear();
 }
 
+// Frees the allocations of buffers released during the last command, once nothing launched on
+// the stream can still use them.
+void release_pending(Runtime* rt) {
+  if (rt->pending_free.empty()) return;
+  (void)hipStreamSynchronize(rt->stream);
+  for (void* p : rt->pending_free) (void)hipFree(p);
+  rt->pending_free.clear();
+}
+
 }  // namespace
 
 extern "C" {
@@ -792,6 +817,7 @@ void mi_destroy(void* runtime) {
   if (!rt) return;
   (void)hipSetDevice(rt->device);
   if (rt->stream) (void)hipStreamSynchronize(rt->stream);
+  for (void* p : rt->pending_free) (void)hipFree(p);
   for (auto& kv : rt->rope) {
     (void)hipFree(kv.second.cos);
     (void)hipFree(kv.second.sin);
@@ -822,9 +848,16 @@ void* mi_buffer(void* runtime, const void* bytes, uint64_t size) {
 void mi_free(void* buffer) {
   auto b = static_cast<Buffer*>(buffer);
   if (!b) return;
-  (void)hipSetDevice(b->owner->device);
-  (void)hipStreamSynchronize(b->owner->stream);
-  (void)hipFree(b->ptr);
+  Runtime* rt = b->owner;
+  if (rt->recording) {
+    // the open command may have queued launches (or a plan replay) that use this memory: keep
+    // it until mi_finish / mi_abort
+    rt->pending_free.push_back(b->ptr);
+  } else {
+    (void)hipSetDevice(rt->device);
+    (void)hipStreamSynchronize(rt->stream);
+    (void)hipFree(b->ptr);
+  }
   delete b;
 }
 
@@ -1062,6 +1095,7 @@ int mi_finish(void* runtime) {
   rt->ops.clear();
   rt->segments.clear();
   rt->recording = false;
+  release_pending(rt);
   return failed;
 }
 
@@ -1076,6 +1110,8 @@ void mi_abort(void* runtime) {
   rt->ops.clear();  // queued work was never launched
   rt->segments.clear();
   rt->recording = false;
+  (void)hipSetDevice(rt->device);
+  release_pending(rt);
 }
 
 int mi_profile_enable(void* runtime, int enabled) {

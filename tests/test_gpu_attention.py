@@ -2,8 +2,11 @@
 oracle on identical seeded inputs.
 
 fp32 routes use tessery's own tolerance (atol 2e-6, rtol 2e-5, test_kernels.py:157) and must
-also stay within max-abs 1e-4. fp16-operand routes (fp32 accumulation) use max-abs 2e-3 against
-the oracle evaluated in float64 on the same fp16 inputs; masked / padded / GQA index mapping is
+also stay within max-abs 1e-4. The plain fp16-operand route (fp32 accumulation) and every fp16
+output use max-abs 2e-3 against the oracle evaluated in float64 on the same fp16 inputs. The fused
+norm + RoPE route with fp32 output carries q, k and P as hi + lo fp16 pairs (about 22 bits) and is
+held to the fp32 bar, max-abs 1e-4 (it measures about 1.5e-6): losing one of the splits measures
+5.6e-4 or more and fails it. Masked / padded / GQA index mapping is
 exercised by ragged lengths, padded query rows, head groups of 1, 2 and 4, and sentinel bytes
 around the output."""
 
@@ -19,6 +22,11 @@ pytestmark = pytest.mark.gpu
 
 F32_ATOL, F32_RTOL, F32_MAX = 2e-6, 2e-5, 1e-4
 F16_MAX = 2e-3
+FUSED_F32_MAX = 1e-4  # attention_f16_norm_rope with fp32 output
+
+
+def fused_bar(out_dtype):
+    return FUSED_F32_MAX if out_dtype == "f32" else F16_MAX
 
 
 def run(engine, kernel, inputs, shape, out_dtype=np.float32, **params):
@@ -254,7 +262,8 @@ def test_qwen_norm_rope_fixture(runtime, out_dtype):
     t = {name: f[name] for name in ("q", "k", "v", "q_norm", "k_norm")}
     shape = workloads.Shape(2, 40, 4, 2, 128, causal=True)
     out, planes = norm_rope_attend(runtime, t, f["lengths"], shape, out_dtype)
-    assert np.max(np.abs(out.astype(np.float64) - f["expected"])) <= F16_MAX
+    err = np.max(np.abs(out.astype(np.float64) - f["expected"]))
+    assert err <= fused_bar(out_dtype), err
     # the k prologue writes valid rows only: hi within fp16 rounding of the float64 value, and
     # hi + lo within fp32 rounding of it
     hi, lo = planes[0].astype(np.float64), planes[1].astype(np.float64)
@@ -271,7 +280,7 @@ def test_qwen3_8x512(runtime, out_dtype):
     out, _ = norm_rope_attend(runtime, t, lengths, shape, out_dtype)
     _, expected = oracle_norm_rope(t, lengths)
     err = np.max(np.abs(out.astype(np.float64) - expected))
-    assert err <= F16_MAX, err
+    assert err <= fused_bar(out_dtype), err
 
 
 @pytest.mark.parametrize("layer", [0, 27])
@@ -282,4 +291,22 @@ def test_qwen3_32x512(runtime, layer):
     out, _ = norm_rope_attend(runtime, t, lengths, shape, "f32")
     _, expected = oracle_norm_rope(t, lengths)
     err = np.max(np.abs(out.astype(np.float64) - expected))
-    assert err <= F16_MAX, err
+    assert err <= FUSED_F32_MAX, err
+
+
+@pytest.mark.parametrize("route", ["fused", "plain"])
+def test_f16_routes_are_deterministic(runtime, route):
+    """The same launch on the same inputs gives the same bits. Full tiles skip the causal masking,
+    so their row max reads the QK^T accumulators right after the MFMA chain; this pins that the
+    read waits for the chain to finish (it once depended on timing)."""
+    shape = workloads.Shape(4, 256, 16, 8, 128, causal=True)
+    lengths = np.array([256, 200, 64, 17], np.uint32)
+    if route == "fused":
+        t = workloads.qwen_layer(shape, 0, seed=12)
+        first, _ = norm_rope_attend(runtime, t, lengths, shape, "f32")
+        second, _ = norm_rope_attend(runtime, t, lengths, shape, "f32")
+    else:
+        q, k, v = f16_inputs(12, 4, 256, 16, 8, 128)
+        first = attend(runtime, q, k, v, lengths, bidirectional=False, precision="f16")
+        second = attend(runtime, q, k, v, lengths, bidirectional=False, precision="f16")
+    np.testing.assert_array_equal(first, second)

@@ -257,3 +257,62 @@ def test_model_end_routes_reject_bad_launches(runtime, case):
     finally:
         for b in bufs:
             b.close()
+
+
+def test_buffers_closed_inside_a_command_live_until_it_finishes(runtime):
+    """Closing a buffer while a command is open frees nothing yet: the queued launch still reads
+    and writes it at finish, and the memory is released afterwards (runtime.mm keeps encoded
+    buffers alive the same way)."""
+    rng = np.random.default_rng(21)
+    a = rng.normal(size=4096).astype(np.float32)
+    b = rng.normal(size=4096).astype(np.float32)
+    out = runtime.buffer(a.nbytes)
+    try:
+        with runtime.command():
+            x, y = runtime.upload(a), runtime.upload(b)
+            runtime._dispatch("add", [x, y, out], threads=a.size, n=a.size)
+            x.close()
+            y.close()
+            # a new allocation made while the closed ones are pending must not reuse their memory
+            z = runtime.upload(np.zeros_like(a))
+            runtime._dispatch("add", [z, z, z], threads=a.size, n=a.size)
+        np.testing.assert_array_equal(runtime.read(out, a.shape), a + b)
+        np.testing.assert_array_equal(runtime.read(z, a.shape), 0.0)
+        z.close()
+    finally:
+        out.close()
+    assert runtime.active_bytes == 0
+
+
+@pytest.mark.parametrize("case", ["qkv4_k", "norm_rope_heads", "rms_norm_rows"])
+def test_launcher_limits_are_rejected_at_dispatch(runtime, case):
+    """Shapes whose buffers fit but which a launcher cannot run (qkv4_f16 beyond K = 8192, the
+    k prologue beyond 256 lanes per position, row kernels beyond 2^26 - 4 rows) are refused by
+    mi_dispatch, before anything is queued, not at finish."""
+    bufs = []
+    try:
+        if case == "qkv4_k":
+            m, k, nq, nkv = 128, 16384, 128, 128
+            n = nq + 2 * nkv
+            bufs += [runtime.buffer(m * k * 2), runtime.buffer(n * (k // 8) * 4),
+                     runtime.buffer(n * (k // 64) * 2), runtime.buffer(n * (k // 64) * 2),
+                     runtime.buffer(m * nq * 2), runtime.buffer(m * nkv * 2),
+                     runtime.buffer(m * nkv * 2)]
+            with pytest.raises(InferenceError), runtime.command():
+                runtime._qkv4(bufs, rows=m, k=k, q_cols=nq, kv_cols=nkv, scale_dtype="f16")
+        elif case == "norm_rope_heads":
+            b, s, heads, d = 1, 16, 33, 128
+            bufs += [runtime.buffer(b * s * heads * d * 2), runtime.buffer(d * 2),
+                     runtime.buffer(b * 4), runtime.buffer(2 * b * s * heads * d * 2)]
+            with pytest.raises(InferenceError), runtime.command():
+                runtime._dispatch("norm_rope_f16", bufs, threads=b * s, group_size=256,
+                                  heads=heads, seq=s, dim=d, flags=1)
+        else:
+            rows = (1 << 26) - 3
+            bufs += [runtime.buffer(rows * 4), runtime.buffer(2), runtime.buffer(rows * 4)]
+            with pytest.raises(InferenceError), runtime.command():
+                runtime._dispatch("rms_norm", bufs, threads=rows * 32, group_size=32, cols=1)
+        assert runtime.diagnostics()["completed_commands"] == 0
+    finally:
+        for b in bufs:
+            b.close()
