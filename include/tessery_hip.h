@@ -85,6 +85,27 @@ int mi_graph_counts(void *runtime, uint64_t *launches, uint64_t *builds);
  * host bytes into an existing device buffer, synchronously. */
 int mi_write(void *buffer, const void *bytes, uint64_t size);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops and harnesses that forbid hipMalloc): the fused Qwen3
+ * attention of the attention_f16_norm_rope route (per-head q/k RMSNorm + RoPE, causal or
+ * bidirectional GQA on fp16 operands with fp32 accumulation) on plain device pointers, launched
+ * on `stream` (NULL: the default stream), with no allocation of any kind. q_pre [B,S,H,D] and
+ * k_pre, v [B,S,KV,D] are fp16, lengths u32 [B], q_norm / k_norm bf16 [D], out [B,S,H,D] fp32 or
+ * (out_f16 = 1) fp16; D is 64 or 128, H % KV == 0. The RoPE tables and the normalized k planes
+ * live in a static device array of MI_NOALLOC_SCRATCH_BYTES per GPU, held until the process
+ * ends: 2 * S * D/2 * 4 bytes of tables (<= 2 MiB) and 2 * B*S*KV*D * 2 bytes of k planes
+ * (<= 64 MiB, e.g. 16384 tokens at KV * D = 1024). Every call on one GPU shares that array, so
+ * calls that overlap on one GPU (other streams or threads) race; calls on one stream are ordered.
+ * Returns 0 when the launches were queued, 2 when the shape needs more than the scratch holds,
+ * 1 for any other invalid argument or launch error (nothing is launched for 1 or 2 found
+ * before the first launch). */
+#define MI_NOALLOC_SCRATCH_BYTES ((uint64_t)66 << 20)
+int mi_attention_norm_rope_noalloc(const void *q_pre, const void *k_pre, const void *v,
+                                   const uint32_t *lengths, void *out, const uint16_t *q_norm,
+                                   const uint16_t *k_norm, uint32_t batch, uint32_t seq,
+                                   uint32_t heads, uint32_t kv_heads, uint32_t dim, float eps,
+                                   float theta, int bidirectional, int out_f16, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,7 +20,7 @@ BUILD = PACKAGE / "_build"
 LIBRARY = PACKAGE / "libtessery_hip.so"
 
 SOURCES = ("attention.hip", "norm_rope.hip", "linear4.hip", "qkv4.hip", "dense.hip", "model.hip",
-           "util.hip", "runtime.cpp")
+           "util.hip", "noalloc.hip", "runtime.cpp")
 
 # Per-source flags. The attention kernels never produce NaN from finite inputs (masked scores are
 # -inf, every row has a finite maximum), so max() needs no NaN quieting.
