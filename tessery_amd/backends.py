@@ -200,9 +200,12 @@ class Qwen3Backend:
             rt._dispatch("add", [x, y, x], threads=tokens * self.hidden, n=tokens * self.hidden)
 
         with rt._workspace() as new:
+            # ids and lengths go into reusable workspace buffers, so a repeated shape binds the
+            # same device pointers and its plan replays through the cached graph
+            id_buf, len_buf = new(ids.nbytes), new(lengths.nbytes)
+            rt.write(id_buf, ids)
+            rt.write(len_buf, lengths)
             with rt.command():
-                id_buf = new(ids.nbytes, np.ascontiguousarray(ids))
-                len_buf = new(lengths.nbytes, np.ascontiguousarray(lengths))
                 x, normalized, projected = (new(tokens * self.hidden * 4) for _ in range(3))
                 q, attended = (new(tokens * q_width * 4) for _ in range(2))
                 k, v = (new(tokens * kv_width * 4) for _ in range(2))
@@ -366,9 +369,10 @@ class BertBackend:
             rt._dispatch("add", [x, y, x], threads=tokens * self.hidden, n=tokens * self.hidden)
 
         with rt._workspace() as new:
+            id_buf, len_buf = new(ids.nbytes), new(lengths.nbytes)  # reusable: stable bindings
+            rt.write(id_buf, ids)
+            rt.write(len_buf, lengths)
             with rt.command():
-                id_buf = new(ids.nbytes, np.ascontiguousarray(ids))
-                len_buf = new(lengths.nbytes, np.ascontiguousarray(lengths))
                 x, projected, q, k, v, attended = (new(tokens * self.hidden * 4) for _ in range(6))
                 activated = new(tokens * self.intermediate * 4)
                 output = new(batch * dimensions * 4)

@@ -95,7 +95,10 @@ def test_qwen3_backend_forward(tmp_path, shape, batch, seq, dims):
         np.testing.assert_allclose(first, want, atol=1e-4, rtol=0)
         again = backend.forward(ids, lengths, dimensions=dims)  # plan replay
         np.testing.assert_array_equal(again, first)
-        assert backend.runtime.diagnostics()["graph_builds"] >= 1
+        third = backend.forward(ids, lengths, dimensions=dims)  # same binding: same graph
+        np.testing.assert_array_equal(third, first)
+        diag = backend.runtime.diagnostics()
+        assert (diag["graph_builds"], diag["graph_launches"]) == (1, 2), diag
         with pytest.raises(InferenceError):
             backend.forward(ids + np.uint32(shape["vocab"]), lengths, dimensions=dims)
         with pytest.raises(InferenceError):
@@ -119,6 +122,10 @@ def test_bert_backend_forward(tmp_path, shape, batch, seq):
         np.testing.assert_allclose(first, want, atol=1e-4, rtol=0)
         again = backend.forward(ids, lengths, dimensions=shape["hidden"])
         np.testing.assert_array_equal(again, first)
+        third = backend.forward(ids, lengths, dimensions=shape["hidden"])
+        np.testing.assert_array_equal(third, first)
+        diag = backend.runtime.diagnostics()
+        assert (diag["graph_builds"], diag["graph_launches"]) == (1, 2), diag
         with pytest.raises(InferenceError):
             backend.forward(ids, lengths, dimensions=shape["hidden"] - 1)
     finally:

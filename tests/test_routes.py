@@ -2,6 +2,8 @@
 tessery's tests/unit/test_runtime_loading.py:9-106."""
 
 import json
+
+import numpy as np
 from types import SimpleNamespace
 
 import pytest
@@ -166,3 +168,42 @@ def test_bge_affine_guarded_dispatch(rows, cols, k):
         assert all(c[0][1] == buffers for c in calls)
         if rows % 8:
             assert calls[-1][1]["n"] == rows // 8 * 8
+
+
+def launch_rows(launch, rows, cols):
+    """Rows a launch covers, from its thread count (the row regions mi_dispatch derives,
+    kernels.metal:32-51, 489-605, 655-684, 733-773, 306-322, 396-487)."""
+    n = launch.fields.get("n", 0)
+    if launch.name in ("linear4", "matmul_f32", "matmul_bias_f32"):
+        return n, min(n + 4 * (launch.threads // (cols * 32)), rows)
+    if launch.name in ("linear4_tiled", "matmul_f32_chunk32", "matmul_bias_f32_chunk32",
+                       "matmul_f32_tiled"):
+        return n, n + 8 * (launch.threads // ((cols // 32) * 128))
+    if launch.name == "linear4_tail":
+        return n, min(n + 8, rows)
+    if launch.name in ("linear4_16x32_k64", "linear4_32x32_k64"):
+        tile = 16 if "16x32" in launch.name else 32
+        return 0, tile * (launch.threads // ((cols // 32) * 256))
+    assert launch.name == "linear4_small3"
+    return 0, 3
+
+
+@pytest.mark.parametrize("cols,k", [(1024, 1024), (2048, 1024), (3072, 1024), (1024, 3072),
+                                    (64, 128), (96, 64), (1025, 1024), (384, 384), (385, 384),
+                                    (1536, 384), (384, 1536), (384, 2048)])
+def test_planners_cover_every_row_once(cols, k):
+    """linear4_plan and the dense planners cover rows [0, rows) exactly once at every height."""
+    from tessery_amd.runtime import linear4_plan, matmul_bias_plan, matmul_plan
+
+    for rows in range(1, 600):
+        plans = [linear4_plan(rows=rows, cols=cols, k=k), matmul_plan(rows=rows, cols=cols, k=k)]
+        bias = matmul_bias_plan(rows=rows, cols=cols, k=k)
+        if bias is not None:
+            plans.append(bias)
+        for plan in plans:
+            covered = np.zeros(rows, int)
+            for launch in plan:
+                start, end = launch_rows(launch, rows, cols)
+                assert 0 <= start < end <= rows, (launch, rows)
+                covered[start:end] += 1
+            assert (covered == 1).all(), (rows, cols, k, plan)
