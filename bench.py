@@ -8,10 +8,15 @@ attention launch (q norm+RoPE inside), through the C ABI (HipRuntime -> mi_dispa
 
 It prints one JSON line: tokens/s (execution tokens B*S*layers per second), mask-exact TFLOP/s and
 its fraction of the fp16 MFMA peak, the HBM roofline of the attention kernel from live per-launch
-HIP-event timings, and the float64 NumPy CPU oracle timed on the host on a bounded sample.
+HIP-event timings, and the NumPy CPU oracle timed on the host on a bounded sample (float64 on all
+cores, plus float32 and a one-thread float64 run). Layer 0 is checked against the float64 oracle
+(max-abs <= 1e-4 with fp32 output; the exit status is 1 otherwise). A `secondary` object carries
+kernel times and roofline fractions of the other configurations measured in the same run:
+bge_32x512, qwen3_8x512, qwen_qkv4_16x256 and the headline shape at full length with fp16 output.
 
 --workload selects one of the other measured configurations instead (one JSON line each):
   qwen3_8x512       B=8, S=512, lengths U{64..512} (seed 3), same fused path, 8 layers
+  qwen3_8x512_f32   the same shape on the fp32 route (attention_tiled, D=128), 8 layers
   bge_32x512        BGE-small fp32 bidirectional attention, B=32, S=512, 12 heads x 32,
                     lengths U{2..512} (seed 2), 12 layers, route attention_tiled
   qwen_qkv4_16x256  uint4 QKV projection (x [4096,1024] fp16) -> k norm+RoPE -> fused attention,
@@ -48,6 +53,9 @@ PEAK_F16_TFLOPS = 2516.6
 PEAK_F32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 LAYERS = 28
+# max-abs parity bars of the fused route against the float64 oracle, layer 0
+PARITY_F32_OUT = 1e-4
+PARITY_F16_OUT = 2e-3
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of the attention kernel on this workload, with the
 # copy-kernel calibration of each counter; valid for the kernel source it names
 TRAFFIC_FILE = ROOT / "profiles" / "attention_f16_norm_rope_qwen3_32x512_traffic.txt"
@@ -133,7 +141,8 @@ def run_timed(rt: HipRuntime, step: Callable[[], None], steps: int, warmup: int,
     }
 
 
-def upload_qwen_layers(rt: HipRuntime, shape: workloads.Shape, layers: int, seed: int):
+def upload_qwen_layers(rt: HipRuntime, shape: workloads.Shape, layers: int, seed: int,
+                       out_bytes: int = 4):
     sets = []
     for layer in range(layers):
         t = workloads.qwen_layer(shape, layer, seed=seed)
@@ -144,7 +153,7 @@ def upload_qwen_layers(rt: HipRuntime, shape: workloads.Shape, layers: int, seed
                 "v": rt.upload(t["v"]),
                 "q_norm": rt.upload(t["q_norm"]),
                 "k_norm": rt.upload(t["k_norm"]),
-                "out": rt.buffer(t["q"].size * 4),
+                "out": rt.buffer(t["q"].size * out_bytes),
             }
         )
         if layer == 0:
@@ -152,7 +161,7 @@ def upload_qwen_layers(rt: HipRuntime, shape: workloads.Shape, layers: int, seed
     return sets, host0
 
 
-def fused_attention(rt, shape, s, lengths_buf, k_work):
+def fused_attention(rt, shape, s, lengths_buf, k_work, out_dtype="f32"):
     rt._attention_norm_rope(
         [s["q"], s["k"], s["v"], lengths_buf, s["out"], s["q_norm"], s["k_norm"], k_work],
         tokens=shape.tokens,
@@ -162,23 +171,48 @@ def fused_attention(rt, shape, s, lengths_buf, k_work):
         dim=shape.dim,
         eps=workloads.EPS,
         theta=workloads.THETA,
-        out_dtype="f32",
+        out_dtype=out_dtype,
     )
 
 
-def qwen_cpu_layer(shape, lengths, host0):
-    """float64 NumPy oracle of one layer: q/k norm + RoPE, then attention."""
+def qwen_cpu_layer(shape, lengths, host0, dtype=np.float64, rows=None):
+    """NumPy oracle of one layer (float64: the reference formulation; float32: a timing variant):
+    q/k norm + RoPE, then attention, over all batch rows or the first `rows`."""
     from oracle import attention, norm_rope
 
     qn = workloads.bf16_values(host0["q_norm"]).astype(np.float64)
     kn = workloads.bf16_values(host0["k_norm"]).astype(np.float64)
+    rows = shape.batch if rows is None else rows
+    q_in, k_in, v_in = (host0[name][:rows] for name in ("q", "k", "v"))
 
     def layer():
-        q = norm_rope.norm_rope(host0["q"], qn, workloads.EPS, workloads.THETA)
-        k = norm_rope.norm_rope(host0["k"], kn, workloads.EPS, workloads.THETA)
-        return attention.attention(q, k, host0["v"], lengths, bidirectional=False)
+        q = norm_rope.norm_rope(q_in, qn, workloads.EPS, workloads.THETA, dtype)
+        k = norm_rope.norm_rope(k_in, kn, workloads.EPS, workloads.THETA, dtype)
+        return attention.attention(q, k, v_in, lengths[:rows], bidirectional=False, dtype=dtype)
 
     return layer
+
+
+def qwen_cpu_baselines(shape, lengths, host0, layers: int) -> tuple[np.ndarray, dict]:
+    """The CPU oracle timed on the host: float64 on every available core (the reported value, and
+    the parity reference of layer 0), plus a float32 run on the same cores and a float64 run on
+    one thread over a quarter of the batch rows, scaled to tokens/s of the whole layer."""
+    from threadpoolctl import threadpool_limits
+
+    expected, per_layer, runs = time_cpu(qwen_cpu_layer(shape, lengths, host0))
+    line = cpu_baseline_line(shape, per_layer, runs, layers, " incl. q/k norm+RoPE")
+    _, per32, runs32 = time_cpu(qwen_cpu_layer(shape, lengths, host0, np.float32), budget_s=6.0)
+    rows = max(1, shape.batch // 4)
+    with threadpool_limits(limits=1):
+        _, per1, runs1 = time_cpu(qwen_cpu_layer(shape, lengths, host0, rows=rows), budget_s=8.0)
+    # tokens/s of the sampled rows: per-row work differs, so the sample's own tokens count
+    line["variants"] = [
+        {"dtype": "f32", "threads": line["blas_threads"], "value": shape.tokens / per32,
+         "unit": "tokens/s", "sample": f"1 layer, all rows, median of {runs32}"},
+        {"dtype": "f64", "threads": 1, "value": rows * shape.seq / per1, "unit": "tokens/s",
+         "sample": f"1 layer, batch rows 0..{rows - 1} of {shape.batch}, median of {runs1}"},
+    ]
+    return expected, line
 
 
 def cpu_baseline_line(shape, per_layer: float, runs: int, layers: int, what: str) -> dict:
@@ -194,13 +228,14 @@ def cpu_baseline_line(shape, per_layer: float, runs: int, layers: int, what: str
 
 
 def bench_qwen(args, name: str, shape, lengths, seed: int, layers: int, lengths_text: str,
-               headline: bool) -> dict:
+               headline: bool, out_dtype: str = "f32") -> dict:
+    out_bytes = 2 if out_dtype == "f16" else 4
     flop = workloads.attention_flop(shape, lengths)
-    nbytes = workloads.attention_bytes(shape, lengths, 2, 4)
+    nbytes = workloads.attention_bytes(shape, lengths, 2, out_bytes)
     log(f"workload {name}: B={shape.batch} S={shape.seq} sumL={int(lengths.sum())} "
-        f"layers={layers}; generating inputs")
+        f"layers={layers} out={out_dtype}; generating inputs")
     with HipRuntime() as rt:
-        sets, host0 = upload_qwen_layers(rt, shape, layers, seed)
+        sets, host0 = upload_qwen_layers(rt, shape, layers, seed, out_bytes)
         lengths_buf = rt.upload(lengths)
         k_work = rt.buffer(2 * host0["k"].nbytes)
         if args.calibrate_copy_mib:
@@ -214,10 +249,10 @@ def bench_qwen(args, name: str, shape, lengths, seed: int, layers: int, lengths_
 
         def step():
             for s in sets:
-                fused_attention(rt, shape, s, lengths_buf, k_work)
+                fused_attention(rt, shape, s, lengths_buf, k_work, out_dtype)
 
         t = run_timed(rt, step, args.steps, args.warmup, 2 * layers)
-        out0 = rt.read(sets[0]["out"], host0["q"].shape)
+        out0 = rt.read(sets[0]["out"], host0["q"].shape, np.float16 if out_bytes == 2 else np.float32)
 
     step_s = t["step"]
     attn_avg = t["kernel_s"]["attention_f16_norm_rope"]
@@ -246,7 +281,7 @@ def bench_qwen(args, name: str, shape, lengths, seed: int, layers: int, lengths_
             "layers": layers,
             "valid_tokens": int(lengths.sum()),
             "lengths": lengths_text,
-            "out_dtype": "f32",
+            "out_dtype": out_dtype,
         },
         "valid_tokens_per_s": int(lengths.sum()) * layers / step_s,
         "tflops": tflops,
@@ -269,18 +304,19 @@ def bench_qwen(args, name: str, shape, lengths, seed: int, layers: int, lengths_
     }
     if not args.no_cpu_baseline:
         log("cpu baseline")
-        expected, per_layer, runs = time_cpu(qwen_cpu_layer(shape, lengths, host0))
-        result["cpu_baseline"] = cpu_baseline_line(shape, per_layer, runs, layers,
-                                                   " incl. q/k norm+RoPE")
-        result["max_abs_err_layer0"] = float(np.max(np.abs(out0.astype(np.float64) - expected)))
+        expected, result["cpu_baseline"] = qwen_cpu_baselines(shape, lengths, host0, layers)
+        err = float(np.max(np.abs(out0.astype(np.float64) - expected)))
+        result["max_abs_err_layer0"] = err
+        # the fused route carries q, k and P at ~22 bits: held to the fp32 bar with fp32 output
+        bar = PARITY_F32_OUT if out_dtype == "f32" else PARITY_F16_OUT
+        result["parity"] = {"max_abs": err, "bar": bar, "ok": err <= bar}
     else:
         result["cpu_baseline"] = None
     return result
 
 
-def bench_bge(args) -> dict:
+def bench_bge(args, layers: int = 12) -> dict:
     """BGE-small fp32 bidirectional attention (route attention_tiled), 12 layers."""
-    layers = 12
     shape, lengths = workloads.bge_small_32x512()
     flop = workloads.attention_flop(shape, lengths)
     nbytes = workloads.attention_bytes(shape, lengths, 4, 4)
@@ -350,9 +386,79 @@ def bench_bge(args) -> dict:
     return result
 
 
-def bench_qkv4_block(args) -> dict:
+def bench_qwen_f32(args, layers: int = 8) -> dict:
+    """The fp32 route at the Qwen3 8x512 shape (route attention_tiled, D = 128: the reference's own
+    precision, used by the fp32 Qwen3 backend): q/k normalized and rotated on the host in
+    float64 and rounded to fp32, v N(0,1), lengths U{64..512} (seed 3), 8 layers."""
+    from oracle import norm_rope
+
+    shape, lengths = workloads.qwen3_8x512()
+    flop = workloads.attention_flop(shape, lengths)
+    nbytes = workloads.attention_bytes(shape, lengths, 4, 4)
+    log(f"workload qwen3_8x512_f32: B={shape.batch} S={shape.seq} sumL={int(lengths.sum())}")
+    with HipRuntime() as rt:
+        sets, host0 = [], None
+        for layer in range(layers):
+            t = workloads.qwen_layer(shape, layer, seed=3)
+            qn = workloads.bf16_values(t["q_norm"]).astype(np.float64)
+            kn = workloads.bf16_values(t["k_norm"]).astype(np.float64)
+            host = {"q": norm_rope.norm_rope(t["q"], qn, workloads.EPS, workloads.THETA),
+                    "k": norm_rope.norm_rope(t["k"], kn, workloads.EPS, workloads.THETA),
+                    "v": t["v"]}
+            host = {k: v.astype(np.float32) for k, v in host.items()}
+            host0 = host0 or host
+            s = {k: rt.upload(v) for k, v in host.items()}
+            s["out"] = rt.buffer(host["q"].nbytes)
+            sets.append(s)
+        lengths_buf = rt.upload(lengths)
+
+        def step():
+            for s in sets:
+                rt._attention([s["q"], s["k"], s["v"], lengths_buf, s["out"]], tokens=shape.tokens,
+                              seq=shape.seq, heads=shape.heads, kv_heads=shape.kv_heads,
+                              dim=shape.dim)
+
+        t = run_timed(rt, step, args.steps, args.warmup, layers)
+        out0 = rt.read(sets[0]["out"], host0["q"].shape)
+    step_s = t["step"]
+    (kernel, avg), = t["kernel_s"].items()
+    tflops = flop / avg / 1e12
+    result = {
+        "metric": "prefill attention tokens/s, Qwen3 GQA 8x512, fp32 route, 1 GPU",
+        "value": shape.tokens * layers / step_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_s * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "qwen3_8x512 causal GQA attention on the fp32 route (q/k normed)",
+                   "batch": shape.batch, "seq": shape.seq, "heads": shape.heads,
+                   "kv_heads": shape.kv_heads, "dim": shape.dim, "layers": layers,
+                   "valid_tokens": int(lengths.sum()), "lengths": "uniform [64,512], seed 3"},
+        "kernel_us": {kernel: avg * 1e6},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_F32_TFLOPS,
+                     "unit": "TFLOP/s", "frac": tflops / PEAK_F32_TFLOPS, "traffic": None,
+                     "algorithmic_flop": flop, "algorithmic_bytes": nbytes,
+                     "hbm_gbs": nbytes / avg / 1e9, "kernel": kernel},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        from oracle import attention
+
+        expected = attention.attention(host0["q"], host0["k"], host0["v"], lengths,
+                                       bidirectional=False)
+        err = float(np.max(np.abs(out0.astype(np.float64) - expected)))
+        result["parity"] = {"max_abs": err, "bar": PARITY_F32_OUT, "ok": err <= PARITY_F32_OUT}
+    return result
+
+
+def bench_qkv4_block(args, layers: int = 8) -> dict:
     """uint4 QKV projection -> k norm+RoPE -> fused attention, 8 independent layers."""
-    layers = 8
     shape, lengths, d = workloads.qwen_qkv4_16x256()
     m, k_in = d["x"].shape
     nq, nkv = shape.heads * shape.dim, shape.kv_heads * shape.dim
@@ -865,6 +971,39 @@ def bench_model(args, arch: str) -> dict:
     return result
 
 
+def _kernel_summary(result: dict, peak_tflops: float) -> dict:
+    roof = result["roofline"]
+    summary = {
+        "config": result["config"],
+        "ms_per_step": result["ms_per_step"],
+        "kernel_us": result["kernel_us"],
+        "roofline": {key: roof[key] for key in ("kernel", "bound", "achieved", "peak", "unit",
+                                                "frac")},
+    }
+    if "mfma_tflops" in roof:  # attention kernels on an HBM roof: their MFMA share as well
+        summary["mfma_frac"] = roof["mfma_tflops"] / peak_tflops
+    return summary
+
+
+def secondary_measurements(args) -> dict:
+    """Kernel times and roofline fractions of the other configurations, measured in the same run
+    (2 warmup and 5 timed steps each, no CPU leg): BGE-small 32x512 fp32 attention (4 layers),
+    Qwen3 8x512 fused attention (8 layers), the uint4 QKV block 16x256 (8 layers), and the
+    headline shape at full length (32 x 512, every length 512, fp16 output, 4 layers)."""
+    sub = argparse.Namespace(steps=5, warmup=2, no_cpu_baseline=True, calibrate_copy_mib=0)
+    out = {"bge_32x512": _kernel_summary(bench_bge(sub, layers=4), PEAK_F32_TFLOPS)}
+    shape, lengths = workloads.qwen3_8x512()
+    out["qwen3_8x512"] = _kernel_summary(
+        bench_qwen(sub, "qwen3_8x512", shape, lengths, 3, 8, "uniform [64,512], seed 3",
+                   headline=False), PEAK_F16_TFLOPS)
+    out["qwen_qkv4_16x256"] = _kernel_summary(bench_qkv4_block(sub, layers=8), PEAK_F16_TFLOPS)
+    full = workloads.Shape(32, 512, 16, 8, 128, causal=True)
+    out["qwen3_32x512_full_f16out"] = _kernel_summary(
+        bench_qwen(sub, "qwen3_32x512_full", full, np.full(32, 512, np.uint32), 4, 4,
+                   "all 512", headline=False, out_dtype="f16"), PEAK_F16_TFLOPS)
+    return out
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__,
                                      formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -873,10 +1012,13 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--layers", type=int, default=LAYERS, help="headline workload only")
     parser.add_argument("--workload", default="qwen3_32x512",
-                        choices=["qwen3_32x512", "qwen3_8x512", "bge_32x512", "qwen_qkv4_16x256",
+                        choices=["qwen3_32x512", "qwen3_8x512", "qwen3_8x512_f32", "bge_32x512",
+                                 "qwen_qkv4_16x256",
                                  "qwen_tail_16x256", "qwen_tail_1x128", "bge_layer_32x512",
                                  "bge_plan_1x128", "qwen3_model_8x512", "bge_model_8x512"])
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-secondary", action="store_true",
+                        help="headline only: skip the kernel figures of the other configurations")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="also launch one copy of this many MiB (traffic-counter calibration)")
     args = parser.parse_args()
@@ -892,12 +1034,17 @@ def main() -> int:
         shape, lengths = workloads.qwen3_32x512()
         result = bench_qwen(args, "qwen3_32x512", shape, lengths, 4, args.layers,
                             "log-uniform [1,512], seed 4", headline=True)
+        if not args.no_secondary:
+            log("secondary configurations")
+            result["secondary"] = secondary_measurements(args)
     elif args.workload == "qwen3_8x512":
         shape, lengths = workloads.qwen3_8x512()
         result = bench_qwen(args, "qwen3_8x512", shape, lengths, 3, 8, "uniform [64,512], seed 3",
                             headline=False)
     elif args.workload == "bge_32x512":
         result = bench_bge(args)
+    elif args.workload == "qwen3_8x512_f32":
+        result = bench_qwen_f32(args)
     elif args.workload == "qwen_tail_16x256":
         result = bench_qwen_tail(args)
     elif args.workload == "qwen_tail_1x128":
@@ -913,6 +1060,9 @@ def main() -> int:
     else:
         result = bench_qkv4_block(args)
     print(json.dumps(result), flush=True)
+    if "parity" in result and not result["parity"]["ok"]:
+        log(f"parity failed: max abs {result['parity']['max_abs']:.3e} > {result['parity']['bar']}")
+        return 1
     return 0
 
 

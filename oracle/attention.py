@@ -23,28 +23,30 @@ def attention(
     *,
     bidirectional: bool,
     scale: float | None = None,
-) -> NDArray[np.float64]:
-    """q [B,S,H,D], k/v [B,S,KV,D], lengths [B] -> out [B,S,H,D] float64."""
+    dtype: type = np.float64,
+) -> NDArray:
+    """q [B,S,H,D], k/v [B,S,KV,D], lengths [B] -> out [B,S,H,D] in `dtype` (float64, the
+    reference formulation; float32 only as a timing variant of the CPU baseline)."""
     batch, seq, heads, dim = q.shape
     kv_heads = k.shape[2]
     if heads % kv_heads:
         raise ValueError("heads must be a multiple of kv_heads")
     group = heads // kv_heads
     scale = dim**-0.5 if scale is None else scale
-    out = np.empty(q.shape, dtype=np.float64)
+    out = np.empty(q.shape, dtype=dtype)
     positions = np.arange(seq)[:, None]
     for b in range(batch):
         length = min(int(lengths[b]), seq)
         keys = np.arange(length)[None, :]
         for h in range(heads):
             kh = h // group
-            scores = q[b, :, h].astype(np.float64) @ k[b, :length, kh].astype(np.float64).T
-            scores *= scale
+            scores = q[b, :, h].astype(dtype) @ k[b, :length, kh].astype(dtype).T
+            scores *= dtype(scale)
             if not bidirectional:
                 scores[keys > positions] = -np.inf
             probs = np.exp(scores - scores.max(axis=1, keepdims=True))
             probs /= probs.sum(axis=1, keepdims=True)
-            out[b, :, h] = probs @ v[b, :length, kh].astype(np.float64)
+            out[b, :, h] = probs @ v[b, :length, kh].astype(dtype)
     return out
 
 

@@ -14,10 +14,10 @@ import numpy as np
 from numpy.typing import NDArray
 
 
-def rms_norm(x: NDArray, weight: NDArray, eps: float) -> NDArray[np.float64]:
-    x = np.asarray(x, dtype=np.float64)
-    inv = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
-    return x * inv * np.asarray(weight, dtype=np.float64)
+def rms_norm(x: NDArray, weight: NDArray, eps: float, dtype: type = np.float64) -> NDArray:
+    x = np.asarray(x, dtype=dtype)
+    inv = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + dtype(eps))
+    return x * inv * np.asarray(weight, dtype=dtype)
 
 
 def rope_angles(seq: int, dim: int, theta: float) -> NDArray[np.float64]:
@@ -26,17 +26,18 @@ def rope_angles(seq: int, dim: int, theta: float) -> NDArray[np.float64]:
     return np.arange(seq, dtype=np.float64)[:, None] * inv_freq[None, :]
 
 
-def rope(x: NDArray, theta: float) -> NDArray[np.float64]:
-    """x [B, S, heads, D] (position = axis 1) -> rotated float64."""
-    x = np.asarray(x, dtype=np.float64)
+def rope(x: NDArray, theta: float, dtype: type = np.float64) -> NDArray:
+    """x [B, S, heads, D] (position = axis 1) -> rotated, in `dtype` (angles in float64)."""
+    x = np.asarray(x, dtype=dtype)
     seq, dim = x.shape[1], x.shape[-1]
     half = dim // 2
     angles = rope_angles(seq, dim, theta)[None, :, None, :]
-    cos, sin = np.cos(angles), np.sin(angles)
+    cos, sin = np.cos(angles).astype(dtype), np.sin(angles).astype(dtype)
     a, b = x[..., :half], x[..., half:]
     return np.concatenate((a * cos - b * sin, a * sin + b * cos), axis=-1)
 
 
-def norm_rope(x: NDArray, weight: NDArray, eps: float, theta: float) -> NDArray[np.float64]:
+def norm_rope(x: NDArray, weight: NDArray, eps: float, theta: float,
+              dtype: type = np.float64) -> NDArray:
     """Qwen3 order (qwen3.py:216-237): RMSNorm over D, then RoPE."""
-    return rope(rms_norm(x, weight, eps), theta)
+    return rope(rms_norm(x, weight, eps, dtype), theta, dtype)
