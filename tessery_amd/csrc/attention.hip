@@ -134,40 +134,51 @@ __host__ inline dim3 sched_grid(int B, int KV, int wpp) {
                                     static_cast<unsigned>(B));
 }
 
+// Lane l < B of a wavefront holds batch row l's valid length (clamped to S). Loaded once; the
+// load is unconditional, from a clamped index, so it issues first thing.
+__device__ __forceinline__ uint32_t lane_length(const uint32_t* lengths, int B, int S) {
+  const int lane = threadIdx.x & 63;
+  return min(lengths[min(lane, B - 1)], static_cast<uint32_t>(S));
+}
+
+// Plane rank j -> (batch row, kv head, length). Lengths are quantized to their top six bits
+// below S: q = len >> shift with S >> shift < 64. Rows are ordered by q descending, lower index
+// first among equal q, and the row of rank j / KV is found by radix selection over q's six
+// bits: one ballot per bit and scalar arithmetic, then the remaining lane of that rank in index
+// order (v_mbcnt). The kv head is j % KV.
+__device__ __forceinline__ void ranked_plane(uint32_t len, int B, int S, int KV, Div kvdiv, int j,
+                                             Sched& sc) {
+  const int lane = threadIdx.x & 63;
+  const int jrow = quot(j, kvdiv), kvh = j - jrow * KV;
+  const int shift = max(0, 26 - __clz(S));  // bit length of S minus six
+  const uint32_t q = len >> shift;
+  unsigned long long cand = __ballot(lane < B);
+  int r = jrow;
+#pragma unroll
+  for (int bit = 5; bit >= 0; --bit) {
+    const unsigned long long ones = __ballot((q >> bit) & 1u) & cand;
+    const int c = __popcll(ones);
+    if (r < c) {
+      cand = ones;
+    } else {
+      cand ^= ones;
+      r -= c;
+    }
+  }
+  const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(cand >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(cand), 0u));
+  const unsigned long long hit = __ballot(((cand >> lane) & 1u) && below == static_cast<uint32_t>(r));
+  sc.b = __ffsll(hit) - 1;
+  sc.kvh = kvh;
+  sc.L = static_cast<int>(__builtin_amdgcn_readlane(len, sc.b));
+}
+
 __device__ __forceinline__ Sched schedule(const uint32_t* lengths, int B, int S, int KV, Div kvdiv) {
   Sched sc;
   if (sched_ranked(B, KV)) {
     const int j = static_cast<int>(blockIdx.z) * 8 + static_cast<int>(blockIdx.x);  // plane rank
     sc.wgp = static_cast<int>(gridDim.y - 1 - blockIdx.y);
-    const int jrow = quot(j, kvdiv), kvh = j - jrow * KV;
-    // Lane l < B holds row l's length, quantized to its top six bits below S: q = len >> shift
-    // with S >> shift < 64. Rows are ordered by q descending, lower index first among equal q,
-    // and the row of rank jrow is found by radix selection over q's six bits: one ballot per
-    // bit and scalar arithmetic, then the jrow-th remaining lane in index order (v_mbcnt).
-    // (the load is unconditional, from a clamped index, so it issues first thing)
-    const int lane = threadIdx.x & 63;
-    const uint32_t len = min(lengths[min(lane, B - 1)], static_cast<uint32_t>(S));
-    const int shift = max(0, 26 - __clz(S));  // bit length of S minus six
-    const uint32_t q = len >> shift;
-    unsigned long long cand = __ballot(lane < B);
-    int r = jrow;
-#pragma unroll
-    for (int bit = 5; bit >= 0; --bit) {
-      const unsigned long long ones = __ballot((q >> bit) & 1u) & cand;
-      const int c = __popcll(ones);
-      if (r < c) {
-        cand = ones;
-      } else {
-        cand ^= ones;
-        r -= c;
-      }
-    }
-    const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(cand >> 32),
-                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(cand), 0u));
-    const unsigned long long hit = __ballot(((cand >> lane) & 1u) && below == static_cast<uint32_t>(r));
-    sc.b = __ffsll(hit) - 1;
-    sc.kvh = kvh;
-    sc.L = static_cast<int>(__builtin_amdgcn_readlane(len, sc.b));
+    ranked_plane(lane_length(lengths, B, S), B, S, KV, kvdiv, j, sc);
   } else {
     sc.b = static_cast<int>(blockIdx.z);
     sc.kvh = static_cast<int>(blockIdx.y);
@@ -591,12 +602,10 @@ struct F16Shape {
   Div kv, hbn;  // KV and G >> hsh (head blocks per position block)
 };
 
-__device__ __forceinline__ Geom16 make_geom16(const uint32_t* lengths, int B, int S, int KV,
-                                              int bidi, int wave, F16Shape sh) {
+__device__ __forceinline__ Geom16 geom16_of(const Sched& sc, int bidi, int wave, F16Shape sh) {
   Geom16 g;
   const int G = sh.G, nwb = sh.nwb;
   const int hpw = 1 << sh.hsh, ppw = 16 >> sh.hsh, hbn = G >> sh.hsh;
-  const Sched sc = schedule(lengths, B, S, KV, sh.kv);
   const int wgp = sc.wgp;
   g.b = sc.b;
   g.kvh = sc.kvh;
@@ -718,29 +727,61 @@ struct F16Ring {
 // split the same way (P_hi*V + P_lo*V), so the only fp16 roundings left are those of the inputs.
 // ---------------------------------------------------------------------------------------------
 
+// LDS of one workgroup: the K/V ring, reused after the tile loop to stage the output rows
+// (4 wavefronts x 16 rows of RS bytes: RB of data + 16 of padding, so the 16 rows written by one
+// group of 16 lanes start on 16 different bank groups).
 template <int D, typename TOut, bool FUSED>
-__global__ __launch_bounds__(256, 2) void attn_f16_mfma(
-    const _Float16* __restrict__ q, const _Float16* __restrict__ k, const _Float16* __restrict__ v,
-    const uint32_t* __restrict__ lengths, TOut* __restrict__ out, int B, int S, int H, int KV,
-    float scale_log2, int bidi, const uint16_t* __restrict__ gamma,
-    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin, float eps,
-    size_t k_plane, F16Shape shp) {
+struct F16Lds {
+  static constexpr int RB = D * static_cast<int>(sizeof(TOut));
+  static constexpr int RS = RB + 16;
+  static constexpr int RING = F16Ring<D, FUSED>::NST * F16Ring<D, FUSED>::STAGE;
+  static constexpr int HALVES = RING > 4 * 16 * RS / 2 ? RING : 4 * 16 * RS / 2;
+};
+
+struct F16Args {
+  const _Float16* q;
+  const _Float16* k;
+  const _Float16* v;
+  const uint32_t* lengths;
+  void* out;
+  int B, S, H, KV;
+  float scale_log2;
+  int bidi;
+  const uint16_t* gamma;
+  const float* rope_cos;
+  const float* rope_sin;
+  float eps;
+  size_t k_plane;
+  F16Shape shp;
+};
+
+// One block of one plane: 4 wavefronts x 16 query rows (geometry g), from the q load to the
+// output stores. `ring` is the workgroup's LDS; on return every wavefront has issued its stores
+// and no DMA is in flight.
+template <int D, typename TOut, bool FUSED>
+__device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Float16* ring,
+                                          int wave) {
   using R = F16Ring<D, FUSED>;
   constexpr int KT = R::KT, KPL = R::KPL, NST = R::NST, RPB = R::RPB, CPR = R::CPR;
   constexpr int NS = D / 32;   // k-steps per 16x16 score block
   constexpr int NDT = D / 16;  // 16-channel output blocks
   static_assert(D == 64 || D == 128, "pipelined fp16 kernel serves D = 64 or 128");
-  // output staging after the loop: 4 wavefronts x 16 rows of RS bytes (RB of data + 16 of
-  // padding, so the 16 rows written by one group of 16 lanes start on 16 different bank groups)
-  constexpr int RB = D * static_cast<int>(sizeof(TOut));
-  constexpr int RS = RB + 16;
-  constexpr int LDS_HALVES = NST * R::STAGE > 4 * 16 * RS / 2 ? NST * R::STAGE : 4 * 16 * RS / 2;
-  __shared__ __attribute__((aligned(1024))) _Float16 ring[LDS_HALVES];
-
-  const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, gq = lane >> 4;
-  // the wavefront index is uniform; readfirstlane lets the compiler branch on it with scalars
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const Geom16 g = make_geom16(lengths, B, S, KV, bidi, wave, shp);
+  constexpr int RB = F16Lds<D, TOut, FUSED>::RB, RS = F16Lds<D, TOut, FUSED>::RS;
+  const _Float16* __restrict__ q = a.q;
+  const _Float16* __restrict__ k = a.k;
+  const _Float16* __restrict__ v = a.v;
+  TOut* __restrict__ out = static_cast<TOut*>(a.out);
+  const int S = a.S, H = a.H, KV = a.KV, bidi = a.bidi;
+  const float scale_log2 = a.scale_log2, eps = a.eps;
+  const uint16_t* __restrict__ gamma = a.gamma;
+  const float* __restrict__ rope_cos = a.rope_cos;
+  const float* __restrict__ rope_sin = a.rope_sin;
+  const size_t k_plane = a.k_plane;
+  // the lane index as an opaque value, so the per-lane offsets derived from it are recomputed
+  // where they are used instead of being held in registers from the start
+  int tid = static_cast<int>(threadIdx.x);
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, r = lane & 15, gq = lane >> 4;
   const int qpos = g.p0 + (r >> g.hsh);
   const int qhead = g.head0 + (r & ((1 << g.hsh) - 1));
   const bool qvalid = g.active && qpos < S;
@@ -1092,6 +1133,16 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(
   }
 }
 
+
+template <int D, typename TOut, bool FUSED>
+__global__ __launch_bounds__(256, 2) void attn_f16_mfma(F16Args a) {
+  __shared__ __attribute__((aligned(1024))) _Float16 ring[F16Lds<D, TOut, FUSED>::HALVES];
+  // the wavefront index is uniform; readfirstlane lets the compiler branch on it with scalars
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const Sched sc = schedule(a.lengths, a.B, a.S, a.KV, a.shp.kv);
+  f16_block<D, TOut, FUSED>(a, geom16_of(sc, a.bidi, wave, a.shp), ring, wave);
+}
+
 // ---------------------------------------------------------------------------------------------
 // Host launchers.
 // ---------------------------------------------------------------------------------------------
@@ -1174,19 +1225,35 @@ hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <int D, typename TOut, bool FUSED>
+static void launch_f16_kernel(const F16Args& f, hipStream_t st) {
+  attn_f16_mfma<D, TOut, FUSED><<<sched_grid(f.B, f.KV, (f.shp.nwb + 3) / 4), 256, 0, st>>>(f);
+}
+
 template <int D, bool FUSED>
-static void launch_f16_d(const AttnArgs& a, dim3 grid, F16Shape shp, float sl2, hipStream_t st) {
-  auto q = static_cast<const _Float16*>(a.q), k = static_cast<const _Float16*>(a.k),
-       v = static_cast<const _Float16*>(a.v);
-  const size_t plane = static_cast<size_t>(a.B) * a.S * a.KV * a.D;
+static void launch_f16_d(const AttnArgs& a, F16Shape shp, float sl2, hipStream_t st) {
+  F16Args f{};
+  f.q = static_cast<const _Float16*>(a.q);
+  f.k = static_cast<const _Float16*>(a.k);
+  f.v = static_cast<const _Float16*>(a.v);
+  f.lengths = a.lengths;
+  f.out = a.out;
+  f.B = a.B;
+  f.S = a.S;
+  f.H = a.H;
+  f.KV = a.KV;
+  f.scale_log2 = sl2;
+  f.bidi = a.bidi;
+  f.gamma = a.gamma_q;
+  f.rope_cos = a.rope_cos;
+  f.rope_sin = a.rope_sin;
+  f.eps = a.eps;
+  f.k_plane = static_cast<size_t>(a.B) * a.S * a.KV * a.D;
+  f.shp = shp;
   if (a.out_f16)
-    attn_f16_mfma<D, _Float16, FUSED><<<grid, 256, 0, st>>>(
-        q, k, v, a.lengths, static_cast<_Float16*>(a.out), a.B, a.S, a.H, a.KV, sl2, a.bidi,
-        a.gamma_q, a.rope_cos, a.rope_sin, a.eps, plane, shp);
+    launch_f16_kernel<D, _Float16, FUSED>(f, st);
   else
-    attn_f16_mfma<D, float, FUSED><<<grid, 256, 0, st>>>(
-        q, k, v, a.lengths, static_cast<float*>(a.out), a.B, a.S, a.H, a.KV, sl2, a.bidi,
-        a.gamma_q, a.rope_cos, a.rope_sin, a.eps, plane, shp);
+    launch_f16_kernel<D, float, FUSED>(f, st);
 }
 
 bool attention_f16_fits(int B, int S, int H, int KV, int D) {
@@ -1210,19 +1277,16 @@ hipError_t launch_attention_f16(const AttnArgs& a, hipStream_t st) {
   shp.nwb = f16_wave_blocks(a.S, shp.G);
   shp.kv = make_div(static_cast<uint32_t>(a.KV));
   shp.hbn = make_div(static_cast<uint32_t>(shp.G >> shp.hsh));
-  const dim3 grid = sched_grid(a.B, a.KV, (shp.nwb + 3) / 4);
-
   const float sl2 = a.scale * kLog2e;
   const bool fused = a.gamma_q != nullptr;
   if (fused && (!a.rope_cos || !a.rope_sin)) return hipErrorInvalidValue;
   switch (a.D) {
     case 64:
-      fused ? launch_f16_d<64, true>(a, grid, shp, sl2, st)
-            : launch_f16_d<64, false>(a, grid, shp, sl2, st);
+      fused ? launch_f16_d<64, true>(a, shp, sl2, st) : launch_f16_d<64, false>(a, shp, sl2, st);
       break;
     case 128:
-      fused ? launch_f16_d<128, true>(a, grid, shp, sl2, st)
-            : launch_f16_d<128, false>(a, grid, shp, sl2, st);
+      fused ? launch_f16_d<128, true>(a, shp, sl2, st)
+            : launch_f16_d<128, false>(a, shp, sl2, st);
       break;
     default:
       return hipErrorInvalidValue;

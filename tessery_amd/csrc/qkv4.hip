@@ -8,18 +8,25 @@
 //     y[m][n] += scale[n][g] * A_g[m][n] + bias[n][g] * X_g[m]
 //     A_g[m][n] = sum_{k in g} x[m][k] * code[n][k]      (MFMA; codes 0..15 are exact in fp16,
 //                                                          products exact in fp32)
-//     X_g[m]    = sum_{k in g} x[m][k]                    (fp32, from the staged x tile)
+//     X_g[m]    = sum_{k in g} x[m][k]                    (fp32, x times a ones matrix on MFMA)
 // so the dequantized weight is never rounded to fp16: the only rounding beyond fp32
 // accumulation is the final fp16 store of y.
+// qkv4_f16 feeds the codes to the MFMA as the fp16 subnormals c * 2^-24 (one v_perm per code
+// pair, no exponent arithmetic) and carries everything at 2^-24 scale: the loop folds
+// acc += scale * (2^-24 A_g) on the VALU, the bias term acc += sum_g X_g * (2^-24 bias_g) is one
+// fp32 GEMM of depth K/64 on v_mfma_f32_32x32x2_f32 (row sums of 16 groups kept in LDS, flushed
+// every 16 groups), and the store multiplies by 2^24. Power-of-two scaling is exact, so this is the
+// sum above, term for term.
 //
 // Tiling: 256 threads = 4 wavefronts in a 2x2 grid; workgroup tile 128 rows x 128 columns,
 // wavefront tile 64 x 64 = 2x2 MFMA tiles of 32x32 (v_mfma_f32_32x32x16_f16). MFMA k-step s, lane
 // half h covers columns 32h + 8s .. +7 of the group, so one 16-byte load brings a lane's four
 // weight words of a group, and a word decodes into its eight codes in natural order.
-// Pipeline over the K/64 groups: the x tile of group g + 1 (128 x 64 fp16) is copied into the
-// second of two LDS stages by global_load_lds_dwordx4 and the next weight words, scales and biases
-// are loaded into registers, while group g runs. X_g comes from the MFMA too (x times a ones
-// matrix), so the VALU only decodes codes and folds the group into the accumulator.
+// qkv4_f16 pipelines the K/64 groups through a three-stage LDS ring: x (128 x 64 fp16) and the
+// tile's packed weight words of group g + 2 are copied by global_load_lds_dwordx4 while group g
+// runs, one barrier per group; the scales and biases of all groups arrive once, up front. Each
+// wavefront also keeps the row sums of one of its two 32-row tiles (the four wavefronts cover the
+// 128 rows) in LDS for the bias GEMM.
 // x rows are XOR-swizzled in LDS by (row >> 1) & 7 over their 16-byte chunks: the 16 rows read by
 // one group of 16 lanes land on 16 different bank groups. Rows past M read row M - 1 and are
 // never stored.
@@ -49,6 +56,22 @@ __device__ __forceinline__ half8 decode_codes(uint32_t w) {
   return h - bias;
 }
 
+// codes c0..c7 of a weight word as the fp16 subnormals c * 2^-24 (bit pattern = c), in natural
+// order: the same byte pairing as decode_codes without the exponent, so a word costs 3 masks and
+// shifts plus 4 v_perm. A product x * c * 2^-24 of an fp16 x is exact in fp32 (it stays above
+// 2^-48), so the MFMA sums are 2^-24 times the sums over the integer codes, bit for bit wherever
+// no partial sum drops below the fp32 normal range.
+__device__ __forceinline__ half8 decode_codes_subnormal(uint32_t w) {
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+  uint4v r;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const uint32_t sel = 0x0C000C00u | (static_cast<uint32_t>(4 + p) << 16) | static_cast<uint32_t>(p);
+    r[p] = __builtin_amdgcn_perm(hi, lo, sel);
+  }
+  return __builtin_bit_cast(half8, r);
+}
+
 template <bool BF16>
 __device__ __forceinline__ float word_value(uint16_t w) {
   if constexpr (BF16) {
@@ -60,12 +83,24 @@ __device__ __forceinline__ float word_value(uint16_t w) {
 
 __device__ __forceinline__ int xsw(int row) { return (row >> 1) & 7; }
 
+template <int N>
+struct GroupStage {  // compile-time ring stage of a group
+  static constexpr int value = N;
+};
+
+// Groups between two flushes of the bias term (the row sums of that many groups stay in LDS).
+constexpr int kBiasChunk = 16;
+
 template <bool BF16>
 __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
   // three x stages of 128 rows x 64 halves, as the DMA writes them (1 KiB = 8 rows per block)
   __shared__ __attribute__((aligned(1024))) _Float16 xs[3][128 * 64];
-  // three stages of the packed weight words of the tile's 128 columns for one group (8 words each)
+  // three stages of the packed weight words of the tile's 128 columns for one group, laid out
+  // [column block of 32][k half][column][4 words]: the 16 lanes of one LDS read take 16
+  // consecutive 16-byte chunks
   __shared__ __attribute__((aligned(1024))) uint32_t ws[3][128 * 8];
+  // row sums X_g of the last kBiasChunk groups, [group][128 rows] (fp32)
+  __shared__ __attribute__((aligned(16))) float xg_lds[kBiasChunk][128];
   // scale and bias words of the tile's 128 columns, all groups: [2][128][groups] (dynamic size)
   extern __shared__ __attribute__((aligned(1024))) uint16_t sbuf[];
 
@@ -89,24 +124,29 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
   _Float16* __restrict__ y = a.y[proj];
   const int nw = tile * 128 + wn * 64;  // wavefront's first column
 
-  // ---- DMA of the x tile of one group: wavefront w fills blocks 4w .. 4w+3 (rows 8 per block)
+  // ---- DMA of the x tile of one group: wavefront w fills blocks 4w .. 4w+3 (rows 8 per block);
+  // the group's 128-byte column range is a scalar base, the lane's row and chunk a 32-bit offset
+  // (M * K * 2 < 2^32, checked by the launcher)
   const int dchunk = lane & 7;
-  auto issue_x = [&](int stage, int g) {
+  uint32_t xoff[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int blk = 4 * wave + j, row = 8 * blk + (lane >> 3);
-      const int grow = min(m0 + row, M - 1);
-      const _Float16* src =
-          a.x + static_cast<size_t>(grow) * K + 64 * g + 8 * (dchunk ^ xsw(row));
-      dma16(src, &xs[stage][blk * 512]);
-    }
-  };
+  for (int j = 0; j < 4; ++j) {
+    const int row = 8 * (4 * wave + j) + (lane >> 3);
+    const int grow = min(m0 + row, M - 1);
+    xoff[j] = (static_cast<uint32_t>(grow) * static_cast<uint32_t>(K) +
+               static_cast<uint32_t>(8 * (dchunk ^ xsw(row)))) * 2u;
+  }
   // ---- DMA of the weight words of one group: wavefront w copies columns 32w .. 32w+31 of the
-  // tile (lane l: column 32w + l/2, words 4(l&1) .. +3), so lane l's 16 bytes land at byte 16l
-  const uint32_t* wsrc = w + static_cast<size_t>(tile * 128 + 32 * wave + (lane >> 1)) * (K / 8) +
-                         4 * (lane & 1);
-  auto issue_w = [&](int stage, int g) {
-    dma16(wsrc + 8 * g, reinterpret_cast<_Float16*>(&ws[stage][256 * wave]));
+  // tile; lane l takes column 32w + l % 32, words 4 (l / 32) .. +3, landing at byte 16 l
+  const uint32_t woff =
+      (static_cast<uint32_t>(tile * 128 + 32 * wave + l32) * static_cast<uint32_t>(K / 8) +
+       4u * static_cast<uint32_t>(hh)) * 4u;
+  auto issue = [&](auto stage, int g) {
+    constexpr int st = decltype(stage)::value;
+    const _Float16* xbase = a.x + 64 * g;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16_at(xbase, xoff[j], &xs[st][(4 * wave + j) * 512]);
+    dma16_at(w + 8 * g, woff, reinterpret_cast<_Float16*>(&ws[st][256 * wave]));
   };
   // ---- scales and biases of the tile's columns, all groups: two contiguous runs of
   // 128 * groups words (rows tile*128 .. +127 of [N, groups]), 16 bytes per lane, issued once
@@ -132,80 +172,119 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  const half8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
-  issue_x(0, 0);
-  issue_w(0, 0);
-  if (groups > 1) {
-    issue_x(1, 1);
-    issue_w(1, 1);
-  }
+  // bias term of groups [g0, g0 + count): acc[m][n] += sum_g X_g[m] * bias[n][g] on fp32 MFMA
+  // (v_mfma_f32_32x32x2_f32: k-slot kk of lane l is group g0 + 2 q + kk, kk = l / 32; its output
+  // layout is the one of the 32x32x16 tiles). Called with every wavefront past the barrier that
+  // follows the last of those groups' row sums.
+  auto flush_bias = [&](int g0, int count) {
+    for (int q = 0; q < count; q += 2) {
+      const bool live = q + hh < count;
+      const int g = live ? g0 + q + hh : g0;  // this lane's k-slot (a dead slot reads a live one)
+      float av[2], bv[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        av[i] = live ? xg_lds[g - g0][wm * 64 + 32 * i + l32] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int col = wn * 64 + 32 * j + l32;
+        bv[j] = live ? word_value<BF16>(sbuf[128 * groups + col * groups + g]) * 0x1p-24f : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+  };
 
-  for (int g = 0; g < groups; ++g) {
-    const int stage = g % 3;
+  const half8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+  issue(GroupStage<0>{}, 0);
+  if (groups > 1) issue(GroupStage<1>{}, 1);
+
+  // One group: its tiles live in stage g % 3; group g + 2 goes to stage (g + 2) % 3. The stage is a
+  // compile-time constant (the loop below is unrolled by the ring depth).
+  auto step = [&](int g, auto stage) {
+    constexpr int st = decltype(stage)::value, nxt = (st + 2) % 3;
     // in flight: this group's tiles, then the next group's (5 DMA instructions per wavefront)
     if (g + 1 < groups) wait_vmcnt<5>();
     else wait_vmcnt<0>();
     stage_barrier();
-    if (g + 2 < groups) {
-      const int nst = stage == 0 ? 2 : stage - 1;  // (g + 2) % 3
-      issue_x(nst, g + 2);
-      issue_w(nst, g + 2);
+    if (g + 2 < groups) issue(GroupStage<nxt>{}, g + 2);
+    // the row sums of the previous chunk are all in LDS: add its bias term before the buffer
+    // takes the next chunk
+    if (g % kBiasChunk == 0 && g > 0) {
+      flush_bias(g - kBiasChunk, kBiasChunk);
+      stage_barrier();
     }
-    // the lane's four weight words of this group and the scale / bias of its two columns
+    // the lane's four weight words of this group (column block, k half, column) and the scales
     uint4v wd[2];
-    uint16_t sv[2], bv[2];
+    uint16_t sv[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int col = wn * 64 + 32 * j + l32;
-      wd[j] = *reinterpret_cast<const uint4v*>(&ws[stage][col * 8 + 4 * hh]);
+      wd[j] = *reinterpret_cast<const uint4v*>(&ws[st][256 * (2 * wn + j) + 128 * hh + 4 * l32]);
       sv[j] = sbuf[col * groups + g];
-      bv[j] = sbuf[128 * groups + col * groups + g];
     }
 
     half8 bq[2][4];
-    float gs[2], gb[2];
+    float gs[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) bq[j][s] = decode_codes(wd[j][s]);
+      for (int s4 = 0; s4 < 4; ++s4) bq[j][s4] = decode_codes_subnormal(wd[j][s4]);
       gs[j] = word_value<BF16>(sv[j]);
-      gb[j] = word_value<BF16>(bv[j]);
     }
 
-    // ---- A_g for the 2x2 tiles and X_g (x times ones) per row tile ----
-    floatx16 part[2][2], xg[2];
+    // ---- A_g for the 2x2 tiles; X_g (x times ones) of row tile i = wn: each wavefront keeps the
+    // row sums of one of its two 32-row tiles, the four wavefronts together all 128 rows ----
+    floatx16 part[2][2], xg;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) xg[i][e] = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) part[i][j][e] = 0.0f;
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int row = wm * 64 + 32 * i + l32;
-        const half8 av =
-            *reinterpret_cast<const half8*>(&xs[stage][row * 64 + 8 * ((4 * hh + s) ^ xsw(row))]);
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bq[j][s], part[i][j], 0, 0, 0);
-        xg[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, ones, xg[i], 0, 0, 0);
-      }
-
-    // ---- fold: acc += scale * A_g + bias * X_g ----
+    for (int e = 0; e < 16; ++e) xg[e] = 0.0f;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          acc[i][j][e] = fmaf(gs[j], part[i][j][e], fmaf(gb[j], xg[i][e], acc[i][j][e]));
+        for (int e = 0; e < 16; ++e) part[i][j][e] = 0.0f;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      half8 av[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int row = wm * 64 + 32 * i + l32;
+        av[i] = *reinterpret_cast<const half8*>(&xs[st][row * 64 + 8 * ((4 * hh + s4) ^ xsw(row))]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bq[j][s4], part[i][j], 0, 0, 0);
+      xg = __builtin_amdgcn_mfma_f32_32x32x16_f16(wn ? av[1] : av[0], ones, xg, 0, 0, 0);
+    }
 
+    // ---- scale term in the loop: acc += scale * A_g; X_g to LDS for the bias term ----
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = fmaf(gs[j], part[i][j][e], acc[i][j][e]);
+    if (l32 == 0) {
+      // every column of xg holds the row sums: lane 0 and lane 32 write rows 8 q + 4 hh .. +3
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<floatx4*>(&xg_lds[g % kBiasChunk][wm * 64 + 32 * wn + 8 * q + 4 * hh]) =
+            floatx4{xg[4 * q], xg[4 * q + 1], xg[4 * q + 2], xg[4 * q + 3]};
+    }
+  };
+  for (int g = 0; g < groups; g += 3) {
+    step(g, GroupStage<0>{});
+    if (g + 1 < groups) step(g + 1, GroupStage<1>{});
+    if (g + 2 < groups) step(g + 2, GroupStage<2>{});
   }
+  // the last chunk's row sums: written before this barrier, read after it
+  stage_barrier();
+  flush_bias(groups - (groups - 1) % kBiasChunk - 1, (groups - 1) % kBiasChunk + 1);
 
   // ---- store y[m][n] as fp16 ----
 #pragma unroll
@@ -216,7 +295,7 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int m = m0 + wm * 64 + 32 * i + 8 * (e >> 2) + 4 * hh + (e & 3);
-        if (m < M) y[static_cast<size_t>(m) * N + n] = static_cast<_Float16>(acc[i][j][e]);
+        if (m < M) y[static_cast<size_t>(m) * N + n] = static_cast<_Float16>(acc[i][j][e] * 0x1p24f);
       }
     }
 }
@@ -432,13 +511,16 @@ hipError_t launch_linear4_hilo_f32(const float* x, const uint32_t* w, const uint
 }
 
 // scale and bias words of a column tile, all groups: 2 * 128 * groups halves (8 KiB at K = 1024);
-// with the 60 KiB of x and weight stages, two workgroups fit a CU up to K = 2048
+// with the 68 KiB of x / weight stages and row sums, two workgroups fit a CU up to K = 1536
 static size_t qkv4_sb_bytes(int K) { return static_cast<size_t>(2 * 128 * 2) * (K / 64); }
 
 bool qkv4_f16_fits(int M, int K, const int n[3]) {
   if (M <= 0 || K <= 0 || K % 64 || qkv4_sb_bytes(K) > 64 * 1024) return false;  // K <= 8192
-  for (int p = 0; p < 3; ++p)
-    if (n[p] <= 0 || n[p] % 128) return false;
+  // 32-bit DMA byte offsets inside x [M, K] fp16
+  if (static_cast<uint64_t>(M) * static_cast<uint64_t>(K) * 2 >= (1ull << 32)) return false;
+  for (int p = 0; p < 3; ++p)  // and inside each packed weight matrix [N, K/8] u32
+    if (n[p] <= 0 || n[p] % 128 || static_cast<uint64_t>(n[p]) * static_cast<uint64_t>(K) / 2 >= (1ull << 32))
+      return false;
   return true;
 }
 
