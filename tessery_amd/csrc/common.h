@@ -24,6 +24,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float float2v __attribute__((ext_vector_type(2)));
 typedef uint32_t uint4v __attribute__((ext_vector_type(4)));
+typedef uint32_t uint2v __attribute__((ext_vector_type(2)));
 
 // BF16 storage word -> float (exact): tessery stores norm weights and uint4 scales/biases
 // as bfloat16 words (kernels.metal:10).

@@ -99,8 +99,10 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
   // [column block of 32][k half][column][4 words]: the 16 lanes of one LDS read take 16
   // consecutive 16-byte chunks
   __shared__ __attribute__((aligned(1024))) uint32_t ws[3][128 * 8];
-  // row sums X_g of the last kBiasChunk groups, [group][128 rows] (fp32)
-  __shared__ __attribute__((aligned(16))) float xg_lds[kBiasChunk][128];
+  // row sums X_g of the last kBiasChunk groups, [group][128 rows] (fp32); the last two rows take
+  // the stores of the lanes that hold no row sum (a store from every lane keeps the loop body
+  // one basic block)
+  __shared__ __attribute__((aligned(16))) float xg_lds[kBiasChunk + 2][128];
   // scale and bias words of the tile's 128 columns, all groups: [2][128][groups] (dynamic size)
   extern __shared__ __attribute__((aligned(1024))) uint16_t sbuf[];
 
@@ -164,42 +166,70 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
       }
   }
 
-  floatx16 acc[2][2];
+  // The wavefront's two 32-row tiles in the order it works on them: tile t1 = wn first (its
+  // row sums are this wavefront's share), then t2 = 1 - wn. acc1 / acc2 accumulate them.
+  const int t1 = wn, t2 = 1 - wn;
+  floatx16 acc1[2], acc2[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    for (int e = 0; e < 16; ++e) acc1[j][e] = acc2[j][e] = 0.0f;
 
-  // bias term of groups [g0, g0 + count): acc[m][n] += sum_g X_g[m] * bias[n][g] on fp32 MFMA
+  // bias term of groups [g0, g0 + count): acc[t][n] += sum_g X_g[m] * bias[n][g] on fp32 MFMA
   // (v_mfma_f32_32x32x2_f32: k-slot kk of lane l is group g0 + 2 q + kk, kk = l / 32; its output
   // layout is the one of the 32x32x16 tiles). Called with every wavefront past the barrier that
   // follows the last of those groups' row sums.
   auto flush_bias = [&](int g0, int count) {
-    for (int q = 0; q < count; q += 2) {
-      const bool live = q + hh < count;
-      const int g = live ? g0 + q + hh : g0;  // this lane's k-slot (a dead slot reads a live one)
-      float av[2], bv[2];
+    // every operand first (one LDS round trip), then the MFMAs of the live pairs
+    float a1v[kBiasChunk / 2], a2v[kBiasChunk / 2], bv[kBiasChunk / 2][2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        av[i] = live ? xg_lds[g - g0][wm * 64 + 32 * i + l32] : 0.0f;
+    for (int q2 = 0; q2 < kBiasChunk / 2; ++q2) {
+      const int q = 2 * q2 + hh;  // this lane's k-slot: group g0 + q
+      const bool live = q < count;
+      const int qc = live ? q : 0;  // a dead slot reads a live one and uses zeros
+      a1v[q2] = live ? xg_lds[qc][wm * 64 + 32 * t1 + l32] : 0.0f;
+      a2v[q2] = live ? xg_lds[qc][wm * 64 + 32 * t2 + l32] : 0.0f;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int col = wn * 64 + 32 * j + l32;
-        bv[j] = live ? word_value<BF16>(sbuf[128 * groups + col * groups + g]) * 0x1p-24f : 0.0f;
+        bv[q2][j] =
+            live ? word_value<BF16>(sbuf[128 * groups + col * groups + g0 + qc]) * 0x1p-24f : 0.0f;
       }
+    }
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+    for (int q2 = 0; q2 < kBiasChunk / 2; ++q2) {
+      if (2 * q2 >= count) break;  // wavefront-uniform
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < 2; ++j) {
+        acc1[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1v[q2], bv[q2][j], acc1[j], 0, 0, 0);
+        acc2[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a2v[q2], bv[q2][j], acc2[j], 0, 0, 0);
+      }
     }
   };
 
-  const half8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+  // Row sums on v_mfma_f32_16x16x32_f16 from the 32x32x16 A registers of tile t1: read as a
+  // 16x16x32 operand, lane (r = l % 16, q = l / 16) holds 8 values of row r + 16 (q & 1). The B
+  // operand sel[k][n] = 1 where n = (k / 8) & 1 (else 0) sends rows r to column 0 and rows r + 16 to
+  // column 1, so over the four k-steps D[r][0] = X_g[r] and D[r][1] = X_g[r + 16]; lanes with
+  // l % 16 < 2 hold them, four rows each.
+  const _Float16 selv = (lane & 15) == ((lane >> 4) & 1) ? _Float16(1) : _Float16(0);
+  const half8 sel = {selv, selv, selv, selv, selv, selv, selv, selv};
+  const int xg_row = wm * 64 + 32 * t1 + 16 * (lane & 1) + 4 * (lane >> 4);
+
+  // LDS offsets (halves) of the lane's A operand in the two tiles; the swizzle depends on l32 only
+  const int arow1 = wm * 64 + 32 * t1 + l32, arow2 = wm * 64 + 32 * t2 + l32;
+
   issue(GroupStage<0>{}, 0);
   if (groups > 1) issue(GroupStage<1>{}, 1);
+
+  // Products of the previous group's second tile and its scales, folded during the next group's
+  // first-tile MFMAs (zero before the first group).
+  floatx16 p2[2];
+  float gs_prev[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) p2[j][e] = 0.0f;
 
   // One group: its tiles live in stage g % 3; group g + 2 goes to stage (g + 2) % 3. The stage is a
   // compile-time constant (the loop below is unrolled by the ring depth).
@@ -218,86 +248,105 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
     }
     // the lane's four weight words of this group (column block, k half, column) and the scales
     uint4v wd[2];
-    uint16_t sv[2];
+    float gs[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int col = wn * 64 + 32 * j + l32;
       wd[j] = *reinterpret_cast<const uint4v*>(&ws[st][256 * (2 * wn + j) + 128 * hh + 4 * l32]);
-      sv[j] = sbuf[col * groups + g];
+      gs[j] = word_value<BF16>(sbuf[col * groups + g]);
     }
-
     half8 bq[2][4];
-    float gs[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) bq[j][s4] = decode_codes_subnormal(wd[j][s4]);
-      gs[j] = word_value<BF16>(sv[j]);
-    }
+      for (int s4 = 0; s4 < 4; ++s4)
+        bq[j][s4] = decode_codes_subnormal(wd[j][s4]);
 
-    // ---- A_g for the 2x2 tiles; X_g (x times ones) of row tile i = wn: each wavefront keeps the
-    // row sums of one of its two 32-row tiles, the four wavefronts together all 128 rows ----
-    floatx16 part[2][2], xg;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) xg[e] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) part[i][j][e] = 0.0f;
+    // ---- tile t1: 2^-24 A_g and the row sums; meanwhile fold the previous group's tile t2 ----
+    floatx16 p1[2];
+    floatx4 xg = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
-      half8 av[2];
+      const half8 av =
+          *reinterpret_cast<const half8*>(&xs[st][arow1 * 64 + 8 * ((4 * hh + s4) ^ xsw(l32))]);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int row = wm * 64 + 32 * i + l32;
-        av[i] = *reinterpret_cast<const half8*>(&xs[st][row * 64 + 8 * ((4 * hh + s4) ^ xsw(row))]);
+      for (int j = 0; j < 2; ++j) {
+        if (s4 == 0)
+          p1[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bq[j][0], floatx16{}, 0, 0, 0);
+        else
+          p1[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bq[j][s4], p1[j], 0, 0, 0);
       }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bq[j][s4], part[i][j], 0, 0, 0);
-      xg = __builtin_amdgcn_mfma_f32_32x32x16_f16(wn ? av[1] : av[0], ones, xg, 0, 0, 0);
+      xg = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, sel, xg, 0, 0, 0);
     }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc2[j][e] = fmaf(gs_prev[j], p2[j][e], acc2[j][e]);
 
-    // ---- scale term in the loop: acc += scale * A_g; X_g to LDS for the bias term ----
+    // ---- tile t2; meanwhile fold tile t1 ----
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int s4 = 0; s4 < 4; ++s4) {
+      const half8 av =
+          *reinterpret_cast<const half8*>(&xs[st][arow2 * 64 + 8 * ((4 * hh + s4) ^ xsw(l32))]);
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][j][e] = fmaf(gs[j], part[i][j][e], acc[i][j][e]);
-    if (l32 == 0) {
-      // every column of xg holds the row sums: lane 0 and lane 32 write rows 8 q + 4 hh .. +3
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<floatx4*>(&xg_lds[g % kBiasChunk][wm * 64 + 32 * wn + 8 * q + 4 * hh]) =
-            floatx4{xg[4 * q], xg[4 * q + 1], xg[4 * q + 2], xg[4 * q + 3]};
+      for (int j = 0; j < 2; ++j) {
+        if (s4 == 0)
+          p2[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bq[j][0], floatx16{}, 0, 0, 0);
+        else
+          p2[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bq[j][s4], p2[j], 0, 0, 0);
+      }
     }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc1[j][e] = fmaf(gs[j], p1[j][e], acc1[j][e]);
+    gs_prev[0] = gs[0];
+    gs_prev[1] = gs[1];
+    // instruction order of the block above: LDS reads, the decode, then each MFMA followed by a
+    // few VALU instructions (the folds), so the folds run while the MFMAs do
+    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // LDS reads
+    __builtin_amdgcn_sched_group_barrier(0x002, 56, 0);  // VALU: decode
+#pragma unroll
+    for (int k = 0; k < 12; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (tile t1, row sums)
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU (fold of the previous t2)
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (tile t2)
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU (fold of t1)
+    }
+    float* xg_dst = (lane & 15) < 2 ? &xg_lds[g % kBiasChunk][xg_row] : &xg_lds[kBiasChunk][4 * lane];
+    *reinterpret_cast<floatx4*>(xg_dst) = xg;
   };
   for (int g = 0; g < groups; g += 3) {
     step(g, GroupStage<0>{});
     if (g + 1 < groups) step(g + 1, GroupStage<1>{});
     if (g + 2 < groups) step(g + 2, GroupStage<2>{});
   }
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc2[j][e] = fmaf(gs_prev[j], p2[j][e], acc2[j][e]);
   // the last chunk's row sums: written before this barrier, read after it
   stage_barrier();
   flush_bias(groups - (groups - 1) % kBiasChunk - 1, (groups - 1) % kBiasChunk + 1);
 
-  // ---- store y[m][n] as fp16 ----
+  // ---- store y[m][n] = 2^24 acc as fp16 ----
+  auto store_tile = [&](const floatx16& t, int tile_row, int j) {
+    const int n = nw + 32 * j + l32;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = nw + 32 * j + l32;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = m0 + wm * 64 + 32 * i + 8 * (e >> 2) + 4 * hh + (e & 3);
-        if (m < M) y[static_cast<size_t>(m) * N + n] = static_cast<_Float16>(acc[i][j][e] * 0x1p24f);
-      }
+    for (int e = 0; e < 16; ++e) {
+      const int m = m0 + wm * 64 + 32 * tile_row + 8 * (e >> 2) + 4 * hh + (e & 3);
+      if (m < M)
+        y[static_cast<size_t>(m) * N + n] = static_cast<_Float16>(t[e] * 0x1p24f);
     }
+  };
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    store_tile(acc1[j], t1, j);
+    store_tile(acc2[j], t2, j);
+  }
 }
 
 

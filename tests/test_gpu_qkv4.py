@@ -23,7 +23,9 @@ def weights(rng, n, k, kind):
 
 
 @pytest.mark.parametrize("kind", ["f16", "bf16"])
-@pytest.mark.parametrize("m,k,nq,nkv", [(300, 1024, 2048, 1024), (128, 256, 128, 128), (1, 64, 256, 128)])
+@pytest.mark.parametrize("m,k,nq,nkv", [(300, 1024, 2048, 1024), (128, 256, 128, 128), (1, 64, 256, 128),
+                                         (65, 320, 128, 128), (257, 448, 256, 128),
+                                         (130, 1536, 128, 256), (200, 128, 128, 128)])
 def test_qkv4_matches_f64(runtime, kind, m, k, nq, nkv):
     rng = np.random.default_rng(5 + m)
     x = rng.standard_normal((m, k), dtype=np.float32).astype(np.float16)
