@@ -11,12 +11,13 @@
 //     X_g[m]    = sum_{k in g} x[m][k]                    (fp32, x times a ones matrix on MFMA)
 // so the dequantized weight is never rounded to fp16: the only rounding beyond fp32
 // accumulation is the final fp16 store of y.
-// qkv4_f16 feeds the codes to the MFMA as the fp16 subnormals c * 2^-24 (one v_perm per code
-// pair, no exponent arithmetic) and carries everything at 2^-24 scale: the loop folds
-// acc += scale * (2^-24 A_g) on the VALU, the bias term acc += sum_g X_g * (2^-24 bias_g) is one
-// fp32 GEMM of depth K/64 on v_mfma_f32_32x32x2_f32 (row sums of 16 groups kept in LDS, flushed
-// every 16 groups), and the store multiplies by 2^24. Power-of-two scaling is exact, so this is the
-// sum above, term for term.
+// qkv4_f16 folds only acc += scale * A_g in the loop; the bias term acc += sum_g bias_g X_g is
+// one fp32 GEMM of depth K/64 on v_mfma_f32_32x32x2_f32 (row sums of 16 groups kept in LDS,
+// flushed every 16 groups).
+// The codes enter the MFMA as normal fp16 integers (1024 + c, less 1024, both exact). fp16
+// subnormal codes (c * 2^-24, one v_perm per code pair) would save half the decode, but the MFMA
+// does not sum products of subnormal operands exactly: measured against float64 they leave a
+// one-sided error near 1e-6 of sum |x| |w|, where normal codes give 1e-7.
 //
 // Tiling: 256 threads = 4 wavefronts in a 2x2 grid; workgroup tile 128 rows x 128 columns,
 // wavefront tile 64 x 64 = 2x2 MFMA tiles of 32x32 (v_mfma_f32_32x32x16_f16). MFMA k-step s, lane
@@ -56,22 +57,6 @@ __device__ __forceinline__ half8 decode_codes(uint32_t w) {
   return h - bias;
 }
 
-// codes c0..c7 of a weight word as the fp16 subnormals c * 2^-24 (bit pattern = c), in natural
-// order: the same byte pairing as decode_codes without the exponent, so a word costs 3 masks and
-// shifts plus 4 v_perm. A product x * c * 2^-24 of an fp16 x is exact in fp32 (it stays above
-// 2^-48), so the MFMA sums are 2^-24 times the sums over the integer codes, bit for bit wherever
-// no partial sum drops below the fp32 normal range.
-__device__ __forceinline__ half8 decode_codes_subnormal(uint32_t w) {
-  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-  uint4v r;
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const uint32_t sel = 0x0C000C00u | (static_cast<uint32_t>(4 + p) << 16) | static_cast<uint32_t>(p);
-    r[p] = __builtin_amdgcn_perm(hi, lo, sel);
-  }
-  return __builtin_bit_cast(half8, r);
-}
-
 template <bool BF16>
 __device__ __forceinline__ float word_value(uint16_t w) {
   if constexpr (BF16) {
@@ -83,9 +68,36 @@ __device__ __forceinline__ float word_value(uint16_t w) {
 
 __device__ __forceinline__ int xsw(int row) { return (row >> 1) & 7; }
 
+// 16 bytes per lane, global -> VGPRs, at a wave-uniform base (SGPR pair) plus a per-lane 32-bit
+// byte offset and an immediate. Inline asm like the LDS DMA, so the compiler places no waits of
+// its own for it (it cannot count the DMAs, and its waits for mixed streams degrade to
+// vmcnt(0)); the caller reads dst only after wait_vmcnt_pin. dst is a read-write operand: every
+// read of its previous value is ordered before the load (or reads a copy made before it).
+template <int OFF>
+__device__ __forceinline__ void load16_at(floatx4& dst, const void* base, uint32_t off) {
+  asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3"
+               : "+v"(dst)
+               : "v"(off), "s"(base), "i"(OFF)
+               : "memory");
+}
+
+// s_waitcnt vmcnt(N); the four registers count as written here, so nothing reads them earlier.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_pin(floatx4 (&r)[4]) {
+  asm volatile("s_waitcnt vmcnt(%4)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3])
+               : "n"(N)
+               : "memory");
+}
+
 template <int N>
 struct GroupStage {  // compile-time ring stage of a group
   static constexpr int value = N;
+};
+
+template <int ST, int PAR>
+struct GroupStep {  // compile-time ring stage (g % 3) and parity (g % 2) of a group
+  static constexpr int stage = ST, parity = PAR;
 };
 
 // Groups between two flushes of the bias term (the row sums of that many groups stay in LDS).
@@ -193,7 +205,7 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
       for (int j = 0; j < 2; ++j) {
         const int col = wn * 64 + 32 * j + l32;
         bv[q2][j] =
-            live ? word_value<BF16>(sbuf[128 * groups + col * groups + g0 + qc]) * 0x1p-24f : 0.0f;
+            live ? word_value<BF16>(sbuf[128 * groups + col * groups + g0 + qc]) : 0.0f;
       }
     }
 #pragma unroll
@@ -260,9 +272,9 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4)
-        bq[j][s4] = decode_codes_subnormal(wd[j][s4]);
+        bq[j][s4] = decode_codes(wd[j][s4]);
 
-    // ---- tile t1: 2^-24 A_g and the row sums; meanwhile fold the previous group's tile t2 ----
+    // ---- tile t1: A_g and the row sums; meanwhile fold the previous group's tile t2 ----
     floatx16 p1[2];
     floatx4 xg = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -332,14 +344,14 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
   stage_barrier();
   flush_bias(groups - (groups - 1) % kBiasChunk - 1, (groups - 1) % kBiasChunk + 1);
 
-  // ---- store y[m][n] = 2^24 acc as fp16 ----
+  // ---- store y[m][n] = acc as fp16 ----
   auto store_tile = [&](const floatx16& t, int tile_row, int j) {
     const int n = nw + 32 * j + l32;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int m = m0 + wm * 64 + 32 * tile_row + 8 * (e >> 2) + 4 * hh + (e & 3);
       if (m < M)
-        y[static_cast<size_t>(m) * N + n] = static_cast<_Float16>(t[e] * 0x1p24f);
+        y[static_cast<size_t>(m) * N + n] = static_cast<_Float16>(t[e]);
     }
   };
 #pragma unroll
@@ -382,180 +394,248 @@ __global__ __launch_bounds__(256) void row_scales_f32(const float* __restrict__ 
   if (lane == 0) rs[row] = scale;
 }
 
-// 128 x 128 output tile per workgroup, 4 wavefronts in a 2 x 2 grid of 64 x 64 (2 x 2 MFMA
-// tiles of 32 x 32, v_mfma_f32_32x32x16_f16), the A / B k-mapping of qkv4_f16. Two LDS stages of
-// the hi and lo planes (swizzled as in qkv4_f16) and of X_g; group g + 1's x (fp32, 8 float4 per
-// thread), weight words, scales and biases are loaded into registers while group g runs.
+// Groups between two flushes of the bias term in linear4_hilo (their row sums stay in an LDS
+// ring).
+constexpr int kHiloChunk = 16;
+
+// 64 x 128 output tile per workgroup, 4 wavefronts in a 2 x 2 grid of 32 x 64 (1 x 2 MFMA tiles
+// of 32 x 32, v_mfma_f32_32x32x16_f16), the A / B k-mapping of qkv4_f16. Per group g, after one
+// barrier:
+//   * the MFMAs of group g (hi and lo planes of x from LDS stage g % 2) interleave with the
+//     staging of group g + 1 into the other stage: x * 2^e_m split into hi / lo halves
+//     (hi = fp16(x 2^e), lo = fp16(x 2^e - hi)) and its row sums;
+//   * the fold acc += scale * A_g follows the MFMAs;
+//   * the bias term acc += sum_g bias_g X_g runs on v_mfma_f32_32x32x2_f32 over a ring of
+//     kHiloChunk row sums in LDS, flushed every kHiloChunk groups.
+// Memory: the tile's packed weight words ride a three-stage LDS ring (global_load_lds_dwordx4,
+// group g + 2 issued during group g, the qkv4_f16 layout); the scales and biases of all groups
+// arrive in LDS once, up front; fp32 x is prefetched two groups ahead in two register sets.
+// 64-row tiles keep two workgroups on every CU down to 8 column tiles x 4096 rows.
 __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__ x,
                                                       const float* __restrict__ rs,
                                                       const uint32_t* __restrict__ w,
                                                       const uint16_t* __restrict__ sc,
                                                       const uint16_t* __restrict__ bi,
                                                       float* __restrict__ y, int M, int N, int K) {
-  __shared__ __attribute__((aligned(1024))) _Float16 xs[2][2][128 * 64];  // [stage][hi, lo]
-  __shared__ __attribute__((aligned(16))) float xsum[2][128];
+  constexpr int TM = 64;
+  __shared__ __attribute__((aligned(1024))) _Float16 xs[2][2][TM * 64];  // [stage][hi, lo]
+  __shared__ __attribute__((aligned(1024))) uint32_t ws[3][128 * 8];      // qkv4_f16 layout
+  __shared__ __attribute__((aligned(16))) float xg_lds[kHiloChunk][TM];
+  // scale and bias words of the tile's 128 columns, all groups: [2][128][groups] (dynamic size)
+  extern __shared__ __attribute__((aligned(1024))) uint16_t sbuf[];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wm = wave >> 1, wn = wave & 1;
   const int groups = K / 64;
-  const int m0 = blockIdx.x * 128;
-  const int nw = blockIdx.y * 128 + wn * 64;
+  const int m0 = blockIdx.x * TM;
+  const int tile = blockIdx.y;
+  const int nw = tile * 128 + wn * 64;
+  const int wrow = wm * 32;  // wavefront's rows in the tile
 
-  // staging role: row srow of the tile, floats 32 * skh .. +31 of each group
-  const int srow = tid >> 1, skh = tid & 1;
-  const int grow = min(m0 + srow, M - 1);  // rows past M repeat row M - 1, never stored
-  const float* xsrc = x + static_cast<size_t>(grow) * K + 32 * skh;
-  const float rscale = rs[grow];
-  floatx4 xr[8];
-  auto load_x = [&](int g) {
+  // ---- scales and biases: two contiguous runs of 128 * groups words, 16 bytes per lane ----
+  {
+    const int chunks = 128 * groups / 8;
+    const uint16_t* srcs[2] = {sc + static_cast<size_t>(tile * 128) * groups,
+                               bi + static_cast<size_t>(tile * 128) * groups};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) xr[j] = *reinterpret_cast<const floatx4*>(xsrc + 64 * g + 4 * j);
-  };
-  // MFMA role: the lane's two columns nw + 32 j + l32, words 4 hh .. 4 hh + 3 of each group
-  const uint32_t* wp[2];
-  const uint16_t* sp[2];
-  const uint16_t* bp[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const size_t n = static_cast<size_t>(nw + 32 * j + l32);
-    wp[j] = w + n * (K / 8) + 4 * hh;
-    sp[j] = sc + n * groups;
-    bp[j] = bi + n * groups;
+    for (int part = 0; part < 2; ++part)
+      for (int blk = wave; blk * 64 < chunks; blk += 4) {
+        const int chunk = blk * 64 + lane;
+        if (chunk < chunks)
+          dma16(srcs[part] + 8 * chunk,
+                reinterpret_cast<_Float16*>(sbuf + part * 128 * groups + blk * 512));
+      }
   }
-  uint4v wd[2], wdn[2];
-  uint16_t sv[2], bv[2], svn[2], bvn[2];
-  auto load_w = [&](int g, uint4v* wo, uint16_t* so, uint16_t* bo) {
+
+  // ---- staging role: row srow of the tile, floats 16 * spart .. +15 of each group ----
+  const int srow = tid >> 2, spart = tid & 3;
+  const int grow = min(m0 + srow, M - 1);  // rows past M repeat row M - 1, never stored
+  // byte offset of the lane's floats in x (M * K * 4 < 2^32, checked by the launcher)
+  const uint32_t xoff = (static_cast<uint32_t>(grow) * static_cast<uint32_t>(K) +
+                         16u * static_cast<uint32_t>(spart)) * 4u;
+  const float rscale = rs[grow];
+  floatx4 xr[2][4];
+  auto load_x = [&](int g, int set) {
+    const float* base = x + 64 * g;
+    load16_at<0>(xr[set][0], base, xoff);
+    load16_at<16>(xr[set][1], base, xoff);
+    load16_at<32>(xr[set][2], base, xoff);
+    load16_at<48>(xr[set][3], base, xoff);
+  };
+  // hi / lo halves of the x in register set `set` into LDS stage st; returns the partial row sum
+  auto stage_x = [&](int set, int st) {
+    float sum = 0.0f;
+    half8 hv[2], lv[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      wo[j] = *reinterpret_cast<const uint4v*>(wp[j] + 8 * g);
-      so[j] = sp[j][g];
-      bo[j] = bp[j][g];
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float v = xr[set][j][t];
+        const _Float16 h = static_cast<_Float16>(v * rscale);
+        hv[j >> 1][4 * (j & 1) + t] = h;
+        lv[j >> 1][4 * (j & 1) + t] = static_cast<_Float16>(fmaf(v, rscale, -static_cast<float>(h)));
+        sum = fmaf(v, rscale, sum);
+      }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int pos = srow * 64 + 8 * ((2 * spart + c) ^ xsw(srow));
+      *reinterpret_cast<half8*>(&xs[st][0][pos]) = hv[c];
+      *reinterpret_cast<half8*>(&xs[st][1][pos]) = lv[c];
+    }
+    return sum;
+  };
+
+  // ---- weight words of one group: wavefront w copies columns 32w .. 32w+31 of the tile; lane l
+  // takes column 32w + l % 32, words 4 (l / 32) .. +3 (the qkv4_f16 ring) ----
+  const uint32_t woff =
+      (static_cast<uint32_t>(tile * 128 + 32 * wave + l32) * static_cast<uint32_t>(K / 8) +
+       4u * static_cast<uint32_t>(hh)) * 4u;
+  auto issue_w = [&](int st, int g) {
+    dma16_at(w + 8 * g, woff, reinterpret_cast<_Float16*>(&ws[st][256 * wave]));
+  };
+
+  floatx16 acc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[j][e] = 0.0f;
+
+  // acc[j] += sum_{g in [g0, g0 + count)} bias[n][g] X_g[m] (v_mfma_f32_32x32x2_f32: k-slot
+  // kk = l / 32 of lane l is group g0 + 2 q + kk); operands first, then the MFMAs
+  auto flush_bias = [&](int g0, int count) {
+    float av[kHiloChunk / 2], bw[kHiloChunk / 2][2];
+#pragma unroll
+    for (int q2 = 0; q2 < kHiloChunk / 2; ++q2) {
+      const int q = 2 * q2 + hh;
+      const bool live = q < count;
+      const int qc = live ? q : 0;
+      av[q2] = live ? xg_lds[(g0 + qc) % kHiloChunk][wrow + l32] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int col = wn * 64 + 32 * j + l32;
+        bw[q2][j] = live ? bf16_to_float(sbuf[128 * groups + col * groups + g0 + qc]) : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int q2 = 0; q2 < kHiloChunk / 2; ++q2) {
+      if (2 * q2 >= count) break;  // wavefront-uniform
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q2], bw[q2][j], acc[j], 0, 0, 0);
     }
   };
 
-  floatx16 acc[2][2];
+  // Memory instructions in issue order (the memory counter retires in order): scales / biases
+  // (above); x of group 0; then x of group k + 1 right before the weights of group k, for every
+  // k. The prologue issues x(1), w(0), stages group 0, then x(2), w(1); step g issues x(g + 3),
+  // w(g + 2) (both clamped to the last group). So at the start of step g the weights of group g
+  // have exactly 5 younger memory instructions (x(g + 2), w(g + 1)), and x(g + 1), issued before
+  // w(g), is complete too.
+  load_x(0, 0);
+  load_x(min(1, groups - 1), 1);
+  issue_w(0, 0);
+  wait_vmcnt_pin<5>(xr[0]);  // x(0): x(1) and w(0) are younger
+  float xsum = stage_x(0, 0);
+  load_x(min(2, groups - 1), 0);
+  issue_w(1, min(1, groups - 1));
+
+  // One group: weights in ring stage st = g % 3, x in LDS stage g % 2, the x of group g + 1 in
+  // register set (g + 1) % 2; PAR = g % 2 is compile-time (the loop below is unrolled by two and
+  // has no other branch, which keeps the compiler's memory waits exact).
+  auto step = [&](int g, int st, auto parity) {
+    constexpr int par = decltype(parity)::value;
+    wait_vmcnt_pin<5>(xr[par ^ 1]);  // this group's weight words and the x of group g + 1
+    __syncthreads();  // weights of group g and x of group g visible; group g - 1's stages free
+    if (g % kHiloChunk == 0 && g > 0) {
+      flush_bias(g - kHiloChunk, kHiloChunk);
+      __syncthreads();  // the ring takes group g's row sums next
+    }
+    float rsum = xsum;
+    rsum += __shfl_xor(rsum, 1);
+    rsum += __shfl_xor(rsum, 2);
+    if (spart == 0) xg_lds[g % kHiloChunk][srow] = rsum;
+
+    uint4v wd[2];
+    float gs[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 2; ++j) {
+      const int col = wn * 64 + 32 * j + l32;
+      wd[j] = *reinterpret_cast<const uint4v*>(&ws[st][256 * (2 * wn + j) + 128 * hh + 4 * l32]);
+      gs[j] = bf16_to_float(sbuf[col * groups + g]);
+    }
+    // stage group g + 1 from its register set, refill that set with group g + 3, then the
+    // weights of group g + 2 into the ring stage group g - 1 used
+    xsum = stage_x(par ^ 1, par ^ 1);
+    load_x(min(g + 3, groups - 1), par ^ 1);
+    issue_w(st == 0 ? 2 : st - 1, min(g + 2, groups - 1));
+
+    floatx16 p[2];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      const int row = wrow + l32;
+      const int off = row * 64 + 8 * ((4 * hh + s4) ^ xsw(row));
+      const half8 ah = *reinterpret_cast<const half8*>(&xs[par][0][off]);
+      const half8 al = *reinterpret_cast<const half8*>(&xs[par][1][off]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const half8 bq = decode_codes(wd[j][s4]);
+        p[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bq, s4 ? p[j] : floatx16{}, 0, 0, 0);
+        p[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bq, p[j], 0, 0, 0);
+      }
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-
-  load_x(0);
-  load_w(0, wd, sv, bv);
-  for (int g = 0; g < groups; ++g) {
-    const int stage = g & 1;
-    // ---- scale, split and stage group g's x; its row sum X_g ----
-    {
-      float sum = 0.0f;
-      half8 hv[4], lv[4];
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const float v = xr[j][t] * rscale;
-          const _Float16 h = static_cast<_Float16>(v);
-          sum += v;
-          hv[j >> 1][4 * (j & 1) + t] = h;
-          lv[j >> 1][4 * (j & 1) + t] = static_cast<_Float16>(v - static_cast<float>(h));
-        }
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int pos = srow * 64 + 8 * ((4 * skh + c) ^ xsw(srow));
-        *reinterpret_cast<half8*>(&xs[stage][0][pos]) = hv[c];
-        *reinterpret_cast<half8*>(&xs[stage][1][pos]) = lv[c];
-      }
-      sum += __shfl_xor(sum, 1);
-      if (!skh) xsum[stage][srow] = sum;
-    }
-    if (g + 1 < groups) {
-      load_x(g + 1);
-      load_w(g + 1, wdn, svn, bvn);
-    }
-    __syncthreads();
-
-    // ---- A_g for the wavefront's 2 x 2 tiles, both halves into one sum ----
-    floatx16 part[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) part[i][j][e] = 0.0f;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      half8 bq[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) bq[j] = decode_codes(wd[j][s]);
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int row = wm * 64 + 32 * i + l32;
-        const int off = row * 64 + 8 * ((4 * hh + s) ^ xsw(row));
-        const half8 ah = *reinterpret_cast<const half8*>(&xs[stage][0][off]);
-        const half8 al = *reinterpret_cast<const half8*>(&xs[stage][1][off]);
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bq[j], part[i][j], 0, 0, 0);
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bq[j], part[i][j], 0, 0, 0);
-      }
-    }
-
-    // ---- fold: acc += scale * A_g + bias * X_g ----
-    float gs[2], gb[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      gs[j] = bf16_to_float(sv[j]);
-      gb[j] = bf16_to_float(bv[j]);
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      floatx4 xg[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        xg[q] = *reinterpret_cast<const floatx4*>(&xsum[stage][wm * 64 + 32 * i + 8 * q + 4 * hh]);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e)
-          acc[i][j][e] = fmaf(gs[j], part[i][j][e], fmaf(gb[j], xg[e >> 2][e & 3], acc[i][j][e]));
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      wd[j] = wdn[j];
-      sv[j] = svn[j];
-      bv[j] = bvn[j];
-    }
+      for (int e = 0; e < 16; ++e) acc[j][e] = fmaf(gs[j], p[j][e], acc[j][e]);
+  };
+  int st = 0;  // g % 3
+  int g = 0;
+  for (; g + 1 < groups; g += 2) {
+    step(g, st, GroupStage<0>{});
+    st = st == 2 ? 0 : st + 1;
+    step(g + 1, st, GroupStage<1>{});
+    st = st == 2 ? 0 : st + 1;
+  }
+  if (g < groups) step(g, st, GroupStage<0>{});
+  // the clamped prefetches past the last group: their registers stay reserved until they land
+  wait_vmcnt_pin<0>(xr[0]);
+  wait_vmcnt_pin<0>(xr[1]);
+  __syncthreads();  // the last chunk's row sums
+  {
+    const int last = (groups - 1) / kHiloChunk * kHiloChunk;
+    flush_bias(last, groups - last);
   }
 
   // ---- y = acc / 2^e_m, fp32, row-major ----
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int e = 0; e < 16; ++e) {
+    const int m = m0 + wrow + 8 * (e >> 2) + 4 * hh + (e & 3);
+    if (m < M) {
+      // 1 / rs[m], exact: rs[m] = 2^e_m with |e_m| <= 126, frexp gives e_m + 1
+      const float inv = __builtin_amdgcn_ldexpf(1.0f, 1 - __builtin_amdgcn_frexp_expf(rs[m]));
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int m = m0 + wm * 64 + 32 * i + 8 * (e >> 2) + 4 * hh + (e & 3);
-      if (m < M) {
-        const float inv = 1.0f / rs[m];
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          y[static_cast<size_t>(m) * N + nw + 32 * j + l32] = acc[i][j][e] * inv;
-      }
+      for (int j = 0; j < 2; ++j) y[static_cast<size_t>(m) * N + nw + 32 * j + l32] = acc[j][e] * inv;
     }
+  }
 }
 
 }  // namespace
+
+// scale and bias words of a column tile in linear4_hilo, all groups (24 KiB at K = 3072; with the
+// 48 KiB of x / weight stages and row sums two workgroups fit a CU up to K = 4096)
+static size_t hilo_sb_bytes(int K) { return static_cast<size_t>(2 * 128 * 2) * (K / 64); }
 
 hipError_t launch_linear4_hilo_f32(const float* x, const uint32_t* w, const uint16_t* scales,
                                    const uint16_t* biases, float* y, int M, int N, int K,
                                    float* scratch, size_t scratch_floats, hipStream_t st) {
   if (M <= 0) return hipSuccess;
-  if (K <= 0 || K % 64 || N <= 0 || N % 128 || !scratch ||
+  if (K <= 0 || K % 64 || hilo_sb_bytes(K) > 64 * 1024 || N <= 0 || N % 128 || !scratch ||
+      static_cast<uint64_t>(M) * static_cast<uint64_t>(K) * 4 >= (1ull << 32) ||
       static_cast<size_t>(M) > scratch_floats || (reinterpret_cast<uintptr_t>(x) & 15))
     return hipErrorInvalidValue;
   row_scales_f32<<<(M + 3) / 4, 256, 0, st>>>(x, M, K, scratch);
-  dim3 grid((M + 127) / 128, N / 128);
-  linear4_hilo<<<grid, 256, 0, st>>>(x, scratch, w, scales, biases, y, M, N, K);
+  dim3 grid((M + 63) / 64, N / 128);
+  linear4_hilo<<<grid, 256, hilo_sb_bytes(K), st>>>(x, scratch, w, scales, biases, y, M, N, K);
   return hipGetLastError();
 }
 
