@@ -57,6 +57,26 @@ __device__ __forceinline__ half8 decode_codes(uint32_t w) {
   return h - bias;
 }
 
+// codes of a weight word as fp16 in the order c0 c2 c4 c6 c1 c3 c5 c7 (even nibbles, then odd):
+// v_perm pairs each nibble byte with the fp16 exponent byte 0x64 (1024 + c) straight from the
+// masked word, and 1024 is subtracted exactly. The x operand must be staged in the same k order
+// within each 8-element chunk (linear4_hilo stages it so), then every product is the same.
+__device__ __forceinline__ half8 decode_codes_evenodd(uint32_t w) {
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+  const uint32_t e64 = 0x64646464u;
+  uint4v r;
+  r[0] = __builtin_amdgcn_perm(e64, lo, 0x04010400u);  // c0 c2
+  r[1] = __builtin_amdgcn_perm(e64, lo, 0x04030402u);  // c4 c6
+  r[2] = __builtin_amdgcn_perm(e64, hi, 0x04010400u);  // c1 c3
+  r[3] = __builtin_amdgcn_perm(e64, hi, 0x04030402u);  // c5 c7
+  half8 h = __builtin_bit_cast(half8, r);
+  const half8 bias = {1024, 1024, 1024, 1024, 1024, 1024, 1024, 1024};
+  return h - bias;
+}
+
+// position of k-offset e (0..7) of a chunk in the decode_codes_evenodd order
+__host__ __device__ constexpr int evenodd_pos(int e) { return (e >> 1) + 4 * (e & 1); }
+
 template <bool BF16>
 __device__ __forceinline__ float word_value(uint16_t w) {
   if constexpr (BF16) {
@@ -403,7 +423,8 @@ constexpr int kHiloChunk = 16;
 // barrier:
 //   * the MFMAs of group g (hi and lo planes of x from LDS stage g % 2) interleave with the
 //     staging of group g + 1 into the other stage: x * 2^e_m split into hi / lo halves
-//     (hi = fp16(x 2^e), lo = fp16(x 2^e - hi)) and its row sums;
+//     (hi = fp16(x 2^e), lo = fp16(x 2^e - hi)), stored in the k order of
+//     decode_codes_evenodd within each 8-element chunk, and its row sums;
 //   * the fold acc += scale * A_g follows the MFMAs;
 //   * the bias term acc += sum_g bias_g X_g runs on v_mfma_f32_32x32x2_f32 over a ring of
 //     kHiloChunk row sums in LDS, flushed every kHiloChunk groups.
@@ -472,8 +493,9 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
       for (int t = 0; t < 4; ++t) {
         const float v = xr[set][j][t];
         const _Float16 h = static_cast<_Float16>(v * rscale);
-        hv[j >> 1][4 * (j & 1) + t] = h;
-        lv[j >> 1][4 * (j & 1) + t] = static_cast<_Float16>(fmaf(v, rscale, -static_cast<float>(h)));
+        const int pos = evenodd_pos(4 * (j & 1) + t);  // the order of the decoded codes
+        hv[j >> 1][pos] = h;
+        lv[j >> 1][pos] = static_cast<_Float16>(fmaf(v, rscale, -static_cast<float>(h)));
         sum = fmaf(v, rscale, sum);
       }
 #pragma unroll
@@ -578,7 +600,7 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
       const half8 al = *reinterpret_cast<const half8*>(&xs[par][1][off]);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const half8 bq = decode_codes(wd[j][s4]);
+        const half8 bq = decode_codes_evenodd(wd[j][s4]);
         p[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bq, s4 ? p[j] : floatx16{}, 0, 0, 0);
         p[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bq, p[j], 0, 0, 0);
       }
