@@ -10,7 +10,9 @@
 // Three kernels:
 //   attn_scalar      one wavefront per (token, head); any D <= 256. Routes "attention" and
 //                    "attention_f16_scalar".
-//   attn_f32_mfma    fp32 MFMA (v_mfma_f32_32x32x2_f32) tiles, D in {32,64,128}; any S.
+//   attn_f32_ring    fp32 MFMA (v_mfma_f32_32x32x2_f32) tiles on an LDS DMA ring, D in {32,64};
+//   attn_f32_split   the same fp32 MFMA arithmetic for D = 128, keys split over two wavefronts
+//                    per row block and merged in fixed order; any S.
 //                    Routes "attention_tiled", "attention_tail_32", "attention_tail_128".
 //   attn_f16_mfma    fp16 operands / fp32 accumulation (v_mfma_f32_16x16x32_f16 and
 //                    16x16x16_f16), D in {64,128}, any S, optional fused per-head RMSNorm + RoPE
@@ -199,8 +201,10 @@ struct F32Shape {
   Div g, kv;
 };
 
+// Row block rb = wgp * RBW + sub of the plane (RBW row blocks per workgroup).
+template <int RBW = 4>
 __device__ __forceinline__ Geom make_geom(const uint32_t* lengths, int B, int S, int KV, int bidi,
-                                          int wave, F32Shape sh) {
+                                          int sub, F32Shape sh) {
   Geom g;
   const int G = sh.G;
   const int nrb = G * ((S + 31) / 32);
@@ -208,13 +212,13 @@ __device__ __forceinline__ Geom make_geom(const uint32_t* lengths, int B, int S,
   const int wgp = sc.wgp;
   g.b = sc.b;
   g.kvh = sc.kvh;
-  const int rb = wgp * 4 + wave;
+  const int rb = wgp * RBW + sub;
   g.active = rb < nrb;
   const int pb = quot(rb, sh.g);
   g.head = g.kvh * G + (rb - pb * G);
   g.p0 = pb * 32;
   g.L = sc.L;
-  const int rb_last = min(wgp * 4 + 3, nrb - 1);
+  const int rb_last = min(wgp * RBW + RBW - 1, nrb - 1);
   if (bidi) {
     g.wave_end = g.active ? g.L : 0;
     g.wg_end = g.L;
@@ -248,36 +252,46 @@ __device__ __forceinline__ float pair32(float x, bool take_max) {
 constexpr float kMaxSlack = 8.0f;
 
 // ---------------------------------------------------------------------------------------------
-// fp32 MFMA kernel. v_mfma_f32_32x32x2_f32: A[i][k] from lane (i, k=l/32), B[k][j] from lane
-// (j, k=l/32), D[8a+4(l/32)+c][l%32] in acc[4a+c].
+// fp32 MFMA kernel, D = 128, key-split. v_mfma_f32_32x32x2_f32: A[i][k] from lane (i, k=l/32),
+// B[k][j] from lane (j, k=l/32), D[8a+4(l/32)+c][l%32] in acc[4a+c].
 //   S^T: k-step s uses channel d = s + (l/32)*D/2, so each lane's Q values are contiguous.
 //   O^T: k-step (a, c) pairs keys 8a+c (lanes 0-31) and 8a+4+c (lanes 32-63); P^T comes from
 //        acc[4a+c] of the same lane, V is read row-major from LDS (one float per lane).
-// Key tile 32, K/V tiles padded to D+4 floats per row (rows 4 banks apart: conflict-free
-// 16-byte reads), next tile prefetched into registers while the current one is consumed.
+// A workgroup takes two row blocks of 32 query rows that share the KV head (two query heads of
+// a GQA group, or two position blocks) and splits their keys: wavefront 2h + r runs row block r
+// over the key tiles h, h + 2, h + 4, ... (half h), each half staging its own 32-key tiles
+// (K and V padded to D+4 floats per row: rows 4 banks apart, conflict-free 16-byte reads),
+// the next tile prefetched into registers while the current one is consumed. The two halves of a
+// row block end with their own (O, running max, sum); half 1 passes them through LDS and half 0
+// merges them in that fixed order (deterministic). The longest work item is half a row block's
+// keys, and the workgroups outnumber the CU slots, so causal and ragged planes balance.
 // ---------------------------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(256, 2) void attn_f32_mfma(const float* __restrict__ q,
-                                                        const float* __restrict__ k,
-                                                        const float* __restrict__ v,
-                                                        const uint32_t* __restrict__ lengths,
-                                                        float* __restrict__ out, int B, int S,
-                                                        int H, int KV, float scale_log2,
-                                                        int bidi, F32Shape shp) {
+__global__ __launch_bounds__(256, 2) void attn_f32_split(const float* __restrict__ q,
+                                                         const float* __restrict__ k,
+                                                         const float* __restrict__ v,
+                                                         const uint32_t* __restrict__ lengths,
+                                                         float* __restrict__ out, int B, int S,
+                                                         int H, int KV, float scale_log2,
+                                                         int bidi, F32Shape shp) {
   constexpr int KT = 32;
   constexpr int ROW = D + 4;
-  constexpr int CH = KT * D / 4;            // 16-byte chunks per K (or V) tile
-  constexpr int CPT = (CH + 255) / 256;     // chunks per thread
+  constexpr int CH = KT * D / 4;           // 16-byte chunks per K (or V) tile
+  constexpr int CPT = (CH + 127) / 128;    // chunks per thread of a half (128 threads)
   constexpr int HALF = D / 2;
-  __shared__ __attribute__((aligned(16))) float Ks[KT * ROW];
-  __shared__ __attribute__((aligned(16))) float Vs[KT * ROW];
+  __shared__ __attribute__((aligned(16))) float Ks[2][KT * ROW];
+  __shared__ __attribute__((aligned(16))) float Vs[2][KT * ROW];
+  static_assert(2 * KT * ROW >= 2 * (D / 32 * 16 + 2) * 64, "merge exchange fits in Ks");
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  const Geom g = make_geom(lengths, B, S, KV, bidi, wave, shp);
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = wave >> 1, sub = wave & 1;
+  const Geom g = make_geom<2>(lengths, B, S, KV, bidi, sub, shp);
   const int qpos = g.p0 + l32;
   const bool qvalid = g.active && qpos < S;
   const int limit = bidi ? g.L : min(qpos + 1, g.L);
   const int ntiles = (g.wg_end + KT - 1) / KT;
+  const int niter = (ntiles + 1) / 2;  // both halves step together; half h takes tile 2 it + h
 
   // Q row slice held in registers as B operands.
   float qf[HALF];
@@ -301,15 +315,17 @@ __global__ __launch_bounds__(256, 2) void attn_f32_mfma(const float* __restrict_
     for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
 
+  // this half's 128 threads stage its tiles
+  const int ht = tid & 127;
   floatx4 kreg[CPT], vreg[CPT];
   auto load_tile = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int c = tid + 256 * i;
+      const int c = ht + 128 * i;
       const int key = c / (D / 4), ck = c % (D / 4);
       const int kg = kt * KT + key;
       floatx4 kz = {0.f, 0.f, 0.f, 0.f}, vz = kz;
-      if (c < CH && kg < g.L) {
+      if (c < CH && kt < ntiles && kg < g.L) {
         const size_t off = ((static_cast<size_t>(g.b) * S + kg) * KV + g.kvh) * D + 4 * ck;
         kz = *reinterpret_cast<const floatx4*>(k + off);
         vz = *reinterpret_cast<const floatx4*>(v + off);
@@ -318,28 +334,31 @@ __global__ __launch_bounds__(256, 2) void attn_f32_mfma(const float* __restrict_
       vreg[i] = vz;
     }
   };
-  if (ntiles > 0) load_tile(0);
+  if (niter > 0) load_tile(half);
 
-  for (int kt = 0; kt < ntiles; ++kt) {
+  float* const kh = Ks[half];
+  float* const vh = Vs[half];
+  for (int it = 0; it < niter; ++it) {
+    const int kt = 2 * it + half;
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int c = tid + 256 * i;
+      const int c = ht + 128 * i;
       if (c < CH) {
         const int key = c / (D / 4), ck = c % (D / 4);
-        *reinterpret_cast<floatx4*>(&Ks[key * ROW + 4 * ck]) = kreg[i];
-        *reinterpret_cast<floatx4*>(&Vs[key * ROW + 4 * ck]) = vreg[i];
+        *reinterpret_cast<floatx4*>(&kh[key * ROW + 4 * ck]) = kreg[i];
+        *reinterpret_cast<floatx4*>(&vh[key * ROW + 4 * ck]) = vreg[i];
       }
     }
     __syncthreads();
-    if (kt + 1 < ntiles) load_tile(kt + 1);
-    if (kt * KT < g.wave_end) {
+    if (it + 1 < niter) load_tile(kt + 2);
+    if (kt < ntiles && kt * KT < g.wave_end) {
       floatx16 s;
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[e] = 0.0f;
 #pragma unroll
       for (int c = 0; c < HALF / 4; ++c) {
-        const floatx4 kk = *reinterpret_cast<const floatx4*>(&Ks[l32 * ROW + hh * HALF + 4 * c]);
+        const floatx4 kk = *reinterpret_cast<const floatx4*>(&kh[l32 * ROW + hh * HALF + 4 * c]);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
           s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[t], qf[4 * c + t], s, 0, 0, 0);
@@ -377,31 +396,49 @@ __global__ __launch_bounds__(256, 2) void attn_f32_mfma(const float* __restrict_
         const int key = 8 * (e >> 2) + 4 * hh + (e & 3);
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt)
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[key * ROW + 32 * dt + l32], s[e], o[dt],
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vh[key * ROW + 32 * dt + l32], s[e], o[dt],
                                                        0, 0, 0);
       }
     }
   }
 
-  if (qvalid) {
-    const float inv = 1.0f / l_run;
+  // ---- merge: half 1 hands (O, max, sum) of its row block to half 0 through LDS ----
+  __syncthreads();  // every wavefront is done with the tiles
+  float* const xch = &Ks[0][0] + sub * (D / 32 * 16 + 2) * 64;
+  if (half == 1) {
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) xch[(16 * dt + e) * 64 + lane] = o[dt][e];
+    xch[(D / 32 * 16) * 64 + lane] = m_run;
+    xch[(D / 32 * 16 + 1) * 64 + lane] = l_run;
+  }
+  __syncthreads();
+  if (half == 0 && qvalid) {
+    const float m1 = xch[(D / 32 * 16) * 64 + lane], l1 = xch[(D / 32 * 16 + 1) * 64 + lane];
+    const float m = fmaxf(m_run, m1);  // finite: key 0 lies in half 0 for every valid row
+    const float c0 = __builtin_amdgcn_exp2f(m_run - m), c1 = __builtin_amdgcn_exp2f(m1 - m);
+    const float inv = 1.0f / (l_run * c0 + l1 * c1);
     const size_t base = ((static_cast<size_t>(g.b) * S + qpos) * H + g.head) * D;
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
-        floatx4 r = {o[dt][4 * a] * inv, o[dt][4 * a + 1] * inv, o[dt][4 * a + 2] * inv,
-                     o[dt][4 * a + 3] * inv};
+        floatx4 r;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          r[c] = (o[dt][4 * a + c] * c0 + xch[(16 * dt + 4 * a + c) * 64 + lane] * c1) * inv;
         __builtin_nontemporal_store(r, reinterpret_cast<floatx4*>(out + base + 32 * dt + 8 * a + 4 * hh));
       }
   }
 }
 
 // ---------------------------------------------------------------------------------------------
-// fp32 MFMA kernel with an LDS DMA ring, D = 32 and 64: the geometry, MFMA layout and arithmetic
-// of attn_f32_mfma, with the K and V tiles of 32 keys streamed through a 3-stage ring filled by
-// global_load_lds_dwordx4 two tiles ahead (one barrier per tile) instead of being staged through
-// registers, and the tile loop unrolled by the ring depth (LDS addresses = register + immediate).
+// fp32 MFMA kernel with an LDS DMA ring, D = 32 and 64: the MFMA layout and arithmetic of
+// attn_f32_split, with four row blocks per workgroup (make_geom<4>, no key split), the K and V
+// tiles of 32 keys streamed through a 3-stage ring filled by global_load_lds_dwordx4 two tiles
+// ahead (one barrier per tile), and the tile loop unrolled by the ring depth (LDS addresses =
+// register + immediate).
 // LDS rows hold D floats, no padding:
 //   K: row r holds key r, its 16-byte chunks XOR-swizzled by ksw32(r), so the rows read by one
 //      group of 16 lanes (one chunk each) fall on 16 different bank groups;
@@ -1152,6 +1189,13 @@ static dim3 mfma_grid(int B, int S, int H, int KV) {
   return sched_grid(B, KV, (nrb + 3) / 4);
 }
 
+// attn_f32_split: two row blocks per workgroup
+static dim3 split_grid(int B, int S, int H, int KV) {
+  const int G = H / KV;
+  const int nrb = G * ((S + 31) / 32);
+  return sched_grid(B, KV, (nrb + 1) / 2);
+}
+
 // Grid limits and the exactness bound of the Div quotients (n * d < 2^32 for every quotient the
 // geometry takes: plane rank / KV on the ranked schedule, row block / head blocks).
 static bool geometry_fits(int B, int KV, int nblocks, int blockdiv) {
@@ -1217,7 +1261,8 @@ hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st) {
       attn_f32_ring<64><<<grid, 256, 0, st>>>(q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
       break;
     case 128:
-      attn_f32_mfma<128><<<grid, 256, 0, st>>>(q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
+      attn_f32_split<128><<<split_grid(a.B, a.S, a.H, a.KV), 256, 0, st>>>(
+          q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
       break;
     default:
       return hipErrorInvalidValue;
