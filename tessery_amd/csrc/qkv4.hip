@@ -19,15 +19,16 @@
 // does not sum products of subnormal operands exactly: measured against float64 they leave a
 // one-sided error near 1e-6 of sum |x| |w|, where normal codes give 1e-7.
 //
-// Tiling: 256 threads = 4 wavefronts in a 2x2 grid; workgroup tile 128 rows x 128 columns,
-// wavefront tile 64 x 64 = 2x2 MFMA tiles of 32x32 (v_mfma_f32_32x32x16_f16). MFMA k-step s, lane
-// half h covers columns 32h + 8s .. +7 of the group, so one 16-byte load brings a lane's four
-// weight words of a group, and a word decodes into its eight codes in natural order.
+// Tiling: workgroup tile 128 rows x 128 columns (v_mfma_f32_32x32x16_f16 tiles of 32x32). MFMA
+// k-step s, lane half h covers columns 32h + 8s .. +7 of the group, so one 16-byte load brings a
+// lane's four weight words of a group, and a word decodes into its eight codes in natural order.
+// qkv4_f16: 4 wavefronts, each with 32 columns and all 128 rows (1 x 4 MFMA tiles), so every
+// weight word is decoded once per workgroup; linear4_hilo: 64 rows, a 2 x 2 grid of 32 x 64.
 // qkv4_f16 pipelines the K/64 groups through a three-stage LDS ring: x (128 x 64 fp16) and the
 // tile's packed weight words of group g + 2 are copied by global_load_lds_dwordx4 while group g
 // runs, one barrier per group; the scales and biases of all groups arrive once, up front. Each
-// wavefront also keeps the row sums of one of its two 32-row tiles (the four wavefronts cover the
-// 128 rows) in LDS for the bias GEMM.
+// wavefront folds one 32-row tile on the VALU while the MFMAs run the next, and keeps the row
+// sums of one tile (the four wavefronts cover the 128 rows) in LDS for the bias GEMM.
 // x rows are XOR-swizzled in LDS by (row >> 1) & 7 over their 16-byte chunks: the 16 rows read by
 // one group of 16 lanes land on 16 different bank groups. Rows past M read row M - 1 and are
 // never stored.
@@ -140,7 +141,6 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  const int wm = wave >> 1, wn = wave & 1;
   const int M = a.M, K = a.K, groups = K / 64;
   const int m0 = blockIdx.x * 128;
 
@@ -156,7 +156,6 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
   const uint16_t* __restrict__ sc = a.s[proj];
   const uint16_t* __restrict__ bi = a.b[proj];
   _Float16* __restrict__ y = a.y[proj];
-  const int nw = tile * 128 + wn * 64;  // wavefront's first column
 
   // ---- DMA of the x tile of one group: wavefront w fills blocks 4w .. 4w+3 (rows 8 per block);
   // the group's 128-byte column range is a scalar base, the lane's row and chunk a 32-bit offset
@@ -198,70 +197,60 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
       }
   }
 
-  // The wavefront's two 32-row tiles in the order it works on them: tile t1 = wn first (its
-  // row sums are this wavefront's share), then t2 = 1 - wn. acc1 / acc2 accumulate them.
-  const int t1 = wn, t2 = 1 - wn;
-  floatx16 acc1[2], acc2[2];
+  // Each wavefront owns the tile's 32 columns 32 w .. 32 w + 31 (its weight block: each weight
+  // word is decoded once per workgroup) and all 128 rows, as four 32-row tiles taken in the
+  // order r_k = (w + k) % 4: the first is the one whose row sums it keeps.
+  const int col = 32 * wave + l32;  // the lane's column in the tile
+  floatx16 acc[4];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int k = 0; k < 4; ++k)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc1[j][e] = acc2[j][e] = 0.0f;
+    for (int e = 0; e < 16; ++e) acc[k][e] = 0.0f;
+  auto rtile = [&](int k) { return (wave + k) & 3; };
 
-  // bias term of groups [g0, g0 + count): acc[t][n] += sum_g X_g[m] * bias[n][g] on fp32 MFMA
+  // bias term of groups [g0, g0 + count): acc[k][m][n] += sum_g X_g[m] * bias[n][g] on fp32 MFMA
   // (v_mfma_f32_32x32x2_f32: k-slot kk of lane l is group g0 + 2 q + kk, kk = l / 32; its output
   // layout is the one of the 32x32x16 tiles). Called with every wavefront past the barrier that
   // follows the last of those groups' row sums.
   auto flush_bias = [&](int g0, int count) {
     // every operand first (one LDS round trip), then the MFMAs of the live pairs
-    float a1v[kBiasChunk / 2], a2v[kBiasChunk / 2], bv[kBiasChunk / 2][2];
+    float av[kBiasChunk / 2][4], bv[kBiasChunk / 2];
 #pragma unroll
     for (int q2 = 0; q2 < kBiasChunk / 2; ++q2) {
       const int q = 2 * q2 + hh;  // this lane's k-slot: group g0 + q
       const bool live = q < count;
       const int qc = live ? q : 0;  // a dead slot reads a live one and uses zeros
-      a1v[q2] = live ? xg_lds[qc][wm * 64 + 32 * t1 + l32] : 0.0f;
-      a2v[q2] = live ? xg_lds[qc][wm * 64 + 32 * t2 + l32] : 0.0f;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int col = wn * 64 + 32 * j + l32;
-        bv[q2][j] =
-            live ? word_value<BF16>(sbuf[128 * groups + col * groups + g0 + qc]) : 0.0f;
-      }
+      for (int k = 0; k < 4; ++k) av[q2][k] = live ? xg_lds[qc][32 * rtile(k) + l32] : 0.0f;
+      bv[q2] = live ? word_value<BF16>(sbuf[128 * groups + col * groups + g0 + qc]) : 0.0f;
     }
 #pragma unroll
     for (int q2 = 0; q2 < kBiasChunk / 2; ++q2) {
       if (2 * q2 >= count) break;  // wavefront-uniform
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        acc1[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1v[q2], bv[q2][j], acc1[j], 0, 0, 0);
-        acc2[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a2v[q2], bv[q2][j], acc2[j], 0, 0, 0);
-      }
+      for (int k = 0; k < 4; ++k)
+        acc[k] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q2][k], bv[q2], acc[k], 0, 0, 0);
     }
   };
 
-  // Row sums on v_mfma_f32_16x16x32_f16 from the 32x32x16 A registers of tile t1: read as a
+  // Row sums on v_mfma_f32_16x16x32_f16 from the 32x32x16 A registers of tile r_0: read as a
   // 16x16x32 operand, lane (r = l % 16, q = l / 16) holds 8 values of row r + 16 (q & 1). The B
   // operand sel[k][n] = 1 where n = (k / 8) & 1 (else 0) sends rows r to column 0 and rows r + 16 to
   // column 1, so over the four k-steps D[r][0] = X_g[r] and D[r][1] = X_g[r + 16]; lanes with
   // l % 16 < 2 hold them, four rows each.
   const _Float16 selv = (lane & 15) == ((lane >> 4) & 1) ? _Float16(1) : _Float16(0);
   const half8 sel = {selv, selv, selv, selv, selv, selv, selv, selv};
-  const int xg_row = wm * 64 + 32 * t1 + 16 * (lane & 1) + 4 * (lane >> 4);
-
-  // LDS offsets (halves) of the lane's A operand in the two tiles; the swizzle depends on l32 only
-  const int arow1 = wm * 64 + 32 * t1 + l32, arow2 = wm * 64 + 32 * t2 + l32;
+  const int xg_row = 32 * wave + 16 * (lane & 1) + 4 * (lane >> 4);
 
   issue(GroupStage<0>{}, 0);
   if (groups > 1) issue(GroupStage<1>{}, 1);
 
-  // Products of the previous group's second tile and its scales, folded during the next group's
-  // first-tile MFMAs (zero before the first group).
-  floatx16 p2[2];
-  float gs_prev[2] = {0.0f, 0.0f};
+  // Products of tile r_k are folded while the MFMAs of the next tile run: p[k % 2] holds them.
+  // Before the first group the pending tile (r_3 of group -1) is zero with scale zero.
+  floatx16 p[2];
+  float gs_prev = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) p2[j][e] = 0.0f;
+  for (int e = 0; e < 16; ++e) p[1][e] = 0.0f;
 
   // One group: its tiles live in stage g % 3; group g + 2 goes to stage (g + 2) % 3. The stage is a
   // compile-time constant (the loop below is unrolled by the ring depth).
@@ -278,75 +267,45 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
       flush_bias(g - kBiasChunk, kBiasChunk);
       stage_barrier();
     }
-    // the lane's four weight words of this group (column block, k half, column) and the scales
-    uint4v wd[2];
-    float gs[2];
+    // the lane's four weight words of this group (column block, k half, column) and its scale
+    const uint4v wd = *reinterpret_cast<const uint4v*>(&ws[st][256 * wave + 128 * hh + 4 * l32]);
+    const float gs = word_value<BF16>(sbuf[col * groups + g]);
+    half8 bq[4];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = wn * 64 + 32 * j + l32;
-      wd[j] = *reinterpret_cast<const uint4v*>(&ws[st][256 * (2 * wn + j) + 128 * hh + 4 * l32]);
-      gs[j] = word_value<BF16>(sbuf[col * groups + g]);
-    }
-    half8 bq[2][4];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4)
-        bq[j][s4] = decode_codes(wd[j][s4]);
+    for (int s4 = 0; s4 < 4; ++s4) bq[s4] = decode_codes(wd[s4]);
 
-    // ---- tile t1: A_g and the row sums; meanwhile fold the previous group's tile t2 ----
-    floatx16 p1[2];
     floatx4 xg = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-      const half8 av =
-          *reinterpret_cast<const half8*>(&xs[st][arow1 * 64 + 8 * ((4 * hh + s4) ^ xsw(l32))]);
+    for (int k = 0; k < 4; ++k) {
+      const int arow = 32 * rtile(k) + l32;  // the swizzle depends on l32 only
+      floatx16& pk = p[k & 1];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        if (s4 == 0)
-          p1[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bq[j][0], floatx16{}, 0, 0, 0);
-        else
-          p1[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bq[j][s4], p1[j], 0, 0, 0);
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const half8 av =
+            *reinterpret_cast<const half8*>(&xs[st][arow * 64 + 8 * ((4 * hh + s4) ^ xsw(l32))]);
+        pk = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bq[s4], s4 ? pk : floatx16{}, 0, 0, 0);
+        if (k == 0) xg = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, sel, xg, 0, 0, 0);
       }
-      xg = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, sel, xg, 0, 0, 0);
+      // fold the previous tile (r_{k-1}, or r_3 of the previous group) while these MFMAs run
+      floatx16& pp = p[(k + 1) & 1];
+      floatx16& ap = acc[(k + 3) & 3];
+      const float gp = k == 0 ? gs_prev : gs;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) ap[e] = fmaf(gp, pp[e], ap[e]);
     }
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc2[j][e] = fmaf(gs_prev[j], p2[j][e], acc2[j][e]);
-
-    // ---- tile t2; meanwhile fold tile t1 ----
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-      const half8 av =
-          *reinterpret_cast<const half8*>(&xs[st][arow2 * 64 + 8 * ((4 * hh + s4) ^ xsw(l32))]);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        if (s4 == 0)
-          p2[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bq[j][0], floatx16{}, 0, 0, 0);
-        else
-          p2[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bq[j][s4], p2[j], 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc1[j][e] = fmaf(gs[j], p1[j][e], acc1[j][e]);
-    gs_prev[0] = gs[0];
-    gs_prev[1] = gs[1];
-    // instruction order of the block above: LDS reads, the decode, then each MFMA followed by a
-    // few VALU instructions (the folds), so the folds run while the MFMAs do
-    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // LDS reads
-    __builtin_amdgcn_sched_group_barrier(0x002, 56, 0);  // VALU: decode
-#pragma unroll
-    for (int k = 0; k < 12; ++k) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (tile t1, row sums)
-      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU (fold of the previous t2)
-    }
+    gs_prev = gs;
+    // instruction order of the block above: the decode, then each MFMA followed by a few VALU
+    // instructions (the folds), so the folds run while the MFMAs do
+    __builtin_amdgcn_sched_group_barrier(0x002, 28, 0);  // VALU: decode
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (tile t2)
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU (fold of t1)
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (tile r_0, row sums)
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU (fold of r_3 of the last group)
+    }
+#pragma unroll
+    for (int k = 0; k < 12; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (tiles r_1 .. r_3)
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU (fold of the tile before)
     }
     float* xg_dst = (lane & 15) < 2 ? &xg_lds[g % kBiasChunk][xg_row] : &xg_lds[kBiasChunk][4 * lane];
     *reinterpret_cast<floatx4*>(xg_dst) = xg;
@@ -357,28 +316,20 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
     if (g + 2 < groups) step(g + 2, GroupStage<2>{});
   }
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc2[j][e] = fmaf(gs_prev[j], p2[j][e], acc2[j][e]);
+  for (int e = 0; e < 16; ++e) acc[3][e] = fmaf(gs_prev, p[1][e], acc[3][e]);
   // the last chunk's row sums: written before this barrier, read after it
   stage_barrier();
   flush_bias(groups - (groups - 1) % kBiasChunk - 1, (groups - 1) % kBiasChunk + 1);
 
   // ---- store y[m][n] = acc as fp16 ----
-  auto store_tile = [&](const floatx16& t, int tile_row, int j) {
-    const int n = nw + 32 * j + l32;
+  const int n = tile * 128 + col;
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int m = m0 + wm * 64 + 32 * tile_row + 8 * (e >> 2) + 4 * hh + (e & 3);
-      if (m < M)
-        y[static_cast<size_t>(m) * N + n] = static_cast<_Float16>(t[e]);
+      const int m = m0 + 32 * rtile(k) + 8 * (e >> 2) + 4 * hh + (e & 3);
+      if (m < M) y[static_cast<size_t>(m) * N + n] = static_cast<_Float16>(acc[k][e]);
     }
-  };
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    store_tile(acc1[j], t1, j);
-    store_tile(acc2[j], t2, j);
-  }
 }
 
 
