@@ -26,7 +26,8 @@
 // weight word is decoded once per workgroup; linear4_hilo: 64 rows, a 2 x 2 grid of 32 x 64.
 // qkv4_f16 pipelines the K/64 groups through a three-stage LDS ring: x (128 x 64 fp16) and the
 // tile's packed weight words of group g + 2 are copied by global_load_lds_dwordx4 while group g
-// runs, one barrier per group; the scales and biases of all groups arrive once, up front. Each
+// runs, one barrier per group; the scales and biases of all groups arrive once, up front,
+// transposed to [group][column] (conflict-free per-group reads). Each
 // wavefront folds one 32-row tile on the VALU while the MFMAs run the next, and keeps the row
 // sums of one tile (the four wavefronts cover the 128 rows) in LDS for the bias GEMM.
 // x rows are XOR-swizzled in LDS by (row >> 1) & 7 over their 16-byte chunks: the 16 rows read by
@@ -102,6 +103,31 @@ __device__ __forceinline__ void load16_at(floatx4& dst, const void* base, uint32
                : "memory");
 }
 
+// Scale and bias words of a 128-column tile, all groups, into LDS transposed to
+// [part][group][column] (part 0 scales, 1 biases): the lanes of a column block then read one
+// group's words from consecutive addresses (in the global [N, groups] layout they are `groups`
+// words apart, an 8- to 16-way LDS bank conflict). Thread t copies column t % 128 of part t / 128
+// with ordinary loads; callers issue it before any LDS DMA of theirs and wait for the LDS writes
+// (lgkmcnt) before the barrier that publishes them.
+__device__ __forceinline__ void copy_scales_transposed(uint16_t* sbuf, const uint16_t* sc,
+                                                       const uint16_t* bi, int tile, int groups) {
+  const int tid = threadIdx.x, part = tid >> 7, col = tid & 127;
+  const uint16_t* src = (part ? bi : sc) + static_cast<size_t>(tile * 128 + col) * groups;
+  uint16_t* dst = sbuf + part * 128 * groups + col;
+  if (groups % 8 == 0) {  // 16-byte rows of 8 groups (the row starts are 16-byte aligned)
+    for (int g8 = 0; g8 < groups; g8 += 8) {
+      const uint4v v = *reinterpret_cast<const uint4v*>(src + g8);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dst[(g8 + 2 * i) * 128] = static_cast<uint16_t>(v[i] & 0xffffu);
+        dst[(g8 + 2 * i + 1) * 128] = static_cast<uint16_t>(v[i] >> 16);
+      }
+    }
+  } else {
+    for (int g = 0; g < groups; ++g) dst[g * 128] = src[g];
+  }
+}
+
 // s_waitcnt vmcnt(N); the four registers count as written here, so nothing reads them earlier.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt_pin(floatx4 (&r)[4]) {
@@ -136,7 +162,7 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
   // the stores of the lanes that hold no row sum (a store from every lane keeps the loop body
   // one basic block)
   __shared__ __attribute__((aligned(16))) float xg_lds[kBiasChunk + 2][128];
-  // scale and bias words of the tile's 128 columns, all groups: [2][128][groups] (dynamic size)
+  // scale and bias words of the tile's 128 columns, all groups: [2][groups][128] (dynamic size)
   extern __shared__ __attribute__((aligned(1024))) uint16_t sbuf[];
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -181,21 +207,9 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
     for (int j = 0; j < 4; ++j) dma16_at(xbase, xoff[j], &xs[st][(4 * wave + j) * 512]);
     dma16_at(w + 8 * g, woff, reinterpret_cast<_Float16*>(&ws[st][256 * wave]));
   };
-  // ---- scales and biases of the tile's columns, all groups: two contiguous runs of
-  // 128 * groups words (rows tile*128 .. +127 of [N, groups]), 16 bytes per lane, issued once
-  {
-    const int chunks = 128 * groups / 8;  // 16-byte chunks per run
-    const uint16_t* srcs[2] = {sc + static_cast<size_t>(tile * 128) * groups,
-                               bi + static_cast<size_t>(tile * 128) * groups};
-#pragma unroll
-    for (int part = 0; part < 2; ++part)
-      for (int blk = wave; blk * 64 < chunks; blk += 4) {
-        const int chunk = blk * 64 + lane;
-        if (chunk < chunks)
-          dma16(srcs[part] + 8 * chunk,
-                reinterpret_cast<_Float16*>(sbuf + part * 128 * groups + blk * 512));
-      }
-  }
+  // ---- scales and biases of the tile's columns, all groups, transposed into LDS once ----
+  copy_scales_transposed(sbuf, sc, bi, tile, groups);
+  wait_lgkmcnt<0>();  // published by the first group's barrier
 
   // Each wavefront owns the tile's 32 columns 32 w .. 32 w + 31 (its weight block: each weight
   // word is decoded once per workgroup) and all 128 rows, as four 32-row tiles taken in the
@@ -222,7 +236,7 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
       const int qc = live ? q : 0;  // a dead slot reads a live one and uses zeros
 #pragma unroll
       for (int k = 0; k < 4; ++k) av[q2][k] = live ? xg_lds[qc][32 * rtile(k) + l32] : 0.0f;
-      bv[q2] = live ? word_value<BF16>(sbuf[128 * groups + col * groups + g0 + qc]) : 0.0f;
+      bv[q2] = live ? word_value<BF16>(sbuf[128 * groups + (g0 + qc) * 128 + col]) : 0.0f;
     }
 #pragma unroll
     for (int q2 = 0; q2 < kBiasChunk / 2; ++q2) {
@@ -269,7 +283,7 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
     }
     // the lane's four weight words of this group (column block, k half, column) and its scale
     const uint4v wd = *reinterpret_cast<const uint4v*>(&ws[st][256 * wave + 128 * hh + 4 * l32]);
-    const float gs = word_value<BF16>(sbuf[col * groups + g]);
+    const float gs = word_value<BF16>(sbuf[g * 128 + col]);
     half8 bq[4];
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) bq[s4] = decode_codes(wd[s4]);
@@ -381,7 +395,8 @@ constexpr int kHiloChunk = 16;
 //     kHiloChunk row sums in LDS, flushed every kHiloChunk groups.
 // Memory: the tile's packed weight words ride a three-stage LDS ring (global_load_lds_dwordx4,
 // group g + 2 issued during group g, the qkv4_f16 layout); the scales and biases of all groups
-// arrive in LDS once, up front; fp32 x is prefetched two groups ahead in two register sets.
+// arrive in LDS once, up front, transposed to [group][column]; fp32 x is prefetched two groups
+// ahead in two register sets.
 // 64-row tiles keep two workgroups on every CU down to 8 column tiles x 4096 rows.
 __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__ x,
                                                       const float* __restrict__ rs,
@@ -393,7 +408,7 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
   __shared__ __attribute__((aligned(1024))) _Float16 xs[2][2][TM * 64];  // [stage][hi, lo]
   __shared__ __attribute__((aligned(1024))) uint32_t ws[3][128 * 8];      // qkv4_f16 layout
   __shared__ __attribute__((aligned(16))) float xg_lds[kHiloChunk][TM];
-  // scale and bias words of the tile's 128 columns, all groups: [2][128][groups] (dynamic size)
+  // scale and bias words of the tile's 128 columns, all groups: [2][groups][128] (dynamic size)
   extern __shared__ __attribute__((aligned(1024))) uint16_t sbuf[];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
@@ -404,20 +419,10 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
   const int nw = tile * 128 + wn * 64;
   const int wrow = wm * 32;  // wavefront's rows in the tile
 
-  // ---- scales and biases: two contiguous runs of 128 * groups words, 16 bytes per lane ----
-  {
-    const int chunks = 128 * groups / 8;
-    const uint16_t* srcs[2] = {sc + static_cast<size_t>(tile * 128) * groups,
-                               bi + static_cast<size_t>(tile * 128) * groups};
-#pragma unroll
-    for (int part = 0; part < 2; ++part)
-      for (int blk = wave; blk * 64 < chunks; blk += 4) {
-        const int chunk = blk * 64 + lane;
-        if (chunk < chunks)
-          dma16(srcs[part] + 8 * chunk,
-                reinterpret_cast<_Float16*>(sbuf + part * 128 * groups + blk * 512));
-      }
-  }
+  // ---- scales and biases of the tile's columns, all groups, transposed into LDS once (before
+  // any of this kernel's asm loads: the memory-wait counts below assume none older) ----
+  copy_scales_transposed(sbuf, sc, bi, tile, groups);
+  wait_lgkmcnt<0>();  // published by the first group's barrier
 
   // ---- staging role: row srow of the tile, floats 16 * spart .. +15 of each group ----
   const int srow = tid >> 2, spart = tid & 3;
@@ -486,7 +491,7 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int col = wn * 64 + 32 * j + l32;
-        bw[q2][j] = live ? bf16_to_float(sbuf[128 * groups + col * groups + g0 + qc]) : 0.0f;
+        bw[q2][j] = live ? bf16_to_float(sbuf[128 * groups + (g0 + qc) * 128 + col]) : 0.0f;
       }
     }
 #pragma unroll
@@ -498,8 +503,8 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
     }
   };
 
-  // Memory instructions in issue order (the memory counter retires in order): scales / biases
-  // (above); x of group 0; then x of group k + 1 right before the weights of group k, for every
+  // Memory instructions in issue order (the memory counter retires in order; the scale / bias
+  // loads above have completed): x of group 0; then x of group k + 1 right before the weights of group k, for every
   // k. The prologue issues x(1), w(0), stages group 0, then x(2), w(1); step g issues x(g + 3),
   // w(g + 2) (both clamped to the last group). So at the start of step g the weights of group g
   // have exactly 5 younger memory instructions (x(g + 2), w(g + 1)), and x(g + 1), issued before
@@ -534,7 +539,7 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
     for (int j = 0; j < 2; ++j) {
       const int col = wn * 64 + 32 * j + l32;
       wd[j] = *reinterpret_cast<const uint4v*>(&ws[st][256 * (2 * wn + j) + 128 * hh + 4 * l32]);
-      gs[j] = bf16_to_float(sbuf[col * groups + g]);
+      gs[j] = bf16_to_float(sbuf[g * 128 + col]);
     }
     // stage group g + 1 from its register set, refill that set with group g + 3, then the
     // weights of group g + 2 into the ring stage group g - 1 used
