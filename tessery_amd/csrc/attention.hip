@@ -260,8 +260,9 @@ constexpr float kMaxSlack = 8.0f;
 // A workgroup takes two row blocks of 32 query rows that share the KV head (two query heads of
 // a GQA group, or two position blocks) and splits their keys: wavefront 2h + r runs row block r
 // over the key tiles h, h + 2, h + 4, ... (half h), each half staging its own 32-key tiles
-// (K and V padded to D+4 floats per row: rows 4 banks apart, conflict-free 16-byte reads),
-// the next tile prefetched into registers while the current one is consumed. The two halves of a
+// (K padded to D+4 floats per row: rows 4 banks apart, conflict-free 16-byte reads; V rows with
+// the four 32-channel output tiles interleaved, one 16-byte read per key step), the next tile
+// prefetched into registers while the current one is consumed. The two halves of a
 // row block end with their own (O, running max, sum); half 1 passes them through LDS and half 0
 // merges them in that fixed order (deterministic). The longest work item is half a row block's
 // keys, and the workgroups outnumber the CU slots, so causal and ragged planes balance.
@@ -280,7 +281,10 @@ __global__ __launch_bounds__(256, 2) void attn_f32_split(const float* __restrict
   constexpr int CPT = (CH + 127) / 128;    // chunks per thread of a half (128 threads)
   constexpr int HALF = D / 2;
   __shared__ __attribute__((aligned(16))) float Ks[2][KT * ROW];
-  __shared__ __attribute__((aligned(16))) float Vs[2][KT * ROW];
+  // V rows hold channel d at 4 (d % 32) + d / 32: one 16-byte read gives a lane its channels
+  // l, l + 32, l + 64, l + 96, the A operands of the four output tiles at one key step
+  __shared__ __attribute__((aligned(16))) float Vs[2][KT * D];
+  static_assert(D == 128, "the V interleave assumes four 32-channel output tiles");
   static_assert(2 * KT * ROW >= 2 * (D / 32 * 16 + 2) * 64, "merge exchange fits in Ks");
 
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
@@ -334,26 +338,48 @@ __global__ __launch_bounds__(256, 2) void attn_f32_split(const float* __restrict
       vreg[i] = vz;
     }
   };
-  if (niter > 0) load_tile(half);
-
   float* const kh = Ks[half];
   float* const vh = Vs[half];
-  for (int it = 0; it < niter; ++it) {
-    const int kt = 2 * it + half;
-    __syncthreads();
+  auto store_k = [&] {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = ht + 128 * i;
       if (c < CH) {
         const int key = c / (D / 4), ck = c % (D / 4);
         *reinterpret_cast<floatx4*>(&kh[key * ROW + 4 * ck]) = kreg[i];
-        *reinterpret_cast<floatx4*>(&vh[key * ROW + 4 * ck]) = vreg[i];
       }
     }
-    __syncthreads();
-    if (it + 1 < niter) load_tile(kt + 2);
-    if (kt < ntiles && kt * KT < g.wave_end) {
-      floatx16 s;
+  };
+  auto store_v = [&] {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = ht + 128 * i;
+      if (c < CH) {
+        const int key = c / (D / 4), ck = c % (D / 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int d = 4 * ck + j;
+          vh[key * D + 4 * (d & 31) + (d >> 5)] = vreg[i][j];
+        }
+      }
+    }
+  };
+  // Tile kt = 2 it + half. K of the next tile goes to LDS as soon as every wavefront is past the
+  // S phase (between the two barriers), V after the P V phase, so the K registers are free
+  // during P V; the loads of the tile after are issued right after the V store.
+  if (niter > 0) {
+    load_tile(half);
+    store_k();
+    store_v();
+    if (niter > 1) load_tile(half + 2);
+  }
+  __syncthreads();
+  for (int it = 0; it < niter; ++it) {
+    const int kt = 2 * it + half;
+    const bool work = kt < ntiles && kt * KT < g.wave_end;
+    floatx16 s;
+    float corr = 1.0f;
+    if (work) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[e] = 0.0f;
 #pragma unroll
@@ -376,7 +402,7 @@ __global__ __launch_bounds__(256, 2) void attn_f32_split(const float* __restrict
       const float m_tile = fmaxf(mloc, __shfl_xor(mloc, 32));
       const float m_new = fmaxf(m_run, m_tile);
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+      corr = __builtin_amdgcn_exp2f(m_run - m_use);
       float lsum = 0.0f;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
@@ -387,6 +413,10 @@ __global__ __launch_bounds__(256, 2) void attn_f32_split(const float* __restrict
       lsum += __shfl_xor(lsum, 32);
       l_run = l_run * corr + lsum;
       m_run = m_new;
+    }
+    __syncthreads();  // every wavefront is past its S phase: K of the next tile may land
+    if (it + 1 < niter) store_k();
+    if (work) {
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
@@ -394,11 +424,16 @@ __global__ __launch_bounds__(256, 2) void attn_f32_split(const float* __restrict
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int key = 8 * (e >> 2) + 4 * hh + (e & 3);
+        const floatx4 vv = *reinterpret_cast<const floatx4*>(&vh[key * D + 4 * l32]);
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt)
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vh[key * ROW + 32 * dt + l32], s[e], o[dt],
-                                                       0, 0, 0);
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[dt], s[e], o[dt], 0, 0, 0);
       }
+    }
+    __syncthreads();  // every wavefront is past its P V phase: V of the next tile may land
+    if (it + 1 < niter) {
+      store_v();
+      if (it + 2 < niter) load_tile(kt + 4);
     }
   }
 
