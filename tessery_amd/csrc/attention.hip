@@ -175,11 +175,28 @@ __device__ __forceinline__ void ranked_plane(uint32_t len, int B, int S, int KV,
   sc.L = static_cast<int>(__builtin_amdgcn_readlane(len, sc.b));
 }
 
-__device__ __forceinline__ Sched schedule(const uint32_t* lengths, int B, int S, int KV, Div kvdiv) {
+// An XCD's k-th workgroup in dispatch order (k = y + wpp * z) starts on CU k mod 32 of that XCD
+// when a launch fills an idle MI355X (32 CUs per XCD; measured), so workgroups k, k + 32, k + 64
+// and k + 96 share a CU. Items come heaviest first (longest planes, last query blocks first); with
+// wpp a divisor of 32 (16 blocks per plane at S = 512, D = 128) a CU would get four items of the
+// same block index, four long ones on some CUs and four short ones on others. Odd runs of 32 are
+// therefore taken in reverse order (k -> k ^ 31 when the whole run exists), which deals every CU
+// a long and a short item from each pair of runs. serp = 0 (set by the launcher when k / wpp
+// would not be exact by Div) keeps the grid's order.
+__device__ __forceinline__ Sched schedule(const uint32_t* lengths, int B, int S, int KV, Div kvdiv,
+                                          Div wppdiv, int serp) {
   Sched sc;
   if (sched_ranked(B, KV)) {
-    const int j = static_cast<int>(blockIdx.z) * 8 + static_cast<int>(blockIdx.x);  // plane rank
-    sc.wgp = static_cast<int>(gridDim.y - 1 - blockIdx.y);
+    const int wpp = static_cast<int>(gridDim.y), n = wpp * static_cast<int>(gridDim.z);
+    int y = static_cast<int>(blockIdx.y), z = static_cast<int>(blockIdx.z);
+    if (serp) {
+      int k = y + wpp * z;
+      if (((k >> 5) & 1) && (k | 31) < n) k ^= 31;
+      z = quot(k, wppdiv);
+      y = k - z * wpp;
+    }
+    const int j = z * 8 + static_cast<int>(blockIdx.x);  // plane rank
+    sc.wgp = wpp - 1 - y;
     ranked_plane(lane_length(lengths, B, S), B, S, KV, kvdiv, j, sc);
   } else {
     sc.b = static_cast<int>(blockIdx.z);
@@ -198,7 +215,8 @@ struct Geom {
 // Host-computed divisors of the fp32 kernel's geometry (G = H / KV query heads per kv head).
 struct F32Shape {
   int G;
-  Div g, kv;
+  Div g, kv, wpp;  // wpp: workgroups per plane of the launch grid
+  int serp;         // serpentine item order on (see schedule)
 };
 
 // Row block rb = wgp * RBW + sub of the plane (RBW row blocks per workgroup).
@@ -208,7 +226,7 @@ __device__ __forceinline__ Geom make_geom(const uint32_t* lengths, int B, int S,
   Geom g;
   const int G = sh.G;
   const int nrb = G * ((S + 31) / 32);
-  const Sched sc = schedule(lengths, B, S, KV, sh.kv);
+  const Sched sc = schedule(lengths, B, S, KV, sh.kv, sh.wpp, sh.serp);
   const int wgp = sc.wgp;
   g.b = sc.b;
   g.kvh = sc.kvh;
@@ -671,7 +689,8 @@ __host__ __device__ inline int f16_wave_blocks(int S, int G) {
 // blocks per plane.
 struct F16Shape {
   int G, hsh, nwb;
-  Div kv, hbn;  // KV and G >> hsh (head blocks per position block)
+  Div kv, hbn, wpp;  // KV, G >> hsh (head blocks per position block), workgroups per plane
+  int serp;          // serpentine item order on (see schedule)
 };
 
 __device__ __forceinline__ Geom16 geom16_of(const Sched& sc, int bidi, int wave, F16Shape sh) {
@@ -725,6 +744,20 @@ __device__ __forceinline__ float dot_ones(half4 p, float acc) {
   const h2 one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
   acc = __builtin_amdgcn_fdot2(h2{p[0], p[1]}, one, acc, false);
   return __builtin_amdgcn_fdot2(h2{p[2], p[3]}, one, acc, false);
+}
+
+// x0 * sc and x1 * sc rounded to fp16 and packed (hi), and the fp16 of what hi leaves of each
+// (lo = fp16(x * sc - hi), the product exact inside the fma): four v_fma_mix instructions. The
+// lo/hi forms write one half of the destination and keep the other, so each packed pair is built
+// in place; hi's halves enter the lo fmas as fp16 operands (op_sel picks the upper half).
+__device__ __forceinline__ void scaled_split2(float x0, float x1, float sc, uint32_t& hi,
+                                              uint32_t& lo) {
+  asm("v_fma_mixlo_f16 %0, %2, %4, 0\n\t"
+      "v_fma_mixhi_f16 %0, %3, %4, 0\n\t"
+      "v_fma_mixlo_f16 %1, %2, %4, -%0 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixhi_f16 %1, %3, %4, -%0 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+      : "=&v"(hi), "=&v"(lo)
+      : "v"(x0), "v"(x1), "v"(sc));
 }
 
 // The score accumulators of a QK^T chain are read by VALU (row max, masking) right after the last
@@ -894,25 +927,40 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
   if (ntiles > 1) issue(1, 1);
 
   // ---- Q fragment: lane (r, g) holds channels 32s + 8g .. +7 of query r ---------------------
-  const size_t qbase = ((static_cast<size_t>(g.b) * S + qpos_c) * H + qhead) * D + 8 * gq;
-  half8 qh[NS], ql[FUSED ? NS : 1];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) qh[s] = *reinterpret_cast<const half8*>(q + qbase + 32 * s);
-  uint4v gw[FUSED ? NS : 1];
-  floatx4 cs[FUSED ? NS / 2 : 1][2], sn[FUSED ? NS / 2 : 1][2];
+  // FUSED: the gamma words and the cos / sin of the lane's channels (table rows are [D/2] fp32
+  // per position; channel c < D/2 of step s is 32s + 8g + j, j < 8: two 16-byte chunks) go out
+  // first, as asm loads: the compiler would otherwise sink them past the q-dependent row sum into
+  // the tile loop's entry block, putting an L2 round trip behind the q load. The compiler does
+  // not know they are in flight, so their first use is ordered after an explicit vmcnt(0) that
+  // takes the registers as operands (wait_vmcnt_pin6).
+  // tab: gamma [0, NS) (bf16 words, channels 32s + 8g..+7), cos [NS, 2NS), sin [2NS, 3NS) with
+  // entry NS + 2s + h holding channels 32s + 8g + 4h..+3.
+  floatx4 tab[FUSED ? 3 * NS : 1];
   if constexpr (FUSED) {
-    const float* ct = rope_cos + static_cast<size_t>(qpos_c) * (D / 2) + 8 * gq;
-    const float* stt = rope_sin + static_cast<size_t>(qpos_c) * (D / 2) + 8 * gq;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) gw[s] = *reinterpret_cast<const uint4v*>(gamma + 32 * s + 8 * gq);
-#pragma unroll
-    for (int s = 0; s < NS / 2; ++s) {
-      cs[s][0] = *reinterpret_cast<const floatx4*>(ct + 32 * s);
-      cs[s][1] = *reinterpret_cast<const floatx4*>(ct + 32 * s + 4);
-      sn[s][0] = *reinterpret_cast<const floatx4*>(stt + 32 * s);
-      sn[s][1] = *reinterpret_cast<const floatx4*>(stt + 32 * s + 4);
+    const uint32_t goff = static_cast<uint32_t>(16 * gq);
+    const uint32_t toff = static_cast<uint32_t>((qpos_c * (D / 2) + 8 * gq) * 4);
+    load16_at<0>(tab[0], gamma, goff);
+    load16_at<64>(tab[1], gamma, goff);
+    load16_at<0>(tab[NS], rope_cos, toff);
+    load16_at<16>(tab[NS + 1], rope_cos, toff);
+    load16_at<0>(tab[2 * NS], rope_sin, toff);
+    load16_at<16>(tab[2 * NS + 1], rope_sin, toff);
+    if constexpr (NS == 4) {
+      load16_at<128>(tab[2], gamma, goff);
+      load16_at<192>(tab[3], gamma, goff);
+      load16_at<128>(tab[NS + 2], rope_cos, toff);
+      load16_at<144>(tab[NS + 3], rope_cos, toff);
+      load16_at<128>(tab[2 * NS + 2], rope_sin, toff);
+      load16_at<144>(tab[2 * NS + 3], rope_sin, toff);
     }
   }
+  // q rows of one batch row lie within S * H * D halves (below 2^31 bytes, checked by the
+  // launcher): a per-lane 32-bit offset from the batch row's base
+  const _Float16* qrow = q + static_cast<size_t>(g.b) * S * H * D;
+  const uint32_t qoff = static_cast<uint32_t>((qpos_c * H + qhead) * D + 8 * gq);
+  half8 qh[NS], ql[FUSED ? NS : 1];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) qh[s] = *reinterpret_cast<const half8*>(qrow + qoff + 32 * s);
   float one = 1.0f;  // opaque 1.0 for split2
   asm("" : "+v"(one));
   int vzero = 0;  // opaque 0: two reads of one V fragment stay two reads
@@ -920,9 +968,9 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
   if constexpr (FUSED) {
     // RMSNorm over the row (four lanes) then split-half RoPE: channel c < D/2 of step s pairs
     // with channel c + D/2 of step s + NS/2 in the same lane (kernels.metal:53-63, :65-74).
-    // fp32 math; the fp16 q enters v_fma_mix directly and 1/rms is folded into cos and sin:
-    //   A = q_c g_c, B = q_{c+D/2} g_{c+D/2}, (A, B) -> (A cos' - B sin', A sin' + B cos')
-    // with cos' = cos / rms, sin' = sin / rms. Then hi = fp16(x), lo = fp16(x - hi).
+    // fp32 math; the fp16 q enters v_fma_mix directly:
+    //   A = q_c g_c, B = q_{c+D/2} g_{c+D/2}, (A, B) -> x = (A cos - B sin, A sin + B cos)
+    // and 1/rms is applied as x is rounded: hi = fp16(x / rms), lo = fp16(x / rms - hi).
     // sum of squares with v_dot2_f32_f16 on the packed pairs (fp16 products are exact in fp32)
     float ss = 0.0f;
 #pragma unroll
@@ -934,7 +982,9 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
       }
     ss = rowsum4(ss);
     const float inv = __builtin_amdgcn_rsqf(ss * (1.0f / static_cast<float>(D)) + eps);
-    half2v hv[NS][4], lv[NS][4];  // packed channel pairs (m, m + 1)
+    wait_vmcnt_pin6<0>(tab);
+    if constexpr (NS == 4) wait_vmcnt_pin6<0>(tab + 6);
+    uint32_t hv[NS][4], lv[NS][4];  // word m / 2 of step s: channels (m, m + 1) packed
 #pragma unroll
     for (int s = 0; s < NS / 2; ++s)
 #pragma unroll
@@ -942,28 +992,26 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
         float r[2][2];  // [first / second half of the row][channel m, m + 1]
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          const uint32_t w0 = gw[s][m >> 1], w1 = gw[s + NS / 2][m >> 1];
+          const uint32_t w0 = __float_as_uint(tab[s][m >> 1]);
+          const uint32_t w1 = __float_as_uint(tab[s + NS / 2][m >> 1]);
           const float g0 = __uint_as_float(e ? (w0 & 0xffff0000u) : (w0 << 16));
           const float g1 = __uint_as_float(e ? (w1 & 0xffff0000u) : (w1 << 16));
           const float a = fmaf(static_cast<float>(qh[s][m + e]), g0, 0.0f);
           const float bb = fmaf(static_cast<float>(qh[s + NS / 2][m + e]), g1, 0.0f);
-          const float cv = cs[s][m >> 2][(m & 3) + e] * inv, sv = sn[s][m >> 2][(m & 3) + e] * inv;
+          const float cv = tab[NS + 2 * s + (m >> 2)][(m & 3) + e];
+          const float sv = tab[2 * NS + 2 * s + (m >> 2)][(m & 3) + e];
           r[0][e] = fmaf(a, cv, -(bb * sv));
           r[1][e] = fmaf(a, sv, bb * cv);
         }
 #pragma unroll
         for (int half = 0; half < 2; ++half)
-          split2(r[half][0], r[half][1], one, hv[s + half * (NS / 2)][m >> 1],
-                 lv[s + half * (NS / 2)][m >> 1]);
+          scaled_split2(r[half][0], r[half][1], inv, hv[s + half * (NS / 2)][m >> 1],
+                        lv[s + half * (NS / 2)][m >> 1]);
       }
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      qh[s] = __builtin_shufflevector(__builtin_shufflevector(hv[s][0], hv[s][1], 0, 1, 2, 3),
-                                      __builtin_shufflevector(hv[s][2], hv[s][3], 0, 1, 2, 3),
-                                      0, 1, 2, 3, 4, 5, 6, 7);
-      ql[s] = __builtin_shufflevector(__builtin_shufflevector(lv[s][0], lv[s][1], 0, 1, 2, 3),
-                                      __builtin_shufflevector(lv[s][2], lv[s][3], 0, 1, 2, 3),
-                                      0, 1, 2, 3, 4, 5, 6, 7);
+      qh[s] = __builtin_bit_cast(half8, uint4v{hv[s][0], hv[s][1], hv[s][2], hv[s][3]});
+      ql[s] = __builtin_bit_cast(half8, uint4v{lv[s][0], lv[s][1], lv[s][2], lv[s][3]});
     }
   }
   // Rows past S read row S - 1 (finite data) and are never stored; query columns do not mix in
@@ -973,6 +1021,17 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.0f;
+
+  // Rescale of the accumulated output and row sum when the running max moves by d (<= 0). Called
+  // under a wave-uniform branch; the opaque copy of d keeps the exponential (a quarter-rate
+  // instruction) inside it instead of being computed on every tile.
+  auto rescale = [&](float d) {
+    asm volatile("" : "+v"(d));
+    const float corr = __builtin_amdgcn_exp2f(d);
+    l_run *= corr;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
+  };
 
   // QK^T of one 16-key block whose rows start at kr (rows kr..kr+15 of the K tile)
   auto qk_block = [&](const _Float16* kt0, int kr) {
@@ -1021,10 +1080,9 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
       const bool grow = mloc > m_run + kMaxSlack;
       // every row sees key 0 in its first tile (L >= 1), so m_new is finite from tile 0 on
       const float m_new = grow ? mloc : m_run;
-      // rescale factor of what is accumulated: exactly 1 unless the max moved in some lane
-      const bool moved = __any(grow);
-      float corr = 1.0f;
-      if (moved) corr = __builtin_amdgcn_exp2f(m_run - m_new);
+      // what is accumulated is rescaled only when the max moved in some lane (factor exactly 1
+      // in the others)
+      if (__any(grow)) rescale(m_run - m_new);
       half4 pb, pl;
       if constexpr (FUSED) {
         // P as hi + lo fp16 pair: the PV product sees P to ~22 bits, and the row sum is the
@@ -1037,22 +1095,18 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
         split2(pf[2], pf[3], one, h1, l1);
         pb = __builtin_shufflevector(h0, h1, 0, 1, 2, 3);
         pl = __builtin_shufflevector(l0, l1, 0, 1, 2, 3);
-        l_run = fmaf(l_run, corr, (pf[0] + pf[1]) + (pf[2] + pf[3]));
+        l_run += (pf[0] + pf[1]) + (pf[2] + pf[3]);
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           pb[j] = static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(sc[j], scale_log2, -m_new)));
         // the row sum of the ROUNDED probabilities (the ones the PV product uses), accumulated
         // exactly with fp16 dot products
-        l_run = dot_ones(pb, l_run * corr);
+        l_run = dot_ones(pb, l_run);
       }
       // l_run holds this lane's share of the row sum (its own keys); the four shares of a query
       // are combined once, after the last tile
       m_run = m_new;
-      if (moved) {
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
-      }
       // V row 4g + r/4, channels 16dt + 4(r%4) .. +3; chunk swizzled by 2*(row & 7)
       const int vrow = 4 * gq + (r >> 2);
 #pragma unroll
@@ -1091,9 +1145,7 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
       // lazy running max: moved only when a tile exceeds it by more than kMaxSlack
       const bool grow = mloc > m_run + kMaxSlack;
       const float m_new = grow ? mloc : m_run;
-      const bool moved = __any(grow);
-      float corr = 1.0f;
-      if (moved) corr = __builtin_amdgcn_exp2f(m_run - m_new);
+      if (__any(grow)) rescale(m_run - m_new);
       half8 pb, pl;
       if constexpr (FUSED) {
         float pf[8];
@@ -1111,8 +1163,7 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
         pl = __builtin_shufflevector(__builtin_shufflevector(l[0], l[1], 0, 1, 2, 3),
                                      __builtin_shufflevector(l[2], l[3], 0, 1, 2, 3),
                                      0, 1, 2, 3, 4, 5, 6, 7);
-        l_run = fmaf(l_run, corr,
-                     ((pf[0] + pf[1]) + (pf[2] + pf[3])) + ((pf[4] + pf[5]) + (pf[6] + pf[7])));
+        l_run += ((pf[0] + pf[1]) + (pf[2] + pf[3])) + ((pf[4] + pf[5]) + (pf[6] + pf[7]));
       } else {
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk)
@@ -1120,13 +1171,9 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
           for (int j = 0; j < 4; ++j)
             pb[4 * blk + j] = static_cast<_Float16>(
                 __builtin_amdgcn_exp2f(fmaf(sc[blk][j], scale_log2, -m_new)));
-        l_run = dot_ones(pb.lo, dot_ones(pb.hi, l_run * corr));
+        l_run = dot_ones(pb.lo, dot_ones(pb.hi, l_run));
       }
       m_run = m_new;
-      if (moved) {
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
-      }
       // V rows 8g + 4h + r/4, channels 16dt + 4(r%4) .. +3, chunk swizzled by 2*(row & 3)
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
@@ -1159,7 +1206,9 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
   // tile's uses of them after the barrier).
   wait_vmcnt<0>();
   wait_lgkmcnt<0>();
-  const float inv = 1.0f / rowsum4(l_run);
+  // v_rcp_f32 (1 ulp): the row sum is at least the rounded probability of the row maximum, so it
+  // is a normal number whenever the row has a key
+  const float inv = __builtin_amdgcn_rcpf(rowsum4(l_run));
   stage_barrier();
 
   // ---- epilogue: fragments -> row-major rows in LDS -> full-row global stores ---------------
@@ -1185,23 +1234,39 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
   }
   // Rows are read back by other lanes of the same wavefront: LDS executes a wavefront's accesses
   // in order, so no barrier is needed. All reads go out before the first store.
+  // Store i covers rows i * RPI + lo (lo = lane / OCH < RPI). Row r sits at output row
+  // (r >> hsh) * H + (r & (HPW - 1)) after (b, p0, head0); RPI and HPW are powers of two, so
+  // that splits into a wave-uniform part of i * RPI plus a per-lane part of lo (when HPW <= RPI,
+  // i * RPI is a multiple of HPW; otherwise lo < RPI stays inside one group of HPW rows). The
+  // per-lane byte offset is computed once and each store adds a scalar offset.
+  constexpr int RPI = 64 / OCH;
+  const int lo = lane / OCH, hmask = (1 << g.hsh) - 1;
+  const uint32_t voff =
+      static_cast<uint32_t>(((lo >> g.hsh) * H + (lo & hmask)) * RB + 16 * (lane % OCH));
   uint4v val[NI];
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int c = 64 * i + lane;
-    val[i] = *reinterpret_cast<const uint4v*>(ob + (c / OCH) * RS + 16 * (c % OCH));
-  }
+  for (int i = 0; i < NI; ++i)
+    val[i] = *reinterpret_cast<const uint4v*>(ob + (i * RPI + lo) * RS + 16 * (lane % OCH));
+  if (g.active) {
+    const int room = S - g.p0;  // positions of this wave block below S
+    // non-temporal: output rows are written once and not read back here, so they should not
+    // stay dirty in L2 (K/V tiles keep it, and the end-of-kernel writeback stays short)
+    if ((16 >> g.hsh) <= room) {
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int c = 64 * i + lane;
-    const int row = c / OCH;
-    const int prow = row >> g.hsh;  // position offset of the row inside the wave block
-    // output row index relative to (b, p0, head0): prow * H + head offset, 32-bit
-    const unsigned rel = static_cast<unsigned>(prow * H + (row & ((1 << g.hsh) - 1)));
-    if (g.active && g.p0 + prow < S)
-      // non-temporal: output rows are written once and not read back here, so they should not
-      // stay dirty in L2 (K/V tiles keep it, and the end-of-kernel writeback stays short)
-      __builtin_nontemporal_store(val[i], reinterpret_cast<uint4v*>(obase + rel * RB + 16 * (c % OCH)));
+      for (int i = 0; i < NI; ++i) {
+        const int r0 = i * RPI;
+        const uint32_t srow = static_cast<uint32_t>(((r0 >> g.hsh) * H + (r0 & hmask)) * RB);
+        __builtin_nontemporal_store(val[i], reinterpret_cast<uint4v*>(obase + srow + voff));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int r0 = i * RPI;
+        const uint32_t srow = static_cast<uint32_t>(((r0 >> g.hsh) * H + (r0 & hmask)) * RB);
+        if ((lo >> g.hsh) < room - (r0 >> g.hsh))
+          __builtin_nontemporal_store(val[i], reinterpret_cast<uint4v*>(obase + srow + voff));
+      }
+    }
   }
 }
 
@@ -1211,7 +1276,7 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(F16Args a) {
   __shared__ __attribute__((aligned(1024))) _Float16 ring[F16Lds<D, TOut, FUSED>::HALVES];
   // the wavefront index is uniform; readfirstlane lets the compiler branch on it with scalars
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const Sched sc = schedule(a.lengths, a.B, a.S, a.KV, a.shp.kv);
+  const Sched sc = schedule(a.lengths, a.B, a.S, a.KV, a.shp.kv, a.shp.wpp, a.shp.serp);
   f16_block<D, TOut, FUSED>(a, geom16_of(sc, a.bidi, wave, a.shp), ring, wave);
 }
 
@@ -1233,6 +1298,14 @@ static dim3 split_grid(int B, int S, int H, int KV) {
 
 // Grid limits and the exactness bound of the Div quotients (n * d < 2^32 for every quotient the
 // geometry takes: plane rank / KV on the ranked schedule, row block / head blocks).
+// k / wpp is exact by Div for every item index k < wpp * zs when (wpp * zs) * wpp < 2^32.
+static int serpentine_exact(int wpp, int zs) {
+  return static_cast<uint64_t>(wpp) * static_cast<uint64_t>(wpp) * static_cast<uint64_t>(zs) <
+                 (1ull << 32)
+             ? 1
+             : 0;
+}
+
 static bool geometry_fits(int B, int KV, int nblocks, int blockdiv) {
   const uint64_t kv = static_cast<uint64_t>(KV);
   if (B > 65535 || KV > 65535) return false;
@@ -1284,6 +1357,10 @@ hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st) {
   shp.G = a.H / a.KV;
   shp.g = make_div(static_cast<uint32_t>(shp.G));
   shp.kv = make_div(static_cast<uint32_t>(a.KV));
+  const int nrb = shp.G * ((a.S + 31) / 32);
+  const int wpp = a.D == 128 ? (nrb + 1) / 2 : (nrb + 3) / 4;
+  shp.wpp = make_div(static_cast<uint32_t>(wpp));
+  shp.serp = serpentine_exact(wpp, a.B * a.KV / 8);
   const float sl2 = a.scale * kLog2e;
   auto q = static_cast<const float*>(a.q), k = static_cast<const float*>(a.k),
        v = static_cast<const float*>(a.v);
@@ -1344,8 +1421,12 @@ bool attention_f16_fits(int B, int S, int H, int KV, int D) {
   // K/V DMA offsets are 32-bit bytes inside one (batch row, kv head) plane, row * rowbytes by
   // __umul24
   const uint64_t rowbytes = static_cast<uint64_t>(KV) * D * 2;
+  // q loads are 32-bit offsets inside one batch row (S * H * D halves), the output stores
+  // 32-bit offsets inside 16 rows of a wave block (at most 16 * H * D fp32 values)
+  const uint64_t qrow = static_cast<uint64_t>(S) * H * D * 2;
   return static_cast<uint64_t>(S) * rowbytes < (1ull << 32) && S < (1 << 24) &&
-         rowbytes < (1u << 24);
+         rowbytes < (1u << 24) && qrow < (1ull << 31) &&
+         static_cast<uint64_t>(H) * D * 4 * 16 < (1ull << 31);
 }
 
 hipError_t launch_attention_f16(const AttnArgs& a, hipStream_t st) {
@@ -1357,6 +1438,8 @@ hipError_t launch_attention_f16(const AttnArgs& a, hipStream_t st) {
   shp.nwb = f16_wave_blocks(a.S, shp.G);
   shp.kv = make_div(static_cast<uint32_t>(a.KV));
   shp.hbn = make_div(static_cast<uint32_t>(shp.G >> shp.hsh));
+  shp.wpp = make_div(static_cast<uint32_t>((shp.nwb + 3) / 4));
+  shp.serp = serpentine_exact((shp.nwb + 3) / 4, a.B * a.KV / 8);
   const float sl2 = a.scale * kLog2e;
   const bool fused = a.gamma_q != nullptr;
   if (fused && (!a.rope_cos || !a.rope_sin)) return hipErrorInvalidValue;

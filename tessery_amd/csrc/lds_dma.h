@@ -1,8 +1,11 @@
-// LDS DMA helpers for gfx950 kernels that stage tiles with global_load_lds_dwordx4.
+// LDS DMA helpers for gfx950 kernels that stage tiles with global_load_lds_dwordx4, and asm
+// register loads whose waits the kernel places itself.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "common.h"
 
 namespace tessery {
 
@@ -30,6 +33,37 @@ __device__ __forceinline__ void dma16_at(const void* base, uint32_t off, _Float1
                :
                : "v"(off), "s"(base), "s"(addr)
                : "memory", "m0");
+}
+
+// 16 bytes per lane, global -> VGPRs, at a wave-uniform base (SGPR pair) plus a per-lane 32-bit
+// byte offset and an immediate. Inline asm like the LDS DMA, so the compiler places no waits of
+// its own for it (it cannot count the DMAs, and its waits for mixed streams degrade to
+// vmcnt(0)); the caller reads dst only after wait_vmcnt_pin. dst is a read-write operand: every
+// read of its previous value is ordered before the load (or reads a copy made before it).
+template <int OFF>
+__device__ __forceinline__ void load16_at(floatx4& dst, const void* base, uint32_t off) {
+  asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3"
+               : "+v"(dst)
+               : "v"(off), "s"(base), "i"(OFF)
+               : "memory");
+}
+
+// s_waitcnt vmcnt(N); the four registers count as written here, so nothing reads them earlier.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_pin(floatx4 (&r)[4]) {
+  asm volatile("s_waitcnt vmcnt(%4)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3])
+               : "n"(N)
+               : "memory");
+}
+
+// s_waitcnt vmcnt(N) pinning six registers (see wait_vmcnt_pin).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_pin6(floatx4* r) {
+  asm volatile("s_waitcnt vmcnt(%6)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5])
+               : "n"(N)
+               : "memory");
 }
 
 // s_waitcnt vmcnt(n), leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).

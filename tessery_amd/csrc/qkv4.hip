@@ -90,19 +90,6 @@ __device__ __forceinline__ float word_value(uint16_t w) {
 
 __device__ __forceinline__ int xsw(int row) { return (row >> 1) & 7; }
 
-// 16 bytes per lane, global -> VGPRs, at a wave-uniform base (SGPR pair) plus a per-lane 32-bit
-// byte offset and an immediate. Inline asm like the LDS DMA, so the compiler places no waits of
-// its own for it (it cannot count the DMAs, and its waits for mixed streams degrade to
-// vmcnt(0)); the caller reads dst only after wait_vmcnt_pin. dst is a read-write operand: every
-// read of its previous value is ordered before the load (or reads a copy made before it).
-template <int OFF>
-__device__ __forceinline__ void load16_at(floatx4& dst, const void* base, uint32_t off) {
-  asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3"
-               : "+v"(dst)
-               : "v"(off), "s"(base), "i"(OFF)
-               : "memory");
-}
-
 // Scale and bias words of a 128-column tile, all groups, into LDS transposed to
 // [part][group][column] (part 0 scales, 1 biases): the lanes of a column block then read one
 // group's words from consecutive addresses (in the global [N, groups] layout they are `groups`
@@ -126,15 +113,6 @@ __device__ __forceinline__ void copy_scales_transposed(uint16_t* sbuf, const uin
   } else {
     for (int g = 0; g < groups; ++g) dst[g * 128] = src[g];
   }
-}
-
-// s_waitcnt vmcnt(N); the four registers count as written here, so nothing reads them earlier.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt_pin(floatx4 (&r)[4]) {
-  asm volatile("s_waitcnt vmcnt(%4)"
-               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3])
-               : "n"(N)
-               : "memory");
 }
 
 template <int N>
