@@ -447,13 +447,14 @@ def bench_qwen_f32(args, layers: int = 8) -> dict:
                      "hbm_gbs": nbytes / avg / 1e9, "kernel": kernel},
         "cpu_baseline": None,
     }
-    if not args.no_cpu_baseline:
-        from oracle import attention
+    # layer 0 against the float64 oracle (the fp32 route's bar, max-abs 1e-4), also without the
+    # CPU leg
+    from oracle import attention
 
-        expected = attention.attention(host0["q"], host0["k"], host0["v"], lengths,
-                                       bidirectional=False)
-        err = float(np.max(np.abs(out0.astype(np.float64) - expected)))
-        result["parity"] = {"max_abs": err, "bar": PARITY_F32_OUT, "ok": err <= PARITY_F32_OUT}
+    expected = attention.attention(host0["q"], host0["k"], host0["v"], lengths, bidirectional=False)
+    err = float(np.max(np.abs(out0.astype(np.float64) - expected)))
+    result["max_abs_err_layer0"] = err
+    result["parity"] = {"max_abs": err, "bar": PARITY_F32_OUT, "ok": err <= PARITY_F32_OUT}
     return result
 
 

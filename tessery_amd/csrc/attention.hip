@@ -1281,6 +1281,322 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(F16Args a) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// fp32 attention on bf16 MFMA (routes attention_tiled / attention_tail_128 at D = 128).
+//
+// An fp32 value x splits exactly into three bf16 terms by truncation: b1 = the upper half of x's
+// bits (sign, exponent, 7 mantissa bits), r1 = x - b1 (exact: the lower 16 significand bits),
+// b2 = the upper half of r1, b3 = r1 - b2 (at most 8 significant bits, so exactly a bf16). bf16
+// keeps fp32's exponent range, so no scaling is needed. A product x * y is taken as the six
+// terms b_i c_j with i + j <= 4; the three dropped ones are below 2^-24 |x y| (fp32 rounding),
+// every bf16 product is exact in fp32 and the MFMAs accumulate in fp32. The bf16 rate is 16x the
+// fp32 MFMA rate, so the six products still cost well under half of the fp32 instructions.
+//
+// Geometry, schedule and output layout are those of attn_f16_mfma (16 query rows per wavefront,
+// four wave blocks of one (batch row, kv head) plane per workgroup, 16-key tiles). Q is split in
+// registers. K and V tiles arrive as fp32 by LDS DMA (two raw stages) and are split once per
+// workgroup into three bf16 planes each (two buffers): step t converts tile t + 1 while its
+// MFMAs run on tile t, one barrier per step.
+//   raw   [stage][K, V][16 rows][128] fp32: 16-byte chunk c of row r at position c ^ (r >> 3 & 1)
+//   split [buffer][K, V][plane][16 rows][128] bf16: K chunk c at c ^ (r & 15) (the score reads
+//         of one k-step hit 16 rows), V chunk c at c ^ (2 (r & 7) ^ 8 (r >> 3 & 1)) (the
+//         transposed reads of four rows hit four bank groups)
+// Converting thread t owns row (t >> 5 & 7) + 8 (t >> 3 & 1) and channels 8c .. 8c + 7 with
+// c = (t & 7) + 8 (t >> 4 & 1): the 16 threads of one LDS access cover rows r and r + 8, which
+// makes its raw reads and split writes conflict-free under the swizzles above.
+// Score terms per k-step: (k1,q1) (k1,q2) (k2,q1) (k1,q3) (k2,q2) (k3,q1); output terms per
+// 16-channel block, each MFMA stacking two (probability, value) pairs over the same four keys:
+// [p1,p1]x[v1,v2], [p2,p2]x[v1,v2], [p1,p3]x[v3,v1].
+// ---------------------------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+
+// x[0..7] -> three packed bf16x8 words (channel pairs (2m, 2m + 1) in word m)
+__device__ __forceinline__ void split3x8(const floatx4& x0, const floatx4& x1, uint4v& p1,
+                                         uint4v& p2, uint4v& p3) {
+  uint32_t u0[8], u1[8], u2[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const float x = m < 4 ? x0[m] : x1[m - 4];
+    u0[m] = __float_as_uint(x);
+    const float r1 = x - __uint_as_float(u0[m] & 0xffff0000u);
+    u1[m] = __float_as_uint(r1);
+    u2[m] = __float_as_uint(r1 - __uint_as_float(u1[m] & 0xffff0000u));
+  }
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    // upper halves of words 2w (result bits 0-15) and 2w + 1 (bits 16-31)
+    p1[w] = __builtin_amdgcn_perm(u0[2 * w + 1], u0[2 * w], 0x07060302u);
+    p2[w] = __builtin_amdgcn_perm(u1[2 * w + 1], u1[2 * w], 0x07060302u);
+    p3[w] = __builtin_amdgcn_perm(u2[2 * w + 1], u2[2 * w], 0x07060302u);
+  }
+}
+
+// 8 bytes of a row-major bf16 V plane, transposed across each 16-lane group (as lds_read_tr)
+__device__ __forceinline__ shortx4 lds_read_tr_s(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) shortx4*)(p));
+}
+
+__device__ __forceinline__ int vsw_x3(int row) { return (2 * (row & 7)) ^ (8 * ((row >> 3) & 1)); }
+
+struct X3Args {
+  const float* q;
+  const float* k;
+  const float* v;
+  const uint32_t* lengths;
+  float* out;
+  int B, S, H, KV;
+  float scale_log2;
+  int bidi;
+  F16Shape shp;
+};
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void attn_f32x3(X3Args a) {
+  static_assert(D == 128, "the split-bf16 fp32 kernel serves D = 128");
+  constexpr int KT = 16, NS = D / 32, NDT = D / 16;
+  constexpr int TILE = KT * D;                   // elements per K or V tile
+  constexpr int RAW_BYTES = 2 * 2 * TILE * 4;    // [stage][K, V] fp32
+  constexpr int SPLIT_BYTES = 2 * 2 * 3 * TILE * 2;  // [buffer][K, V][plane] bf16
+  constexpr int RB = D * 4, RS = RB + 16;        // output staging rows
+  static_assert(4 * 16 * RS <= RAW_BYTES + SPLIT_BYTES, "output staging fits");
+  __shared__ __attribute__((aligned(1024))) char lds[RAW_BYTES + SPLIT_BYTES];
+  float* const raw = reinterpret_cast<float*>(lds);
+  uint16_t* const spl = reinterpret_cast<uint16_t*>(lds + RAW_BYTES);
+  auto raw_at = [&](int st, int t) { return raw + (2 * st + t) * TILE; };
+  auto spl_at = [&](int buf, int t, int plane) { return spl + ((2 * buf + t) * 3 + plane) * TILE; };
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const Sched sc = schedule(a.lengths, a.B, a.S, a.KV, a.shp.kv, a.shp.wpp, a.shp.serp);
+  const Geom16 g = geom16_of(sc, a.bidi, wave, a.shp);
+  const int S = a.S, H = a.H, KV = a.KV;
+  const float scale_log2 = a.scale_log2;
+  int tid = static_cast<int>(threadIdx.x);
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, r = lane & 15, gq = lane >> 4;
+  const int qpos = g.p0 + (r >> g.hsh);
+  const int qhead = g.head0 + (r & ((1 << g.hsh) - 1));
+  const int qpos_c = min(qpos, S - 1);
+  const int limit = a.bidi ? g.L : min(qpos + 1, g.L);
+  const int ntiles = (g.wg_end + KT - 1) / KT;
+  // plane bases are wave-uniform; per-lane DMA offsets are 32-bit bytes within the plane
+  // (S * KV * D * 4 < 2^32, checked by the launcher)
+  const float* kbase = a.k + (static_cast<size_t>(g.b) * S * KV + g.kvh) * D;
+  const float* vbase = a.v + (static_cast<size_t>(g.b) * S * KV + g.kvh) * D;
+  const uint32_t rowbytes = static_cast<uint32_t>(KV * D * 4);
+
+  // ---- DMA: wavefront w fills rows 4w .. 4w + 3 of the K and V tiles, two 1 KiB blocks each;
+  // block i holds rows 4w + 2i + (lane >> 5), lane l's 16 bytes at chunk position l & 31 ------
+  uint32_t dcoff[2];
+  int drow[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    drow[i] = 4 * wave + 2 * i + (lane >> 5);
+    dcoff[i] = 16u * static_cast<uint32_t>((lane & 31) ^ ((drow[i] >> 3) & 1));
+  }
+  // key rows at or beyond L are fetched from key 0 of this batch row (always in bounds)
+  auto issue = [&](int st, int kt) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int key = kt * KT + drow[i];
+      const uint32_t off = __umul24(static_cast<uint32_t>(key < g.L ? key : 0), rowbytes) + dcoff[i];
+      dma16_at(kbase, off, reinterpret_cast<_Float16*>(raw_at(st, 0) + (4 * wave + 2 * i) * D));
+      dma16_at(vbase, off, reinterpret_cast<_Float16*>(raw_at(st, 1) + (4 * wave + 2 * i) * D));
+    }
+  };
+  issue(0, 0);
+  if (ntiles > 1) issue(1, 1);
+
+  // ---- conversion of one raw stage into one split buffer ------------------------------------
+  const int crow = ((tid >> 5) & 7) + 8 * ((tid >> 3) & 1);
+  const int cc = (tid & 7) + 8 * ((tid >> 4) & 1);
+  const int cf = (crow >> 3) & 1;
+  auto convert = [&](int st, int buf) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const float* src = raw_at(st, t) + crow * D;
+      const floatx4 x0 = *reinterpret_cast<const floatx4*>(src + 4 * ((2 * cc) ^ cf));
+      const floatx4 x1 = *reinterpret_cast<const floatx4*>(src + 4 * ((2 * cc + 1) ^ cf));
+      uint4v w1, w2, w3;
+      split3x8(x0, x1, w1, w2, w3);
+      const int pos = crow * D + 8 * (cc ^ (t == 0 ? (crow & 15) : vsw_x3(crow)));
+      *reinterpret_cast<uint4v*>(spl_at(buf, t, 0) + pos) = w1;
+      *reinterpret_cast<uint4v*>(spl_at(buf, t, 1) + pos) = w2;
+      *reinterpret_cast<uint4v*>(spl_at(buf, t, 2) + pos) = w3;
+    }
+  };
+
+  // ---- Q: lane (r, g) holds channels 32s + 8g .. +7 of query r, as three bf16 planes ---------
+  // q rows of one batch row lie within S * H * D floats (below 2^31 bytes, checked by the
+  // launcher): a per-lane 32-bit offset from the batch row's base
+  const float* qrow = a.q + static_cast<size_t>(g.b) * S * H * D;
+  const uint32_t qoff = static_cast<uint32_t>((qpos_c * H + qhead) * D + 8 * gq);
+  bf16x8 q1[NS], q2[NS], q3[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const floatx4 x0 = *reinterpret_cast<const floatx4*>(qrow + qoff + 32 * s);
+    const floatx4 x1 = *reinterpret_cast<const floatx4*>(qrow + qoff + 32 * s + 4);
+    uint4v w1, w2, w3;
+    split3x8(x0, x1, w1, w2, w3);
+    q1[s] = __builtin_bit_cast(bf16x8, w1);
+    q2[s] = __builtin_bit_cast(bf16x8, w2);
+    q3[s] = __builtin_bit_cast(bf16x8, w3);
+  }
+  // Rows past S read row S - 1 (finite data) and are never stored.
+
+  floatx4 o[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  auto rescale = [&](float d) {
+    asm volatile("" : "+v"(d));
+    const float corr = __builtin_amdgcn_exp2f(d);
+    l_run *= corr;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
+  };
+
+  // tile kt from split buffer buf
+  auto compute = [&](int kt, int buf) {
+    const uint16_t* k1p = spl_at(buf, 0, 0);
+    floatx4 acc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+    const int rbase = r * D, ksw16 = r & 15;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int off = rbase + 8 * ((4 * s + gq) ^ ksw16);
+      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(k1p + off);
+      const bf16x8 k2 = *reinterpret_cast<const bf16x8*>(k1p + TILE + off);
+      const bf16x8 k3 = *reinterpret_cast<const bf16x8*>(k1p + 2 * TILE + off);
+      floatx4& c = acc[s & 1];
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, q1[s], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, q2[s], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2, q1[s], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, q3[s], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2, q2[s], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k3, q1[s], c, 0, 0, 0);
+    }
+    mfma_result_fence(acc[0], acc[1]);
+    floatx4 sc = acc[0] + acc[1];
+    // element j is key 4g + j of this tile
+    if (kt * KT + KT > g.limit_min) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (kt * KT + 4 * gq + j >= limit) sc[j] = -INFINITY;
+    }
+    const float mloc = rowmax4(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]))) * scale_log2;
+    const bool grow = mloc > m_run + kMaxSlack;
+    // every row sees key 0 in its first tile (L >= 1), so m_new is finite from tile 0 on
+    const float m_new = grow ? mloc : m_run;
+    float pf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pf[j] = __builtin_amdgcn_exp2f(fmaf(sc[j], scale_log2, -m_new));
+    // the probabilities as three bf16 terms (exact), keys 4g .. 4g + 3
+    uint32_t u0[4], u1[4], u2[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      u0[j] = __float_as_uint(pf[j]);
+      const float r1 = pf[j] - __uint_as_float(u0[j] & 0xffff0000u);
+      u1[j] = __float_as_uint(r1);
+      u2[j] = __float_as_uint(r1 - __uint_as_float(u1[j] & 0xffff0000u));
+    }
+    uint32_t pw[3][2];
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      pw[0][w] = __builtin_amdgcn_perm(u0[2 * w + 1], u0[2 * w], 0x07060302u);
+      pw[1][w] = __builtin_amdgcn_perm(u1[2 * w + 1], u1[2 * w], 0x07060302u);
+      pw[2][w] = __builtin_amdgcn_perm(u2[2 * w + 1], u2[2 * w], 0x07060302u);
+    }
+    const bf16x8 bp11 = __builtin_bit_cast(bf16x8, uint4v{pw[0][0], pw[0][1], pw[0][0], pw[0][1]});
+    const bf16x8 bp22 = __builtin_bit_cast(bf16x8, uint4v{pw[1][0], pw[1][1], pw[1][0], pw[1][1]});
+    const bf16x8 bp13 = __builtin_bit_cast(bf16x8, uint4v{pw[0][0], pw[0][1], pw[2][0], pw[2][1]});
+    if (__any(grow)) rescale(m_run - m_new);
+    l_run += (pf[0] + pf[1]) + (pf[2] + pf[3]);
+    m_run = m_new;
+    // V row 4g + r/4, channels 16dt + 4(r%4) .. +3 of each plane
+    const uint16_t* v1p = spl_at(buf, 1, 0);
+    const int vrow = 4 * gq + (r >> 2), vsw = vsw_x3(vrow);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const int off = vrow * D + 8 * ((2 * dt + ((r & 3) >> 1)) ^ vsw) + 4 * (r & 1);
+      const shortx4 v1 = lds_read_tr_s(v1p + off);
+      const shortx4 v2 = lds_read_tr_s(v1p + TILE + off);
+      const shortx4 v3 = lds_read_tr_s(v1p + 2 * TILE + off);
+      const bf16x8 a12 = __builtin_bit_cast(bf16x8, __builtin_shufflevector(v1, v2, 0, 1, 2, 3, 4, 5, 6, 7));
+      const bf16x8 a31 = __builtin_bit_cast(bf16x8, __builtin_shufflevector(v3, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a12, bp11, o[dt], 0, 0, 0);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a12, bp22, o[dt], 0, 0, 0);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a31, bp13, o[dt], 0, 0, 0);
+    }
+  };
+
+  // The q loads were issued after both DMA tiles and have been waited for: tile 0 (and 1) have
+  // landed. Split tile 0 before the first step.
+  wait_vmcnt<0>();
+  stage_barrier();
+  convert(0, 0);
+  // Step kt (parity c = kt & 1, a compile-time constant): tile kt + 1 (raw stage c ^ 1, DMA from
+  // step kt - 1) has landed, split buffer c holds tile kt (converted at step kt - 1), raw stage c
+  // and split buffer c ^ 1 are free after the barrier; tile kt + 2 goes to raw stage c, tile
+  // kt + 1 is converted into buffer c ^ 1 while tile kt is computed.
+  auto step = [&](int kt, auto parity) {
+    constexpr int c = decltype(parity)::value;
+    wait_vmcnt<0>();
+    wait_lgkmcnt<0>();
+    stage_barrier();
+    if (kt + 2 < ntiles) issue(c, kt + 2);
+    if (kt + 1 < ntiles) convert(c ^ 1, c ^ 1);
+    if (kt * KT < g.wave_end) compute(kt, c);
+  };
+  for (int kt = 0; kt < ntiles; kt += 2) {
+    step(kt, Stage<0>{});
+    if (kt + 1 < ntiles) step(kt + 1, Stage<1>{});
+  }
+  wait_vmcnt<0>();
+  wait_lgkmcnt<0>();
+  const float inv = __builtin_amdgcn_rcpf(rowsum4(l_run));
+  stage_barrier();
+
+  // ---- epilogue: fragments -> row-major rows in LDS -> full-row stores (as attn_f16_mfma) ----
+  constexpr int OCH = RB / 16, NI = 16 * OCH / 64, RPI = 64 / OCH;
+  char* const ob = lds + wave * 16 * RS;
+  char* const obase = reinterpret_cast<char*>(a.out) +
+                      ((static_cast<size_t>(g.b) * S + g.p0) * H + g.head0) * RB;
+  {
+    char* const orow = ob + r * RS;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+      *reinterpret_cast<floatx4*>(orow + 4 * (16 * dt + 4 * gq)) = o[dt] * inv;
+  }
+  const int lo = lane / OCH, hmask = (1 << g.hsh) - 1;
+  const uint32_t voff =
+      static_cast<uint32_t>(((lo >> g.hsh) * H + (lo & hmask)) * RB + 16 * (lane % OCH));
+  uint4v val[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+    val[i] = *reinterpret_cast<const uint4v*>(ob + (i * RPI + lo) * RS + 16 * (lane % OCH));
+  if (g.active) {
+    const int room = S - g.p0;
+    if ((16 >> g.hsh) <= room) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int r0 = i * RPI;
+        const uint32_t srow = static_cast<uint32_t>(((r0 >> g.hsh) * H + (r0 & hmask)) * RB);
+        __builtin_nontemporal_store(val[i], reinterpret_cast<uint4v*>(obase + srow + voff));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int r0 = i * RPI;
+        const uint32_t srow = static_cast<uint32_t>(((r0 >> g.hsh) * H + (r0 & hmask)) * RB);
+        if ((lo >> g.hsh) < room - (r0 >> g.hsh))
+          __builtin_nontemporal_store(val[i], reinterpret_cast<uint4v*>(obase + srow + voff));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Host launchers.
 // ---------------------------------------------------------------------------------------------
 static dim3 mfma_grid(int B, int S, int H, int KV) {
@@ -1343,6 +1659,32 @@ hipError_t launch_attention_scalar(const AttnArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// attn_f32x3: the geometry of attn_f16_mfma with fp32 operands. K/V DMA offsets are 32-bit bytes
+// inside one (batch row, kv head) plane (row * rowbytes by __umul24), q loads 32-bit offsets inside
+// one batch row, output stores 32-bit offsets inside 16 rows of a wave block.
+static bool attention_f32x3_fits(int B, int S, int H, int KV, int D) {
+  if (D != 128 || B <= 0 || S <= 0 || H <= 0 || KV <= 0 || H % KV) return false;
+  const int G = H / KV;
+  const int hsh = __builtin_ctz(static_cast<unsigned>(f16_heads_per_wave(G)));
+  if (!geometry_fits(B, KV, f16_wave_blocks(S, G), G >> hsh)) return false;
+  const uint64_t rowbytes = static_cast<uint64_t>(KV) * D * 4;
+  return static_cast<uint64_t>(S) * rowbytes < (1ull << 32) && S < (1 << 24) &&
+         rowbytes < (1u << 24) && static_cast<uint64_t>(S) * H * D * 4 < (1ull << 31) &&
+         static_cast<uint64_t>(H) * D * 4 * 16 < (1ull << 31);
+}
+
+static F16Shape f16_shape(int B, int S, int H, int KV) {
+  F16Shape shp;
+  shp.G = H / KV;
+  shp.hsh = __builtin_ctz(static_cast<unsigned>(f16_heads_per_wave(shp.G)));
+  shp.nwb = f16_wave_blocks(S, shp.G);
+  shp.kv = make_div(static_cast<uint32_t>(KV));
+  shp.hbn = make_div(static_cast<uint32_t>(shp.G >> shp.hsh));
+  shp.wpp = make_div(static_cast<uint32_t>((shp.nwb + 3) / 4));
+  shp.serp = serpentine_exact((shp.nwb + 3) / 4, B * KV / 8);
+  return shp;
+}
+
 bool attention_f32_fits(int B, int S, int H, int KV) {
   if (B <= 0 || S <= 0 || H <= 0 || KV <= 0 || H % KV) return false;
   const int G = H / KV;
@@ -1373,8 +1715,25 @@ hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st) {
       attn_f32_ring<64><<<grid, 256, 0, st>>>(q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
       break;
     case 128:
-      attn_f32_split<128><<<split_grid(a.B, a.S, a.H, a.KV), 256, 0, st>>>(
-          q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
+      if (attention_f32x3_fits(a.B, a.S, a.H, a.KV, a.D)) {
+        X3Args x{};
+        x.q = q;
+        x.k = k;
+        x.v = v;
+        x.lengths = a.lengths;
+        x.out = o;
+        x.B = a.B;
+        x.S = a.S;
+        x.H = a.H;
+        x.KV = a.KV;
+        x.scale_log2 = sl2;
+        x.bidi = a.bidi;
+        x.shp = f16_shape(a.B, a.S, a.H, a.KV);
+        attn_f32x3<128><<<sched_grid(a.B, a.KV, (x.shp.nwb + 3) / 4), 256, 0, st>>>(x);
+      } else {
+        attn_f32_split<128><<<split_grid(a.B, a.S, a.H, a.KV), 256, 0, st>>>(
+            q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
+      }
       break;
     default:
       return hipErrorInvalidValue;

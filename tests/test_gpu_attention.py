@@ -150,6 +150,33 @@ def test_extreme_logits_and_masked_blocks(runtime, bidirectional, pattern, seq):
     check_f32(got, expected)
 
 
+def test_qwen3_8x512_fp32_route(runtime):
+    """The fp32 route at the Qwen3 8x512 shape (bench.py --workload qwen3_8x512_f32, layer 0):
+    q/k normalized and rotated in float64 and rounded to fp32, v N(0,1), lengths U{64..512}."""
+    shape, lengths = workloads.qwen3_8x512()
+    t = workloads.qwen_layer(shape, 0, seed=3)
+    qn = workloads.bf16_values(t["q_norm"]).astype(np.float64)
+    kn = workloads.bf16_values(t["k_norm"]).astype(np.float64)
+    q = norm_rope.norm_rope(t["q"], qn, workloads.EPS, workloads.THETA).astype(np.float32)
+    k = norm_rope.norm_rope(t["k"], kn, workloads.EPS, workloads.THETA).astype(np.float32)
+    v = t["v"].astype(np.float32)
+    got = attend(runtime, q, k, v, lengths, bidirectional=False)
+    check_f32(got, ref.attention(q, k, v, lengths, bidirectional=False))
+
+
+@pytest.mark.parametrize("heads,kv", [(8, 2), (16, 2), (12, 4)])
+@pytest.mark.parametrize("bidirectional", [False, True])
+def test_fp32_d128_head_groups(runtime, heads, kv, bidirectional):
+    """fp32 D = 128 with 4, 8 and 3 query heads per kv head: 4 and 8 heads share a wavefront's
+    rows, 3 does not divide 16 and gives one head per wavefront. Ragged lengths, S % 32 != 0."""
+    rng = np.random.default_rng(577)
+    q = rng.normal(size=(2, 200, heads, 128)).astype(np.float32)
+    k, v = [rng.normal(size=(2, 200, kv, 128)).astype(np.float32) for _ in range(2)]
+    lengths = np.array([137, 200], np.uint32)
+    got = attend(runtime, q, k, v, lengths, bidirectional=bidirectional)
+    check_f32(got, ref.attention(q, k, v, lengths, bidirectional=bidirectional))
+
+
 @pytest.mark.parametrize("seq,name", [(16, "attention"), (64, "attention_tiled"),
                                       (100, "attention_tail_32"), (512, "attention_tiled")])
 def test_route_dispatch_counts_and_output_guard(runtime, seq, name):
