@@ -1293,22 +1293,23 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(F16Args a) {
 //
 // Geometry, schedule and output layout are those of attn_f16_mfma (16 query rows per wavefront,
 // four wave blocks of one (batch row, kv head) plane per workgroup, 16-key tiles). Q is split in
-// registers. K and V tiles arrive as fp32 by LDS DMA (two raw stages) and are split once per
-// workgroup into three bf16 planes each (two buffers): step t converts tile t + 1 while its
-// MFMAs run on tile t, one barrier per step.
-//   raw   [stage][K, V][16 rows][128] fp32: 16-byte chunk c of row r at position c ^ (r >> 3 & 1)
+// registers. K and V tiles are loaded as fp32 into registers one step ahead and split once per
+// workgroup into three bf16 planes each, in two LDS buffers (48 KiB: three workgroups per CU at
+// <= 168 VGPRs): step t splits tile t + 1 and loads tile t + 2 while its MFMAs run on tile t,
+// one barrier per step.
 //   split [buffer][K, V][plane][16 rows][128] bf16: K chunk c at c ^ (r & 15) (the score reads
 //         of one k-step hit 16 rows), V chunk c at c ^ (2 (r & 7) ^ 8 (r >> 3 & 1)) (the
 //         transposed reads of four rows hit four bank groups)
 // Converting thread t owns row (t >> 5 & 7) + 8 (t >> 3 & 1) and channels 8c .. 8c + 7 with
 // c = (t & 7) + 8 (t >> 4 & 1): the 16 threads of one LDS access cover rows r and r + 8, which
-// makes its raw reads and split writes conflict-free under the swizzles above.
+// makes its split writes conflict-free under the swizzles above.
 // Score terms per k-step: (k1,q1) (k1,q2) (k2,q1) (k1,q3) (k2,q2) (k3,q1); output terms per
 // 16-channel block, each MFMA stacking two (probability, value) pairs over the same four keys:
 // [p1,p1]x[v1,v2], [p2,p2]x[v1,v2], [p1,p3]x[v3,v1].
 // ---------------------------------------------------------------------------------------------
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short shortx4 __attribute__((ext_vector_type(4)));
+typedef short shortx8 __attribute__((ext_vector_type(8)));
 
 // x[0..7] -> three packed bf16x8 words (channel pairs (2m, 2m + 1) in word m)
 __device__ __forceinline__ void split3x8(const floatx4& x0, const floatx4& x1, uint4v& p1,
@@ -1355,15 +1356,12 @@ template <int D>
 __global__ __launch_bounds__(256, 2) void attn_f32x3(X3Args a) {
   static_assert(D == 128, "the split-bf16 fp32 kernel serves D = 128");
   constexpr int KT = 16, NS = D / 32, NDT = D / 16;
-  constexpr int TILE = KT * D;                   // elements per K or V tile
-  constexpr int RAW_BYTES = 2 * 2 * TILE * 4;    // [stage][K, V] fp32
+  constexpr int TILE = KT * D;                       // elements per K or V tile
   constexpr int SPLIT_BYTES = 2 * 2 * 3 * TILE * 2;  // [buffer][K, V][plane] bf16
-  constexpr int RB = D * 4, RS = RB + 16;        // output staging rows
-  static_assert(4 * 16 * RS <= RAW_BYTES + SPLIT_BYTES, "output staging fits");
-  __shared__ __attribute__((aligned(1024))) char lds[RAW_BYTES + SPLIT_BYTES];
-  float* const raw = reinterpret_cast<float*>(lds);
-  uint16_t* const spl = reinterpret_cast<uint16_t*>(lds + RAW_BYTES);
-  auto raw_at = [&](int st, int t) { return raw + (2 * st + t) * TILE; };
+  constexpr int RB = D * 4, RS = RB + 16;            // output staging rows
+  static_assert(4 * 16 * RS <= SPLIT_BYTES, "output staging fits");
+  __shared__ __attribute__((aligned(1024))) char lds[SPLIT_BYTES];
+  uint16_t* const spl = reinterpret_cast<uint16_t*>(lds);
   auto spl_at = [&](int buf, int t, int plane) { return spl + ((2 * buf + t) * 3 + plane) * TILE; };
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1385,46 +1383,36 @@ __global__ __launch_bounds__(256, 2) void attn_f32x3(X3Args a) {
   const float* vbase = a.v + (static_cast<size_t>(g.b) * S * KV + g.kvh) * D;
   const uint32_t rowbytes = static_cast<uint32_t>(KV * D * 4);
 
-  // ---- DMA: wavefront w fills rows 4w .. 4w + 3 of the K and V tiles, two 1 KiB blocks each;
-  // block i holds rows 4w + 2i + (lane >> 5), lane l's 16 bytes at chunk position l & 31 ------
-  uint32_t dcoff[2];
-  int drow[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    drow[i] = 4 * wave + 2 * i + (lane >> 5);
-    dcoff[i] = 16u * static_cast<uint32_t>((lane & 31) ^ ((drow[i] >> 3) & 1));
-  }
-  // key rows at or beyond L are fetched from key 0 of this batch row (always in bounds)
-  auto issue = [&](int st, int kt) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int key = kt * KT + drow[i];
-      const uint32_t off = __umul24(static_cast<uint32_t>(key < g.L ? key : 0), rowbytes) + dcoff[i];
-      dma16_at(kbase, off, reinterpret_cast<_Float16*>(raw_at(st, 0) + (4 * wave + 2 * i) * D));
-      dma16_at(vbase, off, reinterpret_cast<_Float16*>(raw_at(st, 1) + (4 * wave + 2 * i) * D));
-    }
-  };
-  issue(0, 0);
-  if (ntiles > 1) issue(1, 1);
-
-  // ---- conversion of one raw stage into one split buffer ------------------------------------
+  // ---- K / V: converting thread t loads row crow, channels 8c .. 8c + 7 of both tiles into
+  // registers one step ahead (32 contiguous bytes each; the 16 threads of a row segment read 256
+  // contiguous bytes) and splits them into the buffer of the tile. Key rows at or beyond L are
+  // read from key 0 of this batch row (always in bounds).
   const int crow = ((tid >> 5) & 7) + 8 * ((tid >> 3) & 1);
   const int cc = (tid & 7) + 8 * ((tid >> 4) & 1);
-  const int cf = (crow >> 3) & 1;
-  auto convert = [&](int st, int buf) {
+  floatx4 xk[2], xv[2];
+  auto load_tile = [&](int kt) {
+    const int key = kt * KT + crow;
+    const uint32_t off = __umul24(static_cast<uint32_t>(key < g.L ? key : 0), rowbytes) + 32u * cc;
+    const char* kb = reinterpret_cast<const char*>(kbase) + off;
+    const char* vb = reinterpret_cast<const char*>(vbase) + off;
+    xk[0] = *reinterpret_cast<const floatx4*>(kb);
+    xk[1] = *reinterpret_cast<const floatx4*>(kb + 16);
+    xv[0] = *reinterpret_cast<const floatx4*>(vb);
+    xv[1] = *reinterpret_cast<const floatx4*>(vb + 16);
+  };
+  auto convert = [&](int buf) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const float* src = raw_at(st, t) + crow * D;
-      const floatx4 x0 = *reinterpret_cast<const floatx4*>(src + 4 * ((2 * cc) ^ cf));
-      const floatx4 x1 = *reinterpret_cast<const floatx4*>(src + 4 * ((2 * cc + 1) ^ cf));
       uint4v w1, w2, w3;
-      split3x8(x0, x1, w1, w2, w3);
+      if (t == 0) split3x8(xk[0], xk[1], w1, w2, w3);
+      else split3x8(xv[0], xv[1], w1, w2, w3);
       const int pos = crow * D + 8 * (cc ^ (t == 0 ? (crow & 15) : vsw_x3(crow)));
       *reinterpret_cast<uint4v*>(spl_at(buf, t, 0) + pos) = w1;
       *reinterpret_cast<uint4v*>(spl_at(buf, t, 1) + pos) = w2;
       *reinterpret_cast<uint4v*>(spl_at(buf, t, 2) + pos) = w3;
     }
   };
+  load_tile(0);
 
   // ---- Q: lane (r, g) holds channels 32s + 8g .. +7 of query r, as three bf16 planes ---------
   // q rows of one batch row lie within S * H * D floats (below 2^31 bytes, checked by the
@@ -1507,9 +1495,13 @@ __global__ __launch_bounds__(256, 2) void attn_f32x3(X3Args a) {
       pw[1][w] = __builtin_amdgcn_perm(u1[2 * w + 1], u1[2 * w], 0x07060302u);
       pw[2][w] = __builtin_amdgcn_perm(u2[2 * w + 1], u2[2 * w], 0x07060302u);
     }
-    const bf16x8 bp11 = __builtin_bit_cast(bf16x8, uint4v{pw[0][0], pw[0][1], pw[0][0], pw[0][1]});
-    const bf16x8 bp22 = __builtin_bit_cast(bf16x8, uint4v{pw[1][0], pw[1][1], pw[1][0], pw[1][1]});
-    const bf16x8 bp13 = __builtin_bit_cast(bf16x8, uint4v{pw[0][0], pw[0][1], pw[2][0], pw[2][1]});
+    // [p2 p2 p1 p1 p3]: the B operands [p2,p2], [p1,p1], [p1,p3] are 4-register windows of it
+    typedef uint32_t u32x10 __attribute__((ext_vector_type(10)));
+    const u32x10 pq = {pw[1][0], pw[1][1], pw[1][0], pw[1][1], pw[0][0],
+                       pw[0][1], pw[0][0], pw[0][1], pw[2][0], pw[2][1]};
+    const bf16x8 bp22 = __builtin_bit_cast(bf16x8, __builtin_shufflevector(pq, pq, 0, 1, 2, 3));
+    const bf16x8 bp11 = __builtin_bit_cast(bf16x8, __builtin_shufflevector(pq, pq, 4, 5, 6, 7));
+    const bf16x8 bp13 = __builtin_bit_cast(bf16x8, __builtin_shufflevector(pq, pq, 6, 7, 8, 9));
     if (__any(grow)) rescale(m_run - m_new);
     l_run += (pf[0] + pf[1]) + (pf[2] + pf[3]);
     m_run = m_new;
@@ -1522,37 +1514,39 @@ __global__ __launch_bounds__(256, 2) void attn_f32x3(X3Args a) {
       const shortx4 v1 = lds_read_tr_s(v1p + off);
       const shortx4 v2 = lds_read_tr_s(v1p + TILE + off);
       const shortx4 v3 = lds_read_tr_s(v1p + 2 * TILE + off);
-      const bf16x8 a12 = __builtin_bit_cast(bf16x8, __builtin_shufflevector(v1, v2, 0, 1, 2, 3, 4, 5, 6, 7));
-      const bf16x8 a31 = __builtin_bit_cast(bf16x8, __builtin_shufflevector(v3, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+      // [v3 v1 v2]: the A operands [v1,v2] and [v3,v1] are 4-register windows of it
+      typedef short s16x12 __attribute__((ext_vector_type(12)));
+      const shortx8 v31 = __builtin_shufflevector(v3, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+      const s16x12 vt = __builtin_shufflevector(v31, __builtin_shufflevector(v2, v2, 0, 1, 2, 3, 0, 1, 2, 3),
+                                                0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11);
+      const bf16x8 a12 = __builtin_bit_cast(bf16x8, __builtin_shufflevector(vt, vt, 4, 5, 6, 7, 8, 9, 10, 11));
+      const bf16x8 a31 = __builtin_bit_cast(bf16x8, __builtin_shufflevector(vt, vt, 0, 1, 2, 3, 4, 5, 6, 7));
       o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a12, bp11, o[dt], 0, 0, 0);
       o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a12, bp22, o[dt], 0, 0, 0);
       o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a31, bp13, o[dt], 0, 0, 0);
     }
   };
 
-  // The q loads were issued after both DMA tiles and have been waited for: tile 0 (and 1) have
-  // landed. Split tile 0 before the first step.
-  wait_vmcnt<0>();
-  stage_barrier();
-  convert(0, 0);
-  // Step kt (parity c = kt & 1, a compile-time constant): tile kt + 1 (raw stage c ^ 1, DMA from
-  // step kt - 1) has landed, split buffer c holds tile kt (converted at step kt - 1), raw stage c
-  // and split buffer c ^ 1 are free after the barrier; tile kt + 2 goes to raw stage c, tile
-  // kt + 1 is converted into buffer c ^ 1 while tile kt is computed.
+  // Tile 0 is split into buffer 0 and tile 1 loaded before the first step. Step kt (parity
+  // c = kt & 1, a compile-time constant): after the barrier buffer c holds tile kt (split at
+  // step kt - 1) and buffer c ^ 1 is free (computed at step kt - 1); tile kt + 1 (in registers
+  // since step kt - 1) is split into buffer c ^ 1, tile kt + 2 is loaded, tile kt is computed.
+  convert(0);
+  if (ntiles > 1) load_tile(1);
   auto step = [&](int kt, auto parity) {
     constexpr int c = decltype(parity)::value;
-    wait_vmcnt<0>();
     wait_lgkmcnt<0>();
     stage_barrier();
-    if (kt + 2 < ntiles) issue(c, kt + 2);
-    if (kt + 1 < ntiles) convert(c ^ 1, c ^ 1);
+    if (kt + 1 < ntiles) {
+      convert(c ^ 1);
+      if (kt + 2 < ntiles) load_tile(kt + 2);
+    }
     if (kt * KT < g.wave_end) compute(kt, c);
   };
   for (int kt = 0; kt < ntiles; kt += 2) {
     step(kt, Stage<0>{});
     if (kt + 1 < ntiles) step(kt + 1, Stage<1>{});
   }
-  wait_vmcnt<0>();
   wait_lgkmcnt<0>();
   const float inv = __builtin_amdgcn_rcpf(rowsum4(l_run));
   stage_barrier();
