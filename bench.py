@@ -12,7 +12,8 @@ HIP-event timings, and the NumPy CPU oracle timed on the host on a bounded sampl
 cores, plus float32 and a one-thread float64 run). Layer 0 is checked against the float64 oracle
 (max-abs <= 1e-4 with fp32 output; the exit status is 1 otherwise). A `secondary` object carries
 kernel times and roofline fractions of the other configurations measured in the same run:
-bge_32x512, qwen3_8x512, qwen_qkv4_16x256 and the headline shape at full length with fp16 output.
+bge_32x512, qwen3_8x512 (fused and fp32 routes), qwen_qkv4_16x256 and the headline shape at full
+length with fp16 output.
 
 --workload selects one of the other measured configurations instead (one JSON line each):
   qwen3_8x512       B=8, S=512, lengths U{64..512} (seed 3), same fused path, 8 layers
@@ -983,20 +984,24 @@ def _kernel_summary(result: dict, peak_tflops: float) -> dict:
     }
     if "mfma_tflops" in roof:  # attention kernels on an HBM roof: their MFMA share as well
         summary["mfma_frac"] = roof["mfma_tflops"] / peak_tflops
+    if "max_abs_err_layer0" in result:
+        summary["max_abs_err_layer0"] = result["max_abs_err_layer0"]
     return summary
 
 
 def secondary_measurements(args) -> dict:
     """Kernel times and roofline fractions of the other configurations, measured in the same run
     (2 warmup and 5 timed steps each, no CPU leg): BGE-small 32x512 fp32 attention (4 layers),
-    Qwen3 8x512 fused attention (8 layers), the uint4 QKV block 16x256 (8 layers), and the
-    headline shape at full length (32 x 512, every length 512, fp16 output, 4 layers)."""
+    Qwen3 8x512 fused attention (8 layers), the same shape on the fp32 route (4 layers), the
+    uint4 QKV block 16x256 (8 layers), and the headline shape at full length (32 x 512, every
+    length 512, fp16 output, 4 layers)."""
     sub = argparse.Namespace(steps=5, warmup=2, no_cpu_baseline=True, calibrate_copy_mib=0)
     out = {"bge_32x512": _kernel_summary(bench_bge(sub, layers=4), PEAK_F32_TFLOPS)}
     shape, lengths = workloads.qwen3_8x512()
     out["qwen3_8x512"] = _kernel_summary(
         bench_qwen(sub, "qwen3_8x512", shape, lengths, 3, 8, "uniform [64,512], seed 3",
                    headline=False), PEAK_F16_TFLOPS)
+    out["qwen3_8x512_f32"] = _kernel_summary(bench_qwen_f32(sub, layers=4), PEAK_F32_TFLOPS)
     out["qwen_qkv4_16x256"] = _kernel_summary(bench_qkv4_block(sub, layers=8), PEAK_F16_TFLOPS)
     full = workloads.Shape(32, 512, 16, 8, 128, causal=True)
     out["qwen3_32x512_full_f16out"] = _kernel_summary(
