@@ -1281,7 +1281,8 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(F16Args a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// fp32 attention on bf16 MFMA (routes attention_tiled / attention_tail_128 at D = 128).
+// fp32 attention on bf16 MFMA (routes attention_tiled / attention_tail_32 / attention_tail_128
+// at D = 32, 64, 128).
 //
 // An fp32 value x splits exactly into three bf16 terms by truncation: b1 = the upper half of x's
 // bits (sign, exponent, 7 mantissa bits), r1 = x - b1 (exact: the lower 16 significand bits),
@@ -1292,19 +1293,15 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(F16Args a) {
 // fp32 MFMA rate, so the six products still cost well under half of the fp32 instructions.
 //
 // Geometry, schedule and output layout are those of attn_f16_mfma (16 query rows per wavefront,
-// four wave blocks of one (batch row, kv head) plane per workgroup, 16-key tiles). Q is split in
-// registers. K and V tiles are loaded as fp32 into registers one step ahead and split once per
-// workgroup into three bf16 planes each, in two LDS buffers (48 KiB: three workgroups per CU at
-// <= 168 VGPRs): step t splits tile t + 1 and loads tile t + 2 while its MFMAs run on tile t,
-// one barrier per step.
-//   split [buffer][K, V][plane][16 rows][128] bf16: K chunk c at c ^ (r & 15) (the score reads
-//         of one k-step hit 16 rows), V chunk c at c ^ (2 (r & 7) ^ 8 (r >> 3 & 1)) (the
-//         transposed reads of four rows hit four bank groups)
-// Converting thread t owns row (t >> 5 & 7) + 8 (t >> 3 & 1) and channels 8c .. 8c + 7 with
-// c = (t & 7) + 8 (t >> 4 & 1): the 16 threads of one LDS access cover rows r and r + 8, which
-// makes its split writes conflict-free under the swizzles above.
+// four wave blocks of one (batch row, kv head) plane per workgroup); tiles hold 2048 / D keys
+// (8 KiB of fp32 per tensor). Q is split in registers. K and V tiles are loaded as fp32 into
+// registers one step ahead and split once per workgroup into three bf16 planes each, in two LDS
+// buffers (48 KiB: three workgroups per CU at <= 168 VGPRs): step t splits tile t + 1 and loads
+// tile t + 2 while its MFMAs run on tile t, one barrier per step.
+//   split [buffer][K, V][plane][2048 / D rows][D] bf16, chunks swizzled by ksw_x3 / vsw_x3
 // Score terms per k-step: (k1,q1) (k1,q2) (k2,q1) (k1,q3) (k2,q2) (k3,q1); output terms per
-// 16-channel block, each MFMA stacking two (probability, value) pairs over the same four keys:
+// 16-channel block and 16-key block, each MFMA stacking two (probability, value) pairs over the
+// same four keys:
 // [p1,p1]x[v1,v2], [p2,p2]x[v1,v2], [p1,p3]x[v3,v1].
 // ---------------------------------------------------------------------------------------------
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -1338,7 +1335,20 @@ __device__ __forceinline__ shortx4 lds_read_tr_s(const uint16_t* p) {
       (__attribute__((address_space(3))) shortx4*)(p));
 }
 
-__device__ __forceinline__ int vsw_x3(int row) { return (2 * (row & 7)) ^ (8 * ((row >> 3) & 1)); }
+// Chunk swizzles of the split planes (rows of D bf16 = D / 8 chunks of 16 bytes). The score
+// reads of one k-step take one chunk from each of 16 consecutive rows, so within each group of
+// rows that share a bank line (16 / (D / 8) rows) the chunk is XORed with the line index; the
+// transposed V reads take 32 bytes from each of 4 consecutive rows, which must land in four
+// 32-byte bank groups.
+template <int D>
+__device__ __forceinline__ int ksw_x3(int row) {
+  constexpr int CPR = D / 8, RPL = 16 / CPR;
+  return (row / RPL) & (CPR - 1);
+}
+template <int D>
+__device__ __forceinline__ int vsw_x3(int row) {
+  return D == 128 ? 2 * (row & 7) : D == 64 ? 2 * ((row >> 1) & 3) : 0;
+}
 
 struct X3Args {
   const float* q;
@@ -1354,8 +1364,9 @@ struct X3Args {
 
 template <int D>
 __global__ __launch_bounds__(256, 2) void attn_f32x3(X3Args a) {
-  static_assert(D == 128, "the split-bf16 fp32 kernel serves D = 128");
-  constexpr int KT = 16, NS = D / 32, NDT = D / 16;
+  static_assert(D == 32 || D == 64 || D == 128, "the split-bf16 fp32 kernel serves D = 32, 64, 128");
+  // KT keys per tile: every tile is 8 KiB of fp32 per tensor, 8 channels of one row per thread
+  constexpr int KT = 2048 / D, NKB = KT / 16, NS = D / 32, NDT = D / 16, CPR = D / 8;
   constexpr int TILE = KT * D;                       // elements per K or V tile
   constexpr int SPLIT_BYTES = 2 * 2 * 3 * TILE * 2;  // [buffer][K, V][plane] bf16
   constexpr int RB = D * 4, RS = RB + 16;            // output staging rows
@@ -1377,18 +1388,18 @@ __global__ __launch_bounds__(256, 2) void attn_f32x3(X3Args a) {
   const int qpos_c = min(qpos, S - 1);
   const int limit = a.bidi ? g.L : min(qpos + 1, g.L);
   const int ntiles = (g.wg_end + KT - 1) / KT;
-  // plane bases are wave-uniform; per-lane DMA offsets are 32-bit bytes within the plane
+  // plane bases are wave-uniform; per-lane load offsets are 32-bit bytes within the plane
   // (S * KV * D * 4 < 2^32, checked by the launcher)
   const float* kbase = a.k + (static_cast<size_t>(g.b) * S * KV + g.kvh) * D;
   const float* vbase = a.v + (static_cast<size_t>(g.b) * S * KV + g.kvh) * D;
   const uint32_t rowbytes = static_cast<uint32_t>(KV * D * 4);
 
-  // ---- K / V: converting thread t loads row crow, channels 8c .. 8c + 7 of both tiles into
-  // registers one step ahead (32 contiguous bytes each; the 16 threads of a row segment read 256
-  // contiguous bytes) and splits them into the buffer of the tile. Key rows at or beyond L are
-  // read from key 0 of this batch row (always in bounds).
-  const int crow = ((tid >> 5) & 7) + 8 * ((tid >> 3) & 1);
-  const int cc = (tid & 7) + 8 * ((tid >> 4) & 1);
+  // ---- K / V: thread t loads row crow = t / (D / 8), channels 8c .. 8c + 7 (c = t % (D / 8)) of
+  // both tiles into registers one step ahead (32 contiguous bytes; a row's threads read the whole
+  // row) and splits them into the buffer of the tile: the 16 threads of one LDS write cover whole
+  // bank lines, so the writes are conflict-free under any per-row chunk permutation. Key rows at
+  // or beyond L are read from key 0 of this batch row (always in bounds).
+  const int crow = tid / CPR, cc = tid % CPR;
   floatx4 xk[2], xv[2];
   auto load_tile = [&](int kt) {
     const int key = kt * KT + crow;
@@ -1406,7 +1417,7 @@ __global__ __launch_bounds__(256, 2) void attn_f32x3(X3Args a) {
       uint4v w1, w2, w3;
       if (t == 0) split3x8(xk[0], xk[1], w1, w2, w3);
       else split3x8(xv[0], xv[1], w1, w2, w3);
-      const int pos = crow * D + 8 * (cc ^ (t == 0 ? (crow & 15) : vsw_x3(crow)));
+      const int pos = crow * D + 8 * (cc ^ (t == 0 ? ksw_x3<D>(crow) : vsw_x3<D>(crow)));
       *reinterpret_cast<uint4v*>(spl_at(buf, t, 0) + pos) = w1;
       *reinterpret_cast<uint4v*>(spl_at(buf, t, 1) + pos) = w2;
       *reinterpret_cast<uint4v*>(spl_at(buf, t, 2) + pos) = w3;
@@ -1445,85 +1456,105 @@ __global__ __launch_bounds__(256, 2) void attn_f32x3(X3Args a) {
     for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
   };
 
-  // tile kt from split buffer buf
+  // tile kt from split buffer buf; sc[kb][j] is key 16 kb + 4g + j of the tile
   auto compute = [&](int kt, int buf) {
     const uint16_t* k1p = spl_at(buf, 0, 0);
-    floatx4 acc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
-    const int rbase = r * D, ksw16 = r & 15;
+    floatx4 sc[NKB];
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const int off = rbase + 8 * ((4 * s + gq) ^ ksw16);
-      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(k1p + off);
-      const bf16x8 k2 = *reinterpret_cast<const bf16x8*>(k1p + TILE + off);
-      const bf16x8 k3 = *reinterpret_cast<const bf16x8*>(k1p + 2 * TILE + off);
-      floatx4& c = acc[s & 1];
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, q1[s], c, 0, 0, 0);
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, q2[s], c, 0, 0, 0);
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2, q1[s], c, 0, 0, 0);
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, q3[s], c, 0, 0, 0);
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2, q2[s], c, 0, 0, 0);
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k3, q1[s], c, 0, 0, 0);
+    for (int kb = 0; kb < NKB; ++kb) {
+      floatx4 acc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+      const int row = 16 * kb + r, rbase = row * D, ksw = ksw_x3<D>(row);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const int off = rbase + 8 * ((4 * s + gq) ^ ksw);
+        const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(k1p + off);
+        const bf16x8 k2 = *reinterpret_cast<const bf16x8*>(k1p + TILE + off);
+        const bf16x8 k3 = *reinterpret_cast<const bf16x8*>(k1p + 2 * TILE + off);
+        floatx4& c = acc[(s + kb) & 1];
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, q1[s], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, q2[s], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2, q1[s], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, q3[s], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2, q2[s], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k3, q1[s], c, 0, 0, 0);
+      }
+      mfma_result_fence(acc[0], acc[1]);
+      sc[kb] = acc[0] + acc[1];
     }
-    mfma_result_fence(acc[0], acc[1]);
-    floatx4 sc = acc[0] + acc[1];
-    // element j is key 4g + j of this tile
     if (kt * KT + KT > g.limit_min) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (kt * KT + 4 * gq + j >= limit) sc[j] = -INFINITY;
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (kt * KT + 16 * kb + 4 * gq + j >= limit) sc[kb][j] = -INFINITY;
     }
-    const float mloc = rowmax4(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]))) * scale_log2;
+    float mx = fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3]));
+#pragma unroll
+    for (int kb = 1; kb < NKB; ++kb)
+      mx = fmaxf(mx, fmaxf(fmaxf(sc[kb][0], sc[kb][1]), fmaxf(sc[kb][2], sc[kb][3])));
+    const float mloc = rowmax4(mx) * scale_log2;
     const bool grow = mloc > m_run + kMaxSlack;
     // every row sees key 0 in its first tile (L >= 1), so m_new is finite from tile 0 on
     const float m_new = grow ? mloc : m_run;
-    float pf[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) pf[j] = __builtin_amdgcn_exp2f(fmaf(sc[j], scale_log2, -m_new));
-    // the probabilities as three bf16 terms (exact), keys 4g .. 4g + 3
-    uint32_t u0[4], u1[4], u2[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      u0[j] = __float_as_uint(pf[j]);
-      const float r1 = pf[j] - __uint_as_float(u0[j] & 0xffff0000u);
-      u1[j] = __float_as_uint(r1);
-      u2[j] = __float_as_uint(r1 - __uint_as_float(u1[j] & 0xffff0000u));
-    }
-    uint32_t pw[3][2];
-#pragma unroll
-    for (int w = 0; w < 2; ++w) {
-      pw[0][w] = __builtin_amdgcn_perm(u0[2 * w + 1], u0[2 * w], 0x07060302u);
-      pw[1][w] = __builtin_amdgcn_perm(u1[2 * w + 1], u1[2 * w], 0x07060302u);
-      pw[2][w] = __builtin_amdgcn_perm(u2[2 * w + 1], u2[2 * w], 0x07060302u);
-    }
-    // [p2 p2 p1 p1 p3]: the B operands [p2,p2], [p1,p1], [p1,p3] are 4-register windows of it
+    // the probabilities as three bf16 terms (exact); per key block, in the order
+    // [p2 p2 p1 p1 p3], of which the B operands [p2,p2], [p1,p1], [p1,p3] are 4-register windows
     typedef uint32_t u32x10 __attribute__((ext_vector_type(10)));
-    const u32x10 pq = {pw[1][0], pw[1][1], pw[1][0], pw[1][1], pw[0][0],
-                       pw[0][1], pw[0][0], pw[0][1], pw[2][0], pw[2][1]};
-    const bf16x8 bp22 = __builtin_bit_cast(bf16x8, __builtin_shufflevector(pq, pq, 0, 1, 2, 3));
-    const bf16x8 bp11 = __builtin_bit_cast(bf16x8, __builtin_shufflevector(pq, pq, 4, 5, 6, 7));
-    const bf16x8 bp13 = __builtin_bit_cast(bf16x8, __builtin_shufflevector(pq, pq, 6, 7, 8, 9));
-    if (__any(grow)) rescale(m_run - m_new);
-    l_run += (pf[0] + pf[1]) + (pf[2] + pf[3]);
-    m_run = m_new;
-    // V row 4g + r/4, channels 16dt + 4(r%4) .. +3 of each plane
-    const uint16_t* v1p = spl_at(buf, 1, 0);
-    const int vrow = 4 * gq + (r >> 2), vsw = vsw_x3(vrow);
+    u32x10 pq[NKB];
+    float psum = 0.0f;
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      const int off = vrow * D + 8 * ((2 * dt + ((r & 3) >> 1)) ^ vsw) + 4 * (r & 1);
-      const shortx4 v1 = lds_read_tr_s(v1p + off);
-      const shortx4 v2 = lds_read_tr_s(v1p + TILE + off);
-      const shortx4 v3 = lds_read_tr_s(v1p + 2 * TILE + off);
-      // [v3 v1 v2]: the A operands [v1,v2] and [v3,v1] are 4-register windows of it
-      typedef short s16x12 __attribute__((ext_vector_type(12)));
-      const shortx8 v31 = __builtin_shufflevector(v3, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-      const s16x12 vt = __builtin_shufflevector(v31, __builtin_shufflevector(v2, v2, 0, 1, 2, 3, 0, 1, 2, 3),
-                                                0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11);
-      const bf16x8 a12 = __builtin_bit_cast(bf16x8, __builtin_shufflevector(vt, vt, 4, 5, 6, 7, 8, 9, 10, 11));
-      const bf16x8 a31 = __builtin_bit_cast(bf16x8, __builtin_shufflevector(vt, vt, 0, 1, 2, 3, 4, 5, 6, 7));
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a12, bp11, o[dt], 0, 0, 0);
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a12, bp22, o[dt], 0, 0, 0);
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a31, bp13, o[dt], 0, 0, 0);
+    for (int kb = 0; kb < NKB; ++kb) {
+      float pf[4];
+      uint32_t u0[4], u1[4], u2[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        pf[j] = __builtin_amdgcn_exp2f(fmaf(sc[kb][j], scale_log2, -m_new));
+        u0[j] = __float_as_uint(pf[j]);
+        const float r1 = pf[j] - __uint_as_float(u0[j] & 0xffff0000u);
+        u1[j] = __float_as_uint(r1);
+        u2[j] = __float_as_uint(r1 - __uint_as_float(u1[j] & 0xffff0000u));
+      }
+      psum += (pf[0] + pf[1]) + (pf[2] + pf[3]);
+      uint32_t pw[3][2];
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        pw[0][w] = __builtin_amdgcn_perm(u0[2 * w + 1], u0[2 * w], 0x07060302u);
+        pw[1][w] = __builtin_amdgcn_perm(u1[2 * w + 1], u1[2 * w], 0x07060302u);
+        pw[2][w] = __builtin_amdgcn_perm(u2[2 * w + 1], u2[2 * w], 0x07060302u);
+      }
+      pq[kb] = u32x10{pw[1][0], pw[1][1], pw[1][0], pw[1][1], pw[0][0],
+                      pw[0][1], pw[0][0], pw[0][1], pw[2][0], pw[2][1]};
+    }
+    if (__any(grow)) rescale(m_run - m_new);
+    l_run += psum;
+    m_run = m_new;
+    // V row 16 kb + 4g + r/4, channels 16dt + 4(r%4) .. +3 of each plane
+    const uint16_t* v1p = spl_at(buf, 1, 0);
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const bf16x8 bp22 = __builtin_bit_cast(bf16x8, __builtin_shufflevector(pq[kb], pq[kb], 0, 1, 2, 3));
+      const bf16x8 bp11 = __builtin_bit_cast(bf16x8, __builtin_shufflevector(pq[kb], pq[kb], 4, 5, 6, 7));
+      const bf16x8 bp13 = __builtin_bit_cast(bf16x8, __builtin_shufflevector(pq[kb], pq[kb], 6, 7, 8, 9));
+      const int vrow = 16 * kb + 4 * gq + (r >> 2), vsw = vsw_x3<D>(vrow);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const int off = vrow * D + 8 * ((2 * dt + ((r & 3) >> 1)) ^ vsw) + 4 * (r & 1);
+        const shortx4 v1 = lds_read_tr_s(v1p + off);
+        const shortx4 v2 = lds_read_tr_s(v1p + TILE + off);
+        const shortx4 v3 = lds_read_tr_s(v1p + 2 * TILE + off);
+        // [v3 v1 v2]: the A operands [v1,v2] and [v3,v1] are 4-register windows of it
+        typedef short s16x12 __attribute__((ext_vector_type(12)));
+        const shortx8 v31 = __builtin_shufflevector(v3, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+        const s16x12 vt = __builtin_shufflevector(
+            v31, __builtin_shufflevector(v2, v2, 0, 1, 2, 3, 0, 1, 2, 3), 0, 1, 2, 3, 4, 5, 6, 7, 8,
+            9, 10, 11);
+        const bf16x8 a12 =
+            __builtin_bit_cast(bf16x8, __builtin_shufflevector(vt, vt, 4, 5, 6, 7, 8, 9, 10, 11));
+        const bf16x8 a31 =
+            __builtin_bit_cast(bf16x8, __builtin_shufflevector(vt, vt, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a12, bp11, o[dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a12, bp22, o[dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a31, bp13, o[dt], 0, 0, 0);
+      }
     }
   };
 
@@ -1657,7 +1688,7 @@ hipError_t launch_attention_scalar(const AttnArgs& a, hipStream_t st) {
 // inside one (batch row, kv head) plane (row * rowbytes by __umul24), q loads 32-bit offsets inside
 // one batch row, output stores 32-bit offsets inside 16 rows of a wave block.
 static bool attention_f32x3_fits(int B, int S, int H, int KV, int D) {
-  if (D != 128 || B <= 0 || S <= 0 || H <= 0 || KV <= 0 || H % KV) return false;
+  if ((D != 32 && D != 64 && D != 128) || B <= 0 || S <= 0 || H <= 0 || KV <= 0 || H % KV) return false;
   const int G = H / KV;
   const int hsh = __builtin_ctz(static_cast<unsigned>(f16_heads_per_wave(G)));
   if (!geometry_fits(B, KV, f16_wave_blocks(S, G), G >> hsh)) return false;
@@ -1701,6 +1732,35 @@ hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st) {
   auto q = static_cast<const float*>(a.q), k = static_cast<const float*>(a.k),
        v = static_cast<const float*>(a.v);
   auto o = static_cast<float*>(a.out);
+  if (attention_f32x3_fits(a.B, a.S, a.H, a.KV, a.D)) {
+    X3Args x{};
+    x.q = q;
+    x.k = k;
+    x.v = v;
+    x.lengths = a.lengths;
+    x.out = o;
+    x.B = a.B;
+    x.S = a.S;
+    x.H = a.H;
+    x.KV = a.KV;
+    x.scale_log2 = sl2;
+    x.bidi = a.bidi;
+    x.shp = f16_shape(a.B, a.S, a.H, a.KV);
+    const dim3 grid = sched_grid(a.B, a.KV, (x.shp.nwb + 3) / 4);
+    switch (a.D) {
+      case 32:
+        attn_f32x3<32><<<grid, 256, 0, st>>>(x);
+        break;
+      case 64:
+        attn_f32x3<64><<<grid, 256, 0, st>>>(x);
+        break;
+      default:
+        attn_f32x3<128><<<grid, 256, 0, st>>>(x);
+        break;
+    }
+    return hipGetLastError();
+  }
+  // shapes beyond attn_f32x3's 32-bit offsets: the fp32-MFMA kernels
   switch (a.D) {
     case 32:
       attn_f32_ring<32><<<grid, 256, 0, st>>>(q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
@@ -1709,25 +1769,8 @@ hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st) {
       attn_f32_ring<64><<<grid, 256, 0, st>>>(q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
       break;
     case 128:
-      if (attention_f32x3_fits(a.B, a.S, a.H, a.KV, a.D)) {
-        X3Args x{};
-        x.q = q;
-        x.k = k;
-        x.v = v;
-        x.lengths = a.lengths;
-        x.out = o;
-        x.B = a.B;
-        x.S = a.S;
-        x.H = a.H;
-        x.KV = a.KV;
-        x.scale_log2 = sl2;
-        x.bidi = a.bidi;
-        x.shp = f16_shape(a.B, a.S, a.H, a.KV);
-        attn_f32x3<128><<<sched_grid(a.B, a.KV, (x.shp.nwb + 3) / 4), 256, 0, st>>>(x);
-      } else {
-        attn_f32_split<128><<<split_grid(a.B, a.S, a.H, a.KV), 256, 0, st>>>(
-            q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
-      }
+      attn_f32_split<128><<<split_grid(a.B, a.S, a.H, a.KV), 256, 0, st>>>(
+          q, k, v, a.lengths, o, a.B, a.S, a.H, a.KV, sl2, a.bidi, shp);
       break;
     default:
       return hipErrorInvalidValue;
