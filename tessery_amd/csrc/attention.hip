@@ -1336,10 +1336,12 @@ __device__ __forceinline__ shortx4 lds_read_tr_s(const uint16_t* p) {
 }
 
 // Chunk swizzles of the split planes (rows of D bf16 = D / 8 chunks of 16 bytes). The score
-// reads of one k-step take one chunk from each of 16 consecutive rows, so within each group of
-// rows that share a bank line (16 / (D / 8) rows) the chunk is XORed with the line index; the
-// transposed V reads take 32 bytes from each of 4 consecutive rows, which must land in four
-// 32-byte bank groups.
+// reads of one k-step (16-byte accesses, served 16 lanes at a time) take one chunk from each of
+// 16 consecutive rows, so within each group of rows that share a bank line (16 / (D / 8) rows)
+// the chunk is XORed with the line index. The transposed V reads (8-byte accesses, served 32
+// lanes at a time) take 32 bytes from each of 8 consecutive rows, which must land in the eight
+// 32-byte bank groups: the 32-byte unit is XORed with the row's position among the rows that
+// share its bank-line offset.
 template <int D>
 __device__ __forceinline__ int ksw_x3(int row) {
   constexpr int CPR = D / 8, RPL = 16 / CPR;
@@ -1347,7 +1349,7 @@ __device__ __forceinline__ int ksw_x3(int row) {
 }
 template <int D>
 __device__ __forceinline__ int vsw_x3(int row) {
-  return D == 128 ? 2 * (row & 7) : D == 64 ? 2 * ((row >> 1) & 3) : 0;
+  return D == 128 ? 2 * (row & 7) : D == 64 ? 2 * ((row >> 1) & 3) : 2 * ((row >> 2) & 1);
 }
 
 struct X3Args {
