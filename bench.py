@@ -112,11 +112,11 @@ def time_cpu(layer: Callable[[], Any], budget_s: float = 12.0) -> tuple[Any, flo
 
 
 def run_timed(rt: HipRuntime, step: Callable[[], None], steps: int, warmup: int,
-              launches_per_step: int) -> dict[str, Any]:
+              launches_per_step: int, profile: bool = True) -> dict[str, Any]:
     """Warmup, then K steps launched back to back inside one command (synchronized before and
-    after), then the same steps replayed with HIP events around every launch on the runtime
-    stream (a command profiles at most 2048 launches). Returns wall seconds per step, event
-    seconds per step and the per-kernel mean launch durations."""
+    after), then (profile) the same steps replayed with HIP events around every launch on the
+    runtime stream (a command profiles at most 2048 launches). Returns wall seconds per step,
+    event seconds per step and the per-kernel mean launch durations."""
     for _ in range(warmup):
         with rt.command():
             step()
@@ -127,6 +127,8 @@ def run_timed(rt: HipRuntime, step: Callable[[], None], steps: int, warmup: int,
     wall = time.perf_counter() - launched
     gpu = rt.last_gpu_seconds
     log(f"timed {steps} steps: wall {wall * 1e3:.3f} ms, events {gpu * 1e3:.3f} ms")
+    if not profile:
+        return {"step": wall / steps, "gpu_step": gpu / steps if gpu >= 0 else None, "kernel_s": {}}
     prof_steps = max(1, min(steps, 2048 // launches_per_step))
     with rt.profile_kernels() as records:
         with rt.command():
@@ -248,12 +250,24 @@ def bench_qwen(args, name: str, shape, lengths, seed: int, layers: int, lengths_
             dst.close()
         log("inputs resident; warmup")
 
-        def step():
+        def direct():
             for s in sets:
                 fused_attention(rt, shape, s, lengths_buf, k_work, out_dtype)
 
-        t = run_timed(rt, step, args.steps, args.warmup, 2 * layers)
+        # a step is the layers' launches as one prepared plan, replayed as a cached HIP graph
+        # (recorded by the first warmup step; profiled steps launch directly)
+        bindings = [lengths_buf, k_work] + [s[n] for s in sets for n in sorted(s)]
+
+        def step():
+            with rt._execution_plan((name, layers, out_dtype), bindings) as replayed:
+                if not replayed:
+                    direct()
+
+        with rt._workspace():
+            t = run_timed(rt, step, args.steps, args.warmup, 2 * layers)
+        t_direct = run_timed(rt, direct, args.steps, 1, 2 * layers, profile=False)
         out0 = rt.read(sets[0]["out"], host0["q"].shape, np.float16 if out_bytes == 2 else np.float32)
+        graphs = rt.diagnostics()
 
     step_s = t["step"]
     attn_avg = t["kernel_s"]["attention_f16_norm_rope"]
@@ -289,6 +303,8 @@ def bench_qwen(args, name: str, shape, lengths, seed: int, layers: int, lengths_
         "mfma_frac": tflops / PEAK_F16_TFLOPS,
         "dense_convention_tflops": workloads.dense_flop(shape) * layers / step_s / 1e12,
         "gpu_event_ms_per_step": t["gpu_step"] * 1e3 if t["gpu_step"] is not None else None,
+        "ms_per_step_direct_launches": t_direct["step"] * 1e3,
+        "plan_graph": {"builds": graphs["graph_builds"], "launches": graphs["graph_launches"]},
         "kernel_us": {"attention_f16_norm_rope": attn_avg * 1e6,
                       "norm_rope_f16": t["kernel_s"]["norm_rope_f16"] * 1e6},
         "roofline": {
