@@ -981,7 +981,9 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
         ss = __builtin_amdgcn_fdot2(x2, x2, ss, false);
       }
     ss = rowsum4(ss);
-    const float inv = __builtin_amdgcn_rsqf(ss * (1.0f / static_cast<float>(D)) + eps);
+    float inv = __builtin_amdgcn_rsqf(ss * (1.0f / static_cast<float>(D)) + eps);
+    // D = 128: q is carried pre-multiplied by the softmax scale in log2 units (see PRE below)
+    if constexpr (KT == 16) inv *= scale_log2;
     wait_vmcnt_pin6<0>(tab);
     if constexpr (NS == 4) wait_vmcnt_pin6<0>(tab + 6);
     uint32_t hv[NS][4], lv[NS][4];  // word m / 2 of step s: channels (m, m + 1) packed
@@ -1021,6 +1023,14 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.0f;
+  // PRE (fused, D = 128): q arrives scaled, so scores come out in log2 units, and the QK^T chain
+  // starts from nb = -m_base instead of zero, m_base being the row max that the accumulated
+  // output refers to. A tile's scores are then s - m_base as they leave the MFMAs: the common
+  // tile computes its row max and one compare against thr = m_run + kMaxSlack - m_base (-inf
+  // before the first tile, kMaxSlack after it) and feeds the scores to exp2 as they stand.
+  constexpr bool PRE = FUSED && KT == 16;
+  float m_base = 0.0f, thr = -INFINITY;
+  floatx4 nb = floatx4{0.f, 0.f, 0.f, 0.f};
 
   // Rescale of the accumulated output and row sum when the running max moves by d (<= 0). Called
   // under a wave-uniform branch; the opaque copy of d keeps the exponential (a quarter-rate
@@ -1035,7 +1045,7 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
 
   // QK^T of one 16-key block whose rows start at kr (rows kr..kr+15 of the K tile)
   auto qk_block = [&](const _Float16* kt0, int kr) {
-    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+    floatx4 acc = PRE ? nb : floatx4{0.f, 0.f, 0.f, 0.f};
     const int row = kr + r, rbase = row * D, sw = ksw<D>(row);
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
@@ -1075,6 +1085,34 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
         for (int j = 0; j < 4; ++j)
           if (kt * KT + 4 * gq + j >= limit) sc[j] = -INFINITY;
       }
+      half4 pb, pl;
+      if constexpr (PRE) {
+        // sc = s - m_base. Lazy running max as below: every row sees key 0 in its first tile
+        // (L >= 1), so mloc is finite there and the first tile always moves the max.
+        const float mloc = rowmax4(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+        const bool grow = mloc > thr;
+        if (__any(grow)) {
+          const float m_new = grow ? m_base + mloc : m_run;
+          rescale(m_run - m_new);
+          // this tile's scores move to the new base; the next tiles' start from it
+          const float shift = grow ? mloc : 0.0f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) sc[j] -= shift;
+          m_run = m_new;
+          m_base = grow ? m_new : m_base;
+          thr = grow ? kMaxSlack : thr;
+          nb = floatx4{-m_base, -m_base, -m_base, -m_base};
+        }
+        float pf[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pf[j] = __builtin_amdgcn_exp2f(sc[j]);
+        half2v h0, h1, l0, l1;
+        split2(pf[0], pf[1], one, h0, l0);
+        split2(pf[2], pf[3], one, h1, l1);
+        pb = __builtin_shufflevector(h0, h1, 0, 1, 2, 3);
+        pl = __builtin_shufflevector(l0, l1, 0, 1, 2, 3);
+        l_run += (pf[0] + pf[1]) + (pf[2] + pf[3]);
+      } else {
       const float mloc = rowmax4(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]))) * scale_log2;
       // lazy running max: moved only when a tile exceeds it by more than kMaxSlack
       const bool grow = mloc > m_run + kMaxSlack;
@@ -1083,7 +1121,6 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
       // what is accumulated is rescaled only when the max moved in some lane (factor exactly 1
       // in the others)
       if (__any(grow)) rescale(m_run - m_new);
-      half4 pb, pl;
       if constexpr (FUSED) {
         // P as hi + lo fp16 pair: the PV product sees P to ~22 bits, and the row sum is the
         // fp32 sum of the same values
@@ -1104,9 +1141,10 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
         // exactly with fp16 dot products
         l_run = dot_ones(pb, l_run);
       }
+      m_run = m_new;
+      }
       // l_run holds this lane's share of the row sum (its own keys); the four shares of a query
       // are combined once, after the last tile
-      m_run = m_new;
       // V row 4g + r/4, channels 16dt + 4(r%4) .. +3; chunk swizzled by 2*(row & 7)
       const int vrow = 4 * gq + (r >> 2);
 #pragma unroll
