@@ -1088,10 +1088,13 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
       half4 pb, pl;
       if constexpr (PRE) {
         // sc = s - m_base. Lazy running max as below: every row sees key 0 in its first tile
-        // (L >= 1), so mloc is finite there and the first tile always moves the max.
-        const float mloc = rowmax4(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-        const bool grow = mloc > thr;
-        if (__any(grow)) {
+        // (L >= 1), so mloc is finite there and the first tile always moves the max. A row's
+        // max exceeds thr only if one of its four lanes' own maxima does, so the row reduction
+        // runs only in the branch that moves the max.
+        const float lmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        if (__any(lmax > thr)) {
+          const float mloc = rowmax4(lmax);
+          const bool grow = mloc > thr;
           const float m_new = grow ? m_base + mloc : m_run;
           rescale(m_run - m_new);
           // this tile's scores move to the new base; the next tiles' start from it
