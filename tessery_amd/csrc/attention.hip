@@ -746,20 +746,6 @@ __device__ __forceinline__ float dot_ones(half4 p, float acc) {
   return __builtin_amdgcn_fdot2(h2{p[2], p[3]}, one, acc, false);
 }
 
-// x0 * sc and x1 * sc rounded to fp16 and packed (hi), and the fp16 of what hi leaves of each
-// (lo = fp16(x * sc - hi), the product exact inside the fma): four v_fma_mix instructions. The
-// lo/hi forms write one half of the destination and keep the other, so each packed pair is built
-// in place; hi's halves enter the lo fmas as fp16 operands (op_sel picks the upper half).
-__device__ __forceinline__ void scaled_split2(float x0, float x1, float sc, uint32_t& hi,
-                                              uint32_t& lo) {
-  asm("v_fma_mixlo_f16 %0, %2, %4, 0\n\t"
-      "v_fma_mixhi_f16 %0, %3, %4, 0\n\t"
-      "v_fma_mixlo_f16 %1, %2, %4, -%0 op_sel_hi:[0,0,1]\n\t"
-      "v_fma_mixhi_f16 %1, %3, %4, -%0 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
-      : "=&v"(hi), "=&v"(lo)
-      : "v"(x0), "v"(x1), "v"(sc));
-}
-
 // The score accumulators of a QK^T chain are read by VALU (row max, masking) right after the last
 // v_mfma_f32_16x16x32_f16 of the chain, and the hardware does not interlock that read: it needs 8
 // wait states after the MFMA. The compiler counts them inside a basic block but not across the

@@ -32,6 +32,20 @@ __device__ __forceinline__ float bf16_to_float(uint16_t w) {
   return __uint_as_float(static_cast<uint32_t>(w) << 16);
 }
 
+// x0 * sc and x1 * sc rounded to fp16 and packed (hi), and the fp16 of what hi leaves of each
+// (lo = fp16(x * sc - hi), the product exact inside the fma): four v_fma_mix instructions. The
+// lo/hi forms write one half of the destination and keep the other, so each packed pair is built
+// in place; hi's halves enter the lo fmas as fp16 operands (op_sel picks the upper half).
+__device__ __forceinline__ void scaled_split2(float x0, float x1, float sc, uint32_t& hi,
+                                              uint32_t& lo) {
+  asm("v_fma_mixlo_f16 %0, %2, %4, 0\n\t"
+      "v_fma_mixhi_f16 %0, %3, %4, 0\n\t"
+      "v_fma_mixlo_f16 %1, %2, %4, -%0 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixhi_f16 %1, %3, %4, -%0 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+      : "=&v"(hi), "=&v"(lo)
+      : "v"(x0), "v"(x1), "v"(sc));
+}
+
 // x ~ hi + lo in fp16 for a pair of floats: hi = fp16(x) rounded to nearest, lo = fp16(x - hi).
 // `one` is an opaque 1.0: it keeps x - hi an fma with hi as an fp16 operand (one v_fma_mix per
 // element) instead of a convert back and a subtraction.

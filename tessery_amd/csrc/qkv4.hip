@@ -418,25 +418,28 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
     load16_at<48>(xr[set][3], base, xoff);
   };
   // hi / lo halves of the x in register set `set` into LDS stage st; returns the partial row sum
+  // Chunk c holds k-offsets e = 4 (j & 1) + t of registers j = 2c, 2c + 1 in the order
+  // e0 e2 e4 e6 e1 e3 e5 e7 (evenodd_pos), so its packed pairs are (t, t + 2) of one register:
+  // word 2t + (j & 1) of chunk c pairs elements t and t + 2 (t = 0, 1) of register j
+  // (scaled_split2: hi = fp16(v 2^e), lo = fp16(v 2^e - hi), v 2^e exact).
   auto stage_x = [&](int set, int st) {
     float sum = 0.0f;
-    half8 hv[2], lv[2];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float v = xr[set][j][t];
-        const _Float16 h = static_cast<_Float16>(v * rscale);
-        const int pos = evenodd_pos(4 * (j & 1) + t);  // the order of the decoded codes
-        hv[j >> 1][pos] = h;
-        lv[j >> 1][pos] = static_cast<_Float16>(fmaf(v, rscale, -static_cast<float>(h)));
-        sum = fmaf(v, rscale, sum);
-      }
+      for (int t = 0; t < 4; ++t) sum = fmaf(xr[set][j][t], rscale, sum);
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
+      uint32_t hw[4], lw[4];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          scaled_split2(xr[set][2 * c + h][t], xr[set][2 * c + h][t + 2], rscale, hw[2 * t + h],
+                        lw[2 * t + h]);
       const int pos = srow * 64 + 8 * ((2 * spart + c) ^ xsw(srow));
-      *reinterpret_cast<half8*>(&xs[st][0][pos]) = hv[c];
-      *reinterpret_cast<half8*>(&xs[st][1][pos]) = lv[c];
+      *reinterpret_cast<uint4v*>(&xs[st][0][pos]) = uint4v{hw[0], hw[1], hw[2], hw[3]};
+      *reinterpret_cast<uint4v*>(&xs[st][1][pos]) = uint4v{lw[0], lw[1], lw[2], lw[3]};
     }
     return sum;
   };
