@@ -321,6 +321,35 @@ def test_qwen3_32x512(runtime, layer):
     assert err <= FUSED_F32_MAX, err
 
 
+@pytest.mark.parametrize("aligned_first", [False, True])
+def test_fused_late_maximum_moves_the_running_max(runtime, aligned_first):
+    """Fused route, causal: keys 40-55 line up with every query of head 0 (logit 128 / sqrt(128)
+    = 11.3, 16.3 in log2 units, past the lazy max's slack of 8) and point away from head 1's,
+    whose rows share the wavefront. q and k sit in channel 63, whose RoPE angle stays below
+    3e-4 rad up to position 200, so they stay aligned after the rotation. The running max of head
+    0 rows past position 40 moves in the middle of the row (rescale and score shift) while the
+    neighbouring lanes keep theirs. With aligned_first the aligned keys come first (0-15)
+    and every later tile stays far below the max."""
+    rng = np.random.default_rng(1234)
+    b, s, h, kv, d = 2, 200, 4, 2, 128
+    shape = workloads.Shape(b, s, h, kv, d, causal=True)
+    lengths = np.array([200, 150], np.uint32)
+    q = np.zeros((b, s, h, d), np.float16)
+    q[:, :, 0::2, 63] = 4.0   # heads 0 and 2: towards the late keys
+    q[:, :, 1::2, 63] = -4.0  # heads 1 and 3: away from them
+    k = rng.normal(size=(b, s, kv, d)).astype(np.float16)
+    late = slice(0, 16) if aligned_first else slice(40, 56)
+    k[:, late] = 0
+    k[:, late, :, 63] = 3.0
+    v = rng.normal(size=(b, s, kv, d)).astype(np.float16)
+    one = np.full(d, 0x3F80, np.uint16)  # bf16 1.0
+    t = {"q": q, "k": k, "v": v, "q_norm": one, "k_norm": one}
+    out, _ = norm_rope_attend(runtime, t, lengths, shape, "f32")
+    _, expected = oracle_norm_rope(t, lengths)
+    err = np.max(np.abs(out.astype(np.float64) - expected))
+    assert err <= FUSED_F32_MAX, err
+
+
 @pytest.mark.parametrize("route", ["fused", "plain"])
 def test_f16_routes_are_deterministic(runtime, route):
     """The same launch on the same inputs gives the same bits. Full tiles skip the causal masking,
