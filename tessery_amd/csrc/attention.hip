@@ -1102,35 +1102,36 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
         pl = __builtin_shufflevector(l0, l1, 0, 1, 2, 3);
         l_run += (pf[0] + pf[1]) + (pf[2] + pf[3]);
       } else {
-      const float mloc = rowmax4(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]))) * scale_log2;
-      // lazy running max: moved only when a tile exceeds it by more than kMaxSlack
-      const bool grow = mloc > m_run + kMaxSlack;
-      // every row sees key 0 in its first tile (L >= 1), so m_new is finite from tile 0 on
-      const float m_new = grow ? mloc : m_run;
-      // what is accumulated is rescaled only when the max moved in some lane (factor exactly 1
-      // in the others)
-      if (__any(grow)) rescale(m_run - m_new);
-      if constexpr (FUSED) {
-        // P as hi + lo fp16 pair: the PV product sees P to ~22 bits, and the row sum is the
-        // fp32 sum of the same values
-        float pf[4];
+        const float mloc = rowmax4(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]))) * scale_log2;
+        // lazy running max: moved only when a tile exceeds it by more than kMaxSlack
+        const bool grow = mloc > m_run + kMaxSlack;
+        // every row sees key 0 in its first tile (L >= 1), so m_new is finite from tile 0 on
+        const float m_new = grow ? mloc : m_run;
+        // what is accumulated is rescaled only when the max moved in some lane (factor exactly 1
+        // in the others)
+        if (__any(grow)) rescale(m_run - m_new);
+        if constexpr (FUSED) {
+          // P as hi + lo fp16 pair: the PV product sees P to ~22 bits, and the row sum is the
+          // fp32 sum of the same values
+          float pf[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) pf[j] = __builtin_amdgcn_exp2f(fmaf(sc[j], scale_log2, -m_new));
-        half2v h0, h1, l0, l1;
-        split2(pf[0], pf[1], one, h0, l0);
-        split2(pf[2], pf[3], one, h1, l1);
-        pb = __builtin_shufflevector(h0, h1, 0, 1, 2, 3);
-        pl = __builtin_shufflevector(l0, l1, 0, 1, 2, 3);
-        l_run += (pf[0] + pf[1]) + (pf[2] + pf[3]);
-      } else {
+          for (int j = 0; j < 4; ++j)
+            pf[j] = __builtin_amdgcn_exp2f(fmaf(sc[j], scale_log2, -m_new));
+          half2v h0, h1, l0, l1;
+          split2(pf[0], pf[1], one, h0, l0);
+          split2(pf[2], pf[3], one, h1, l1);
+          pb = __builtin_shufflevector(h0, h1, 0, 1, 2, 3);
+          pl = __builtin_shufflevector(l0, l1, 0, 1, 2, 3);
+          l_run += (pf[0] + pf[1]) + (pf[2] + pf[3]);
+        } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          pb[j] = static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(sc[j], scale_log2, -m_new)));
-        // the row sum of the ROUNDED probabilities (the ones the PV product uses), accumulated
-        // exactly with fp16 dot products
-        l_run = dot_ones(pb, l_run);
-      }
-      m_run = m_new;
+          for (int j = 0; j < 4; ++j)
+            pb[j] = static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(sc[j], scale_log2, -m_new)));
+          // the row sum of the ROUNDED probabilities (the ones the PV product uses), accumulated
+          // exactly with fp16 dot products
+          l_run = dot_ones(pb, l_run);
+        }
+        m_run = m_new;
       }
       // l_run holds this lane's share of the row sum (its own keys); the four shares of a query
       // are combined once, after the last tile
