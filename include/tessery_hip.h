@@ -80,6 +80,10 @@ int mi_plan_run(void *runtime, void *plan, void **buffers, uint32_t count);
 /* No counterpart in the reference: the number of graph launches and graph instantiations of plan
  * replays since mi_create (diagnostics). */
 int mi_graph_counts(void *runtime, uint64_t *launches, uint64_t *builds);
+/* No counterpart in the reference: the number of queued-launch pairs and gated-MLP triples
+ * (linear4 gate, linear4 up, silu_gate) that ran as one kernel with the same bits, since
+ * mi_create (diagnostics). */
+int mi_fusion_counts(void *runtime, uint64_t *pairs, uint64_t *gated);
 
 /* No counterpart in the reference (unified memory made it unnecessary there): copy `bytes`
  * host bytes into an existing device buffer, synchronously. */

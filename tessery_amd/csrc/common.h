@@ -32,6 +32,9 @@ __device__ __forceinline__ float bf16_to_float(uint16_t w) {
   return __uint_as_float(static_cast<uint32_t>(w) << 16);
 }
 
+// silu(g) * u as tessery's silu_gate computes it (kernels.metal:334-337)
+__device__ __forceinline__ float silu_times(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
 // x0 * sc and x1 * sc rounded to fp16 and packed (hi), and the fp16 of what hi leaves of each
 // (lo = fp16(x * sc - hi), the product exact inside the fma): four v_fma_mix instructions. The
 // lo/hi forms write one half of the destination and keep the other, so each packed pair is built

@@ -20,9 +20,6 @@
 
 namespace tessery {
 
-// silu(g) * u as tessery's silu_gate computes it (kernels.metal:334-337)
-__device__ __forceinline__ float silu_times(float g, float u) { return g / (1.0f + expf(-g)) * u; }
-
 // The 32 dequantized weights of lane (column n, k-slot h) for group gi: w = code * scale + bias in
 // fp32, codes 32h .. 32h + 31 of the group (zero for columns past the end).
 __device__ __forceinline__ void decode_group(const uint32_t* __restrict__ w,

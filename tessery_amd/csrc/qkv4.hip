@@ -376,17 +376,29 @@ constexpr int kHiloChunk = 16;
 // arrive in LDS once, up front, transposed to [group][column]; fp32 x is prefetched two groups
 // ahead in two register sets.
 // 64-row tiles keep two workgroups on every CU down to 8 column tiles x 4096 rows.
+//
+// DUAL (the gated MLP's gate and up projections of one x): the tile runs both weight sets over the
+// same staged x and row sums, each with its own weight ring, scale / bias words, fold and bias
+// term in the same order as a single launch, and stores up to y2 and silu(gate) * up to y: the
+// values linear4 + linear4 + silu_gate leave in their two outputs.
+template <bool DUAL>
 __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__ x,
                                                       const float* __restrict__ rs,
                                                       const uint32_t* __restrict__ w,
                                                       const uint16_t* __restrict__ sc,
                                                       const uint16_t* __restrict__ bi,
-                                                      float* __restrict__ y, int M, int N, int K) {
+                                                      float* __restrict__ y,
+                                                      const uint32_t* __restrict__ w2,
+                                                      const uint16_t* __restrict__ sc2,
+                                                      const uint16_t* __restrict__ bi2,
+                                                      float* __restrict__ y2, int M, int N, int K) {
   constexpr int TM = 64;
+  constexpr int NW = DUAL ? 2 : 1;  // weight sets
   __shared__ __attribute__((aligned(1024))) _Float16 xs[2][2][TM * 64];  // [stage][hi, lo]
-  __shared__ __attribute__((aligned(1024))) uint32_t ws[3][128 * 8];      // qkv4_f16 layout
+  __shared__ __attribute__((aligned(1024))) uint32_t ws[NW][3][128 * 8];  // qkv4_f16 layout
   __shared__ __attribute__((aligned(16))) float xg_lds[kHiloChunk][TM];
-  // scale and bias words of the tile's 128 columns, all groups: [2][groups][128] (dynamic size)
+  // scale and bias words of the tile's 128 columns, all groups, per weight set:
+  // [set][2][groups][128] (dynamic size)
   extern __shared__ __attribute__((aligned(1024))) uint16_t sbuf[];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
@@ -400,6 +412,7 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
   // ---- scales and biases of the tile's columns, all groups, transposed into LDS once (before
   // any of this kernel's asm loads: the memory-wait counts below assume none older) ----
   copy_scales_transposed(sbuf, sc, bi, tile, groups);
+  if constexpr (DUAL) copy_scales_transposed(sbuf + 2 * 128 * groups, sc2, bi2, tile, groups);
   wait_lgkmcnt<0>();  // published by the first group's barrier
 
   // ---- staging role: row srow of the tile, floats 16 * spart .. +15 of each group ----
@@ -450,50 +463,67 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
       (static_cast<uint32_t>(tile * 128 + 32 * wave + l32) * static_cast<uint32_t>(K / 8) +
        4u * static_cast<uint32_t>(hh)) * 4u;
   auto issue_w = [&](int st, int g) {
-    dma16_at(w + 8 * g, woff, reinterpret_cast<_Float16*>(&ws[st][256 * wave]));
+    dma16_at(w + 8 * g, woff, reinterpret_cast<_Float16*>(&ws[0][st][256 * wave]));
+    if constexpr (DUAL)
+      dma16_at(w2 + 8 * g, woff, reinterpret_cast<_Float16*>(&ws[NW - 1][st][256 * wave]));
   };
 
-  floatx16 acc[2];
+  floatx16 acc[NW][2];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int set = 0; set < NW; ++set)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc[j][e] = 0.0f;
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[set][j][e] = 0.0f;
 
   // acc[j] += sum_{g in [g0, g0 + count)} bias[n][g] X_g[m] (v_mfma_f32_32x32x2_f32: k-slot
   // kk = l / 32 of lane l is group g0 + 2 q + kk); operands first, then the MFMAs
   auto flush_bias = [&](int g0, int count) {
-    float av[kHiloChunk / 2], bw[kHiloChunk / 2][2];
+    float av[kHiloChunk / 2];
 #pragma unroll
     for (int q2 = 0; q2 < kHiloChunk / 2; ++q2) {
       const int q = 2 * q2 + hh;
       const bool live = q < count;
       const int qc = live ? q : 0;
       av[q2] = live ? xg_lds[(g0 + qc) % kHiloChunk][wrow + l32] : 0.0f;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int col = wn * 64 + 32 * j + l32;
-        bw[q2][j] = live ? bf16_to_float(sbuf[128 * groups + (g0 + qc) * 128 + col]) : 0.0f;
-      }
     }
 #pragma unroll
-    for (int q2 = 0; q2 < kHiloChunk / 2; ++q2) {
-      if (2 * q2 >= count) break;  // wavefront-uniform
+    for (int set = 0; set < NW; ++set) {
+      float bw[kHiloChunk / 2][2];
+      const uint16_t* sb = sbuf + set * 2 * 128 * groups;
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q2], bw[q2][j], acc[j], 0, 0, 0);
+      for (int q2 = 0; q2 < kHiloChunk / 2; ++q2) {
+        const int q = 2 * q2 + hh;
+        const bool live = q < count;
+        const int qc = live ? q : 0;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int col = wn * 64 + 32 * j + l32;
+          bw[q2][j] = live ? bf16_to_float(sb[128 * groups + (g0 + qc) * 128 + col]) : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int q2 = 0; q2 < kHiloChunk / 2; ++q2) {
+        if (2 * q2 >= count) break;  // wavefront-uniform
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[set][j] =
+              __builtin_amdgcn_mfma_f32_32x32x2f32(av[q2], bw[q2][j], acc[set][j], 0, 0, 0);
+      }
     }
   };
 
   // Memory instructions in issue order (the memory counter retires in order; the scale / bias
-  // loads above have completed): x of group 0; then x of group k + 1 right before the weights of group k, for every
-  // k. The prologue issues x(1), w(0), stages group 0, then x(2), w(1); step g issues x(g + 3),
-  // w(g + 2) (both clamped to the last group). So at the start of step g the weights of group g
-  // have exactly 5 younger memory instructions (x(g + 2), w(g + 1)), and x(g + 1), issued before
-  // w(g), is complete too.
+  // loads above have completed): x of group 0; then x of group k + 1 right before the weights of
+  // group k (NW DMAs), for every k. The prologue issues x(1), w(0), stages group 0, then x(2),
+  // w(1); step g issues x(g + 3), w(g + 2) (both clamped to the last group). So at the start of
+  // step g the weights of group g have exactly 4 + NW younger memory instructions (x(g + 2),
+  // w(g + 1)), and x(g + 1), issued before w(g), is complete too.
+  constexpr int YOUNGER = 4 + NW;
   load_x(0, 0);
   load_x(min(1, groups - 1), 1);
   issue_w(0, 0);
-  wait_vmcnt_pin<5>(xr[0]);  // x(0): x(1) and w(0) are younger
+  wait_vmcnt_pin<YOUNGER>(xr[0]);  // x(0): x(1) and w(0) are younger
   float xsum = stage_x(0, 0);
   load_x(min(2, groups - 1), 0);
   issue_w(1, min(1, groups - 1));
@@ -503,7 +533,7 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
   // has no other branch, which keeps the compiler's memory waits exact).
   auto step = [&](int g, int st, auto parity) {
     constexpr int par = decltype(parity)::value;
-    wait_vmcnt_pin<5>(xr[par ^ 1]);  // this group's weight words and the x of group g + 1
+    wait_vmcnt_pin<YOUNGER>(xr[par ^ 1]);  // this group's weight words and the x of group g + 1
     __syncthreads();  // weights of group g and x of group g visible; group g - 1's stages free
     if (g % kHiloChunk == 0 && g > 0) {
       flush_bias(g - kHiloChunk, kHiloChunk);
@@ -514,38 +544,44 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
     rsum += __shfl_xor(rsum, 2);
     if (spart == 0) xg_lds[g % kHiloChunk][srow] = rsum;
 
-    uint4v wd[2];
-    float gs[2];
+    uint4v wd[NW][2];
+    float gs[NW][2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = wn * 64 + 32 * j + l32;
-      wd[j] = *reinterpret_cast<const uint4v*>(&ws[st][256 * (2 * wn + j) + 128 * hh + 4 * l32]);
-      gs[j] = bf16_to_float(sbuf[g * 128 + col]);
-    }
+    for (int set = 0; set < NW; ++set)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int col = wn * 64 + 32 * j + l32;
+        wd[set][j] = *reinterpret_cast<const uint4v*>(
+            &ws[set][st][256 * (2 * wn + j) + 128 * hh + 4 * l32]);
+        gs[set][j] = bf16_to_float(sbuf[set * 2 * 128 * groups + g * 128 + col]);
+      }
     // stage group g + 1 from its register set, refill that set with group g + 3, then the
     // weights of group g + 2 into the ring stage group g - 1 used
     xsum = stage_x(par ^ 1, par ^ 1);
     load_x(min(g + 3, groups - 1), par ^ 1);
     issue_w(st == 0 ? 2 : st - 1, min(g + 2, groups - 1));
 
-    floatx16 p[2];
 #pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-      const int row = wrow + l32;
-      const int off = row * 64 + 8 * ((4 * hh + s4) ^ xsw(row));
-      const half8 ah = *reinterpret_cast<const half8*>(&xs[par][0][off]);
-      const half8 al = *reinterpret_cast<const half8*>(&xs[par][1][off]);
+    for (int set = 0; set < NW; ++set) {
+      floatx16 p[2];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const half8 bq = decode_codes_evenodd(wd[j][s4]);
-        p[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bq, s4 ? p[j] : floatx16{}, 0, 0, 0);
-        p[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bq, p[j], 0, 0, 0);
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const int row = wrow + l32;
+        const int off = row * 64 + 8 * ((4 * hh + s4) ^ xsw(row));
+        const half8 ah = *reinterpret_cast<const half8*>(&xs[par][0][off]);
+        const half8 al = *reinterpret_cast<const half8*>(&xs[par][1][off]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const half8 bq = decode_codes_evenodd(wd[set][j][s4]);
+          p[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bq, s4 ? p[j] : floatx16{}, 0, 0, 0);
+          p[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bq, p[j], 0, 0, 0);
+        }
       }
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[set][j][e] = fmaf(gs[set][j], p[j][e], acc[set][j][e]);
     }
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[j][e] = fmaf(gs[j], p[j][e], acc[j][e]);
   };
   int st = 0;  // g % 3
   int g = 0;
@@ -573,7 +609,16 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
       // 1 / rs[m], exact: rs[m] = 2^e_m with |e_m| <= 126, frexp gives e_m + 1
       const float inv = __builtin_amdgcn_ldexpf(1.0f, 1 - __builtin_amdgcn_frexp_expf(rs[m]));
 #pragma unroll
-      for (int j = 0; j < 2; ++j) y[static_cast<size_t>(m) * N + nw + 32 * j + l32] = acc[j][e] * inv;
+      for (int j = 0; j < 2; ++j) {
+        const size_t at = static_cast<size_t>(m) * N + nw + 32 * j + l32;
+        if constexpr (DUAL) {
+          const float gate = acc[0][j][e] * inv, up = acc[1][j][e] * inv;
+          y2[at] = up;
+          y[at] = silu_times(gate, up);
+        } else {
+          y[at] = acc[0][j][e] * inv;
+        }
+      }
     }
   }
 }
@@ -584,17 +629,46 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
 // 48 KiB of x / weight stages and row sums two workgroups fit a CU up to K = 4096)
 static size_t hilo_sb_bytes(int K) { return static_cast<size_t>(2 * 128 * 2) * (K / 64); }
 
+static bool hilo_fits(int M, int N, int K, const float* x, const float* scratch,
+                      size_t scratch_floats) {
+  return K > 0 && K % 64 == 0 && N > 0 && N % 128 == 0 && scratch &&
+         static_cast<uint64_t>(M) * static_cast<uint64_t>(K) * 4 < (1ull << 32) &&
+         static_cast<size_t>(M) <= scratch_floats && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+}
+
 hipError_t launch_linear4_hilo_f32(const float* x, const uint32_t* w, const uint16_t* scales,
                                    const uint16_t* biases, float* y, int M, int N, int K,
                                    float* scratch, size_t scratch_floats, hipStream_t st) {
   if (M <= 0) return hipSuccess;
-  if (K <= 0 || K % 64 || hilo_sb_bytes(K) > 64 * 1024 || N <= 0 || N % 128 || !scratch ||
-      static_cast<uint64_t>(M) * static_cast<uint64_t>(K) * 4 >= (1ull << 32) ||
-      static_cast<size_t>(M) > scratch_floats || (reinterpret_cast<uintptr_t>(x) & 15))
+  if (!hilo_fits(M, N, K, x, scratch, scratch_floats) || hilo_sb_bytes(K) > 64 * 1024)
     return hipErrorInvalidValue;
   row_scales_f32<<<(M + 3) / 4, 256, 0, st>>>(x, M, K, scratch);
   dim3 grid((M + 63) / 64, N / 128);
-  linear4_hilo<<<grid, 256, hilo_sb_bytes(K), st>>>(x, scratch, w, scales, biases, y, M, N, K);
+  linear4_hilo<false><<<grid, 256, hilo_sb_bytes(K), st>>>(x, scratch, w, scales, biases, y,
+                                                          nullptr, nullptr, nullptr, nullptr, M,
+                                                          N, K);
+  return hipGetLastError();
+}
+
+bool linear4_hilo_dual_fits(int M, int N, int K) {
+  // both sets' scale / bias words next to the 60 KiB of stages, rings and row sums: two
+  // workgroups per CU
+  return M >= kLinear4HiloRows && K > 0 && K % 64 == 0 && N > 0 && N % 128 == 0 &&
+         2 * hilo_sb_bytes(K) <= 20 * 1024;
+}
+
+hipError_t launch_linear4_hilo_dual_f32(const float* x, const uint32_t* w, const uint16_t* scales,
+                                        const uint16_t* biases, float* y, const uint32_t* uw,
+                                        const uint16_t* uscales, const uint16_t* ubiases, float* u,
+                                        int M, int N, int K, float* scratch,
+                                        size_t scratch_floats, hipStream_t st) {
+  if (M <= 0) return hipSuccess;
+  if (!linear4_hilo_dual_fits(M, N, K) || !hilo_fits(M, N, K, x, scratch, scratch_floats))
+    return hipErrorInvalidValue;
+  row_scales_f32<<<(M + 3) / 4, 256, 0, st>>>(x, M, K, scratch);
+  dim3 grid((M + 63) / 64, N / 128);
+  linear4_hilo<true><<<grid, 256, 2 * hilo_sb_bytes(K), st>>>(x, scratch, w, scales, biases, y,
+                                                             uw, uscales, ubiases, u, M, N, K);
   return hipGetLastError();
 }
 

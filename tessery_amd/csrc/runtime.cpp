@@ -155,6 +155,7 @@ struct Runtime {
   int device = 0;
   bool graphs = true;  // replay plans through cached HIP graphs (TESSERY_HIP_GRAPHS=0 disables)
   uint64_t graph_launches = 0, graph_builds = 0;
+  uint64_t fused_pairs = 0, fused_gated = 0;  // launch-time fusions (diagnostics)
   float* dense_scratch = nullptr;  // split-K partial sums of small-batch projections
   std::vector<Segment> segments;
   hipStream_t stream = nullptr;
@@ -966,12 +967,62 @@ hipError_t launch_fused_pair(Runtime* rt, const Op& a, const Op& b) {
   return hipErrorNotReady;
 }
 
-// Launches ops [first, last) in order, pairing what launch_fused_pair can run as one kernel.
+bool is_linear4(Route r) {
+  return r == R_LINEAR4 || r == R_LINEAR4_TILED || r == R_LINEAR4_TAIL || r == R_LINEAR4_16X32 ||
+         r == R_LINEAR4_32X32 || r == R_LINEAR4_SMALL3;
+}
+
+// The gated MLP as the reference's unfused form queues it (metal.py:501-530): linear4(x -> g),
+// linear4(x -> u) over the same rows, then silu_gate(g, u). When both projections cover all rows
+// of their outputs and would run the fp16-MFMA kernel, one launch computes both from one staging
+// of x and leaves the same bits in g and u. Returns the launch status, or hipErrorNotReady when
+// ops[i .. i + 2] are not such a triple.
+hipError_t launch_fused_gated(Runtime* rt, const Op& a, const Op& b, const Op& c) {
+  if (!is_linear4(a.route) || b.route != a.route || c.route != R_SILU_GATE) return hipErrorNotReady;
+  const Params &pa = a.p, &pb = b.p;
+  if (pa.rows != pb.rows || pa.cols != pb.cols || pa.k != pb.k || a.ptr[0] != b.ptr[0])
+    return hipErrorNotReady;
+  // outputs distinct from x and from each other: the second projection reads the same x
+  if (a.ptr[4] == a.ptr[0] || b.ptr[4] == a.ptr[0] || a.ptr[4] == b.ptr[4]) return hipErrorNotReady;
+  if (c.ptr[0] != a.ptr[4] || c.ptr[1] != b.ptr[4] ||
+      static_cast<uint64_t>(c.p.n) != static_cast<uint64_t>(pa.rows) * pa.cols)
+    return hipErrorNotReady;
+  RowRange ra, rb;
+  if (!linear4_range(a.route, pa, a.threads, a.group, &ra) ||
+      !linear4_range(b.route, pb, b.threads, b.group, &rb) || ra.r0 != 0 || ra.r1 != pa.rows ||
+      rb.r0 != 0 || rb.r1 != pb.rows)
+    return hipErrorNotReady;
+  const int M = static_cast<int>(pa.rows), N = static_cast<int>(pa.cols),
+            K = static_cast<int>(pa.k);
+  if (!rt->dense_scratch || !tessery::linear4_hilo_dual_fits(M, N, K)) return hipErrorNotReady;
+  const hipError_t e = tessery::launch_linear4_hilo_dual_f32(
+      static_cast<const float*>(a.ptr[0]), static_cast<const uint32_t*>(a.ptr[1]),
+      static_cast<const uint16_t*>(a.ptr[2]), static_cast<const uint16_t*>(a.ptr[3]),
+      static_cast<float*>(a.ptr[4]), static_cast<const uint32_t*>(b.ptr[1]),
+      static_cast<const uint16_t*>(b.ptr[2]), static_cast<const uint16_t*>(b.ptr[3]),
+      static_cast<float*>(b.ptr[4]), M, N, K, rt->dense_scratch, kDenseScratchFloats,
+      rt->stream);
+  // hipErrorInvalidValue: nothing was launched (alignment or sizes); the three ops run as queued
+  return e == hipErrorInvalidValue ? hipErrorNotReady : e;
+}
+
+// Launches ops [first, last) in order, running as one kernel the triples launch_fused_gated takes
+// and the pairs launch_fused_pair takes.
 hipError_t launch_range(Runtime* rt, size_t first, size_t last) {
   for (size_t i = first; i < last; ++i) {
+    const hipError_t gated =
+        i + 2 < last ? launch_fused_gated(rt, rt->ops[i], rt->ops[i + 1], rt->ops[i + 2])
+                     : hipErrorNotReady;
+    if (gated == hipSuccess) {
+      ++rt->fused_gated;
+      i += 2;
+      continue;
+    }
+    if (gated != hipErrorNotReady) return gated;
     const hipError_t fused =
         i + 1 < last ? launch_fused_pair(rt, rt->ops[i], rt->ops[i + 1]) : hipErrorNotReady;
     if (fused == hipSuccess) {
+      ++rt->fused_pairs;
       ++i;
       continue;
     }
@@ -1058,15 +1109,27 @@ int mi_finish(void* runtime) {
   }
   for (size_t i = 0; rt->profiling && i < n && !failed; ++i) {
     if (rt->profiling && hipEventRecord(rt->prof_events[2 * i], rt->stream) != hipSuccess) failed = 1;
-    // a fused pair runs inside the first op's events; the second op's events enclose no work
+    // a fused triple or pair runs inside the first op's events; the others' events enclose no
+    // work
+    const hipError_t gated =
+        failed || i + 2 >= n ? hipErrorNotReady
+                             : launch_fused_gated(rt, rt->ops[i], rt->ops[i + 1], rt->ops[i + 2]);
+    if (!failed && gated != hipErrorNotReady && gated != hipSuccess) failed = 1;
     const hipError_t fused =
-        failed || i + 1 >= n ? hipErrorNotReady : launch_fused_pair(rt, rt->ops[i], rt->ops[i + 1]);
+        failed || gated == hipSuccess || i + 1 >= n
+            ? hipErrorNotReady
+            : launch_fused_pair(rt, rt->ops[i], rt->ops[i + 1]);
     if (!failed && fused != hipErrorNotReady && fused != hipSuccess) failed = 1;
-    if (!failed && fused == hipErrorNotReady && launch(rt, rt->ops[i]) != hipSuccess) failed = 1;
+    if (!failed && gated == hipErrorNotReady && fused == hipErrorNotReady &&
+        launch(rt, rt->ops[i]) != hipSuccess)
+      failed = 1;
     if (!failed && rt->profiling &&
         hipEventRecord(rt->prof_events[2 * i + 1], rt->stream) != hipSuccess)
       failed = 1;
-    if (!failed && fused == hipSuccess) {
+    const size_t extra = !failed && gated == hipSuccess ? 2 : (!failed && fused == hipSuccess ? 1 : 0);
+    rt->fused_gated += extra == 2;
+    rt->fused_pairs += extra == 1;
+    for (size_t e = 0; e < extra && !failed; ++e) {
       ++i;
       if (rt->profiling && (hipEventRecord(rt->prof_events[2 * i], rt->stream) != hipSuccess ||
                             hipEventRecord(rt->prof_events[2 * i + 1], rt->stream) != hipSuccess))
@@ -1183,6 +1246,14 @@ int mi_graph_counts(void* runtime, uint64_t* launches, uint64_t* builds) {
   if (!rt || !launches || !builds) return 1;
   *launches = rt->graph_launches;
   *builds = rt->graph_builds;
+  return 0;
+}
+
+int mi_fusion_counts(void* runtime, uint64_t* pairs, uint64_t* gated) {
+  auto rt = static_cast<Runtime*>(runtime);
+  if (!rt || !pairs || !gated) return 1;
+  *pairs = rt->fused_pairs;
+  *gated = rt->fused_gated;
   return 0;
 }
 

@@ -113,6 +113,53 @@ def test_gated4_other_shapes_match_oracle(runtime, rows, cols, k):
             b.close()
 
 
+@pytest.mark.parametrize("rows,cols,k,fused", [(1024, 3072, 1024, True), (1040, 384, 512, True),
+                                               (1029, 384, 512, False)])
+def test_gated_mlp_on_fp16_mfma_runs_as_one_kernel_with_the_same_bits(runtime, rows, cols, k,
+                                                                       fused):
+    """From 1024 rows the projections run on fp16 MFMA (row-scaled hi + lo halves of x). When the
+    reference's unfused gated form (linear4 gate, linear4 up, silu_gate) is queued with each
+    projection in one launch over all rows, the runtime runs the three as one kernel that stages x
+    once for both weight sets; it leaves the same bits in both outputs as the three launches in
+    separate commands. At 1029 rows each projection is several launches and nothing is fused."""
+    rng = np.random.default_rng(rows + cols + k)
+    x = rng.normal(size=(rows, k)).astype(np.float32)
+    sets = [(ref.pack(rng.integers(0, 16, size=(cols, k), dtype=np.uint32)),
+             bf16_words(rng.uniform(0.01, 0.2, size=(cols, k // 64))),
+             bf16_words(rng.uniform(-1, 0.1, size=(cols, k // 64)))) for _ in range(2)]
+    buffers = [runtime.upload(a) for a in [x, *sets[0], *sets[1]]]
+    buffers += [runtime.buffer(rows * cols * 4) for _ in range(4)]
+    try:
+        before = runtime.diagnostics()["fused_gated"]
+        with runtime.command():
+            runtime._gated4(buffers[:9], rows=rows, cols=cols, k=k)
+        assert runtime.diagnostics()["fused_gated"] == before + int(fused)
+        g2, u2 = buffers[9], buffers[10]
+        with runtime.command():
+            runtime._linear4([*buffers[:4], g2], rows=rows, cols=cols, k=k)
+        with runtime.command():
+            runtime._linear4([buffers[0], *buffers[4:7], u2], rows=rows, cols=cols, k=k)
+        with runtime.command():
+            runtime._dispatch("silu_gate", [g2, u2], threads=rows * cols, n=rows * cols)
+        assert runtime.diagnostics()["fused_gated"] == before + int(fused)
+        got_g, got_u = (runtime.read(b, (rows, cols)) for b in buffers[7:9])
+        np.testing.assert_array_equal(got_g, runtime.read(g2, (rows, cols)))
+        np.testing.assert_array_equal(got_u, runtime.read(u2, (rows, cols)))
+        # against float64: each projection within 2e-6 of sum_k |x| |w| of its element (the fp16
+        # MFMA path's bound), carried through silu(g) * u (|silu'| < 1.1)
+        xd = x.astype(np.float64)
+        wg, wu = (ref.dequantize(*w, k) for w in sets)
+        gate, up = xd @ wg.T, xd @ wu.T
+        bg, bu = 2e-6 * (np.abs(xd) @ np.abs(wg).T), 2e-6 * (np.abs(xd) @ np.abs(wu).T)
+        assert np.all(np.abs(got_u - up) <= bu)
+        silu = gate / (1.0 + np.exp(-gate))
+        bound = 1.1 * bg * (np.abs(up) + bu) + np.abs(silu) * bu + 1e-30
+        assert np.all(np.abs(got_g - silu * up) <= bound), float((np.abs(got_g - silu * up) / bound).max())
+    finally:
+        for b in buffers:
+            b.close()
+
+
 def layer_tail_weights(rng, hidden, attn_width, inter):
     def weight_set(n, k, scale):
         return (ref.pack(rng.integers(0, 16, size=(n, k), dtype=np.uint32)),
