@@ -35,6 +35,49 @@ __device__ __forceinline__ float bf16_to_float(uint16_t w) {
 // silu(g) * u as tessery's silu_gate computes it (kernels.metal:334-337)
 __device__ __forceinline__ float silu_times(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
+// RMSNorm over a D-channel fp16 row, then split-half RoPE (kernels.metal:53-74), for one of the
+// T = D / 16 consecutive lanes that hold the row: lane j owns channels 8j..8j+7 (lo) and their
+// RoPE partners D/2 + 8j..+7 (hi), so the rotation never leaves the lane; the sum of squares
+// reduces over the T lanes (all active). cs / sn point at the lane's eight cos / sin entries of
+// the row's position, gw_lo / gw_hi hold the bf16 gamma words of its channels. fp32 math; out
+// receives the rotated values rounded to fp16 (first: channels 8j.., second: D/2 + 8j..) and
+// out_lo what that rounding left (hi + lo carry the fp32 value to ~22 bits).
+template <int D>
+__device__ __forceinline__ void norm_rope_piece(const half8& lo, const half8& hi, const uint4v& gw_lo,
+                                                const uint4v& gw_hi, const float* cs,
+                                                const float* sn, float eps, half8& first,
+                                                half8& second, half8& first_lo, half8& second_lo) {
+  constexpr int T = D / 16;
+  const floatx4 c0 = *reinterpret_cast<const floatx4*>(cs);
+  const floatx4 c1 = *reinterpret_cast<const floatx4*>(cs + 4);
+  const floatx4 s0 = *reinterpret_cast<const floatx4*>(sn);
+  const floatx4 s1 = *reinterpret_cast<const floatx4*>(sn + 4);
+  float a[8], c[8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    a[m] = static_cast<float>(lo[m]);
+    c[m] = static_cast<float>(hi[m]);
+    ss += a[m] * a[m] + c[m] * c[m];
+  }
+#pragma unroll
+  for (int off = T / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const int sh = 16 * (m & 1);
+    const float wl = bf16_to_float(static_cast<uint16_t>((gw_lo[m >> 1] >> sh) & 0xffffu));
+    const float wh = bf16_to_float(static_cast<uint16_t>((gw_hi[m >> 1] >> sh) & 0xffffu));
+    const float p = a[m] * inv * wl, q = c[m] * inv * wh;
+    const float cv = m < 4 ? c0[m] : c1[m - 4], sv = m < 4 ? s0[m] : s1[m - 4];
+    const float r0 = p * cv - q * sv, r1 = p * sv + q * cv;
+    first[m] = static_cast<_Float16>(r0);
+    second[m] = static_cast<_Float16>(r1);
+    first_lo[m] = static_cast<_Float16>(r0 - static_cast<float>(first[m]));
+    second_lo[m] = static_cast<_Float16>(r1 - static_cast<float>(second[m]));
+  }
+}
+
 // x0 * sc and x1 * sc rounded to fp16 and packed (hi), and the fp16 of what hi leaves of each
 // (lo = fp16(x * sc - hi), the product exact inside the fma): four v_fma_mix instructions. The
 // lo/hi forms write one half of the destination and keep the other, so each packed pair is built

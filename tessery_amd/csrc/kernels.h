@@ -135,6 +135,17 @@ struct Qkv4Args {
   int n[3];
   int M, K;
   int scale_bf16;
+  // Optional k prologue (kn != null): the k tiles also write norm_rope_f16<128>'s output over
+  // y[1] read as [M / kn_S, kn_S, n[1] / 128, 128] (rows past their batch row's length skipped),
+  // the hi plane to kn and, with kn_split, the lo plane to kn + M * n[1], with the same bits.
+  _Float16* kn;
+  int kn_split;
+  const uint16_t* kn_gamma;
+  const float* kn_cos;
+  const float* kn_sin;
+  const uint32_t* kn_lengths;
+  int kn_S;
+  float kn_eps;
 };
 bool qkv4_f16_fits(int M, int K, const int n[3]);
 hipError_t launch_qkv4_f16(const Qkv4Args& a, hipStream_t st);

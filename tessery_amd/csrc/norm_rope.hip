@@ -178,38 +178,11 @@ __global__ __launch_bounds__(256) void norm_rope_f16(const _Float16* __restrict_
     const size_t base = ((static_cast<size_t>(b) * S + pos) * heads + head) * D;
     const half8 lo = *reinterpret_cast<const half8*>(x + base + 8 * j);
     const half8 hi = *reinterpret_cast<const half8*>(x + base + HALF + 8 * j);
-    const float* cs = cos_tab + static_cast<size_t>(pos) * HALF + 8 * j;
-    const float* sn = sin_tab + static_cast<size_t>(pos) * HALF + 8 * j;
-    const floatx4 c0 = *reinterpret_cast<const floatx4*>(cs);
-    const floatx4 c1 = *reinterpret_cast<const floatx4*>(cs + 4);
-    const floatx4 s0 = *reinterpret_cast<const floatx4*>(sn);
-    const floatx4 s1 = *reinterpret_cast<const floatx4*>(sn + 4);
-    float a[8], c[8];
-    float ss = 0.0f;
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      a[m] = static_cast<float>(lo[m]);
-      c[m] = static_cast<float>(hi[m]);
-      ss += a[m] * a[m] + c[m] * c[m];
-    }
     // the T lanes of a row are consecutive threads of one wavefront (T divides 64)
-#pragma unroll
-    for (int off = T / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-    const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
     half8 first, second, first_lo, second_lo;
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      const int sh = 16 * (m & 1);
-      const float wl = bf16_to_float(static_cast<uint16_t>((glo[m >> 1] >> sh) & 0xffffu));
-      const float wh = bf16_to_float(static_cast<uint16_t>((ghi[m >> 1] >> sh) & 0xffffu));
-      const float p = a[m] * inv * wl, q = c[m] * inv * wh;
-      const float cv = m < 4 ? c0[m] : c1[m - 4], sv = m < 4 ? s0[m] : s1[m - 4];
-      const float r0 = p * cv - q * sv, r1 = p * sv + q * cv;
-      first[m] = static_cast<_Float16>(r0);
-      second[m] = static_cast<_Float16>(r1);
-      first_lo[m] = static_cast<_Float16>(r0 - static_cast<float>(first[m]));
-      second_lo[m] = static_cast<_Float16>(r1 - static_cast<float>(second[m]));
-    }
+    norm_rope_piece<D>(lo, hi, glo, ghi, cos_tab + static_cast<size_t>(pos) * HALF + 8 * j,
+                       sin_tab + static_cast<size_t>(pos) * HALF + 8 * j, eps, first, second,
+                       first_lo, second_lo);
     *reinterpret_cast<half8*>(y + base + 8 * j) = first;
     *reinterpret_cast<half8*>(y + base + HALF + 8 * j) = second;
     if (y_lo) {

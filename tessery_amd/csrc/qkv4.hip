@@ -322,6 +322,49 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
       const int m = m0 + 32 * rtile(k) + 8 * (e >> 2) + 4 * hh + (e & 3);
       if (m < M) y[static_cast<size_t>(m) * N + n] = static_cast<_Float16>(acc[k][e]);
     }
+
+  // ---- k prologue of the attention (k tiles, when asked): the tile is one head of 128
+  // channels. Its fp16 values go row-major into the x stages (free since the last group: the
+  // barrier before flush_bias), then norm_rope_piece runs in norm_rope_f16's lane layout (eight
+  // consecutive lanes per row, 32 rows per pass) on the same fp16 values, so both planes hold the
+  // bits of the separate launch.
+  if (proj == 1 && a.kn) {  // workgroup-uniform
+    constexpr int KD = 128, KSTR = KD + 8;  // staged row stride in halves (16 bytes of padding)
+    _Float16* const kst = &xs[0][0];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = 32 * rtile(k) + 8 * (e >> 2) + 4 * hh + (e & 3);
+        kst[row * KSTR + col] = static_cast<_Float16>(acc[k][e]);
+      }
+    wait_lgkmcnt<0>();
+    stage_barrier();
+    const int S = a.kn_S, j = tid & 7;
+    const size_t plane = static_cast<size_t>(M) * N;
+    const uint4v glo = *reinterpret_cast<const uint4v*>(a.kn_gamma + 8 * j);
+    const uint4v ghi = *reinterpret_cast<const uint4v*>(a.kn_gamma + KD / 2 + 8 * j);
+#pragma unroll 1
+    for (int pass = 0; pass < 4; ++pass) {
+      const int row = 32 * pass + (tid >> 3), m = m0 + row;
+      if (m >= M) break;  // rows ascend with tid: the eight lanes of a row leave together
+      const int b = m / S, pos = m - b * S;
+      if (pos >= static_cast<int>(min(a.kn_lengths[b], static_cast<uint32_t>(S)))) continue;
+      const half8 lo = *reinterpret_cast<const half8*>(kst + row * KSTR + 8 * j);
+      const half8 hi = *reinterpret_cast<const half8*>(kst + row * KSTR + KD / 2 + 8 * j);
+      half8 first, second, first_lo, second_lo;
+      norm_rope_piece<KD>(lo, hi, glo, ghi, a.kn_cos + static_cast<size_t>(pos) * (KD / 2) + 8 * j,
+                          a.kn_sin + static_cast<size_t>(pos) * (KD / 2) + 8 * j, a.kn_eps, first,
+                          second, first_lo, second_lo);
+      const size_t base = static_cast<size_t>(m) * N + static_cast<size_t>(tile) * KD;
+      *reinterpret_cast<half8*>(a.kn + base + 8 * j) = first;
+      *reinterpret_cast<half8*>(a.kn + base + KD / 2 + 8 * j) = second;
+      if (a.kn_split) {
+        *reinterpret_cast<half8*>(a.kn + plane + base + 8 * j) = first_lo;
+        *reinterpret_cast<half8*>(a.kn + plane + base + KD / 2 + 8 * j) = second_lo;
+      }
+    }
+  }
 }
 
 

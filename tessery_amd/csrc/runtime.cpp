@@ -589,6 +589,28 @@ const RopeTable* rope_of(Runtime* rt, const Params& p) {
 
 // ---- launch -----------------------------------------------------------------------------------
 
+// Kernel arguments of a qkv4_f16 op: buffers x, w_qkv, s_qkv, b_qkv, yq, yk, yv with the three
+// weight sets concatenated on N (q first); no k prologue.
+tessery::Qkv4Args qkv4_args(const Op& op) {
+  const Params& p = op.p;
+  tessery::Qkv4Args a{};
+  const int K = static_cast<int>(p.k);
+  const int nq = static_cast<int>(p.cols), nkv = static_cast<int>(p.n);
+  const int offsets[3] = {0, nq, nq + nkv};
+  a.x = static_cast<const _Float16*>(op.ptr[0]);
+  for (int i = 0; i < 3; ++i) {
+    a.w[i] = static_cast<const uint32_t*>(op.ptr[1]) + static_cast<size_t>(offsets[i]) * (K / 8);
+    a.s[i] = static_cast<const uint16_t*>(op.ptr[2]) + static_cast<size_t>(offsets[i]) * (K / 64);
+    a.b[i] = static_cast<const uint16_t*>(op.ptr[3]) + static_cast<size_t>(offsets[i]) * (K / 64);
+    a.y[i] = static_cast<_Float16*>(op.ptr[4 + i]);
+    a.n[i] = i == 0 ? nq : nkv;
+  }
+  a.M = static_cast<int>(p.rows);
+  a.K = K;
+  a.scale_bf16 = p.u1 & 1u;
+  return a;
+}
+
 hipError_t launch(Runtime* rt, const Op& op) {
   hipStream_t st = rt->stream;
   const Params& p = op.p;
@@ -668,24 +690,8 @@ hipError_t launch(Runtime* rt, const Op& op) {
           static_cast<int>(p.cols), static_cast<int>(p.k), rt->dense_scratch, kDenseScratchFloats,
           st);
     }
-    case R_QKV4_F16: {
-      tessery::Qkv4Args a{};
-      const int K = static_cast<int>(p.k);
-      const int nq = static_cast<int>(p.cols), nkv = static_cast<int>(p.n);
-      const int offsets[3] = {0, nq, nq + nkv};
-      a.x = static_cast<const _Float16*>(op.ptr[0]);
-      for (int i = 0; i < 3; ++i) {
-        a.w[i] = static_cast<const uint32_t*>(op.ptr[1]) + static_cast<size_t>(offsets[i]) * (K / 8);
-        a.s[i] = static_cast<const uint16_t*>(op.ptr[2]) + static_cast<size_t>(offsets[i]) * (K / 64);
-        a.b[i] = static_cast<const uint16_t*>(op.ptr[3]) + static_cast<size_t>(offsets[i]) * (K / 64);
-        a.y[i] = static_cast<_Float16*>(op.ptr[4 + i]);
-        a.n[i] = i == 0 ? nq : nkv;
-      }
-      a.M = static_cast<int>(p.rows);
-      a.K = K;
-      a.scale_bf16 = p.u1 & 1u;
-      return tessery::launch_qkv4_f16(a, st);
-    }
+    case R_QKV4_F16:
+      return tessery::launch_qkv4_f16(qkv4_args(op), st);
     case R_GATED4_16X32:
     case R_GATED4_8X32: {
       RowRange rr;
@@ -918,7 +924,11 @@ int mi_dispatch(void* runtime, const char* name, void** buffers, uint32_t count,
 //   a projection covering every row of its output, then gelu_f32 over exactly that output
 //     -> the projection with the GELU epilogue;
 //   add(a, b -> a), then layer_norm(a -> a) over the same rows
-//     -> one pass that adds and normalizes in place.
+//     -> one pass that adds and normalizes in place;
+//   add(a, b -> a), then rms_norm(a -> y) -> one pass (add_rms_norm_f32);
+//   an in-place rms_norm, then rope on the same rows -> rms_norm_rope_f32;
+//   qkv4_f16, then norm_rope_f16 over its k output (D = 128) -> the projection with the k
+//     prologue in the k tiles' epilogue.
 // Returns the launch status, or hipErrorNotReady when ops[i], ops[i + 1] are not such a pair.
 hipError_t launch_fused_pair(Runtime* rt, const Op& a, const Op& b) {
   hipStream_t st = rt->stream;
@@ -953,6 +963,28 @@ hipError_t launch_fused_pair(Runtime* rt, const Op& a, const Op& b) {
         static_cast<float*>(a.ptr[0]), static_cast<const float*>(a.ptr[1]),
         static_cast<const uint16_t*>(b.ptr[1]), static_cast<float*>(b.ptr[2]),
         static_cast<int>(b.threads / 32), static_cast<int>(b.p.cols), b.p.eps, st);
+  }
+  if (a.route == R_QKV4_F16 && b.route == R_NORM_ROPE_F16 && b.ptr[0] == a.ptr[5] &&
+      b.p.dim == 128 && static_cast<uint64_t>(b.p.heads) * 128 == a.p.n &&
+      b.threads == a.p.rows) {
+    // the projection's k output, then its k prologue (the fused attention's norm_rope_f16):
+    // the k tiles finish with the prologue; the k output itself is still written
+    for (int i = 0; i < 7; ++i)
+      if (b.ptr[3] == a.ptr[i]) return hipErrorNotReady;
+    for (int i = 4; i < 7; ++i)
+      if (b.ptr[1] == a.ptr[i] || b.ptr[2] == a.ptr[i]) return hipErrorNotReady;
+    const RopeTable* t = rope_of(rt, b.p);
+    if (!t) return hipErrorNotReady;
+    tessery::Qkv4Args q = qkv4_args(a);
+    q.kn = static_cast<_Float16*>(b.ptr[3]);
+    q.kn_split = (b.p.u1 & 1u) != 0;
+    q.kn_gamma = static_cast<const uint16_t*>(b.ptr[1]);
+    q.kn_cos = t->cos;
+    q.kn_sin = t->sin;
+    q.kn_lengths = static_cast<const uint32_t*>(b.ptr[2]);
+    q.kn_S = static_cast<int>(b.p.seq);
+    q.kn_eps = b.p.eps;
+    return tessery::launch_qkv4_f16(q, st);
   }
   if (a.route == R_RMS_NORM && b.route == R_ROPE && a.ptr[2] == a.ptr[0] &&
       b.ptr[0] == a.ptr[0] && b.p.dim == a.p.cols &&
