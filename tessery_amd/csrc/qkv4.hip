@@ -732,6 +732,10 @@ bool qkv4_f16_fits(int M, int K, const int n[3]) {
 hipError_t launch_qkv4_f16(const Qkv4Args& a, hipStream_t st) {
   if (a.M <= 0) return hipSuccess;
   if (!qkv4_f16_fits(a.M, a.K, a.n)) return hipErrorInvalidValue;
+  // the k prologue reads rows as [M / kn_S, kn_S] positions of whole batch rows
+  if (a.kn && (a.kn_S <= 0 || a.M % a.kn_S || !a.kn_gamma || !a.kn_cos || !a.kn_sin ||
+               !a.kn_lengths))
+    return hipErrorInvalidValue;
   int tiles = 0;
   for (int p = 0; p < 3; ++p) tiles += a.n[p] / 128;
   dim3 grid((a.M + 127) / 128, tiles);
