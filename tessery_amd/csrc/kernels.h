@@ -89,14 +89,15 @@ constexpr int kLinear4HiloRows = 1024;
 hipError_t launch_linear4_hilo_f32(const float* x, const uint32_t* w, const uint16_t* scales,
                                    const uint16_t* biases, float* y, int M, int N, int K,
                                    float* scratch, size_t scratch_floats, hipStream_t st);
-// The gated MLP's gate and up projections of one x in one launch on the same path: u = x Wu^T,
-// y = silu(x Wg^T) * u, the values linear4 (gate -> y) + linear4 (up -> u) + silu_gate(y, u)
-// leave, bit for bit. M >= kLinear4HiloRows, both sets' scale / bias words within 20 KiB.
+// Two projections of one x with the same shape in one launch on the same path: u = x Wu^T and
+// y = x Wg^T, or with `gated` (the gated MLP) y = silu(x Wg^T) * u: the values linear4 (-> y) +
+// linear4 (-> u) (+ silu_gate(y, u)) leave, bit for bit. M >= kLinear4HiloRows, both sets' scale
+// / bias words within 20 KiB.
 bool linear4_hilo_dual_fits(int M, int N, int K);
 hipError_t launch_linear4_hilo_dual_f32(const float* x, const uint32_t* w, const uint16_t* scales,
                                         const uint16_t* biases, float* y, const uint32_t* uw,
                                         const uint16_t* uscales, const uint16_t* ubiases, float* u,
-                                        int M, int N, int K, float* scratch,
+                                        bool gated, int M, int N, int K, float* scratch,
                                         size_t scratch_floats, hipStream_t st);
 // gate[i] = silu(gate[i]) * up[i] for i < n (tessery silu_gate, kernels.metal:334-337).
 hipError_t launch_silu_gate_f32(float* gate, const float* up, uint32_t n, hipStream_t st);

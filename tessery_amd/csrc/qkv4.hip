@@ -420,10 +420,11 @@ constexpr int kHiloChunk = 16;
 // ahead in two register sets.
 // 64-row tiles keep two workgroups on every CU down to 8 column tiles x 4096 rows.
 //
-// DUAL (the gated MLP's gate and up projections of one x): the tile runs both weight sets over the
+// DUAL (two projections of one x with the same shape): the tile runs both weight sets over the
 // same staged x and row sums, each with its own weight ring, scale / bias words, fold and bias
-// term in the same order as a single launch, and stores up to y2 and silu(gate) * up to y: the
-// values linear4 + linear4 + silu_gate leave in their two outputs.
+// term in the same order as a single launch, and stores the second projection to y2 and the
+// first to y, or, with `gated` (the gated MLP's gate and up), silu(gate) * up to y: the values
+// linear4 + linear4 (+ silu_gate) leave in their two outputs.
 template <bool DUAL>
 __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__ x,
                                                       const float* __restrict__ rs,
@@ -434,7 +435,8 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
                                                       const uint32_t* __restrict__ w2,
                                                       const uint16_t* __restrict__ sc2,
                                                       const uint16_t* __restrict__ bi2,
-                                                      float* __restrict__ y2, int M, int N, int K) {
+                                                      float* __restrict__ y2, int gated, int M,
+                                                      int N, int K) {
   constexpr int TM = 64;
   constexpr int NW = DUAL ? 2 : 1;  // weight sets
   __shared__ __attribute__((aligned(1024))) _Float16 xs[2][2][TM * 64];  // [stage][hi, lo]
@@ -657,7 +659,7 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
         if constexpr (DUAL) {
           const float gate = acc[0][j][e] * inv, up = acc[1][j][e] * inv;
           y2[at] = up;
-          y[at] = silu_times(gate, up);
+          y[at] = gated ? silu_times(gate, up) : gate;
         } else {
           y[at] = acc[0][j][e] * inv;
         }
@@ -688,8 +690,8 @@ hipError_t launch_linear4_hilo_f32(const float* x, const uint32_t* w, const uint
   row_scales_f32<<<(M + 3) / 4, 256, 0, st>>>(x, M, K, scratch);
   dim3 grid((M + 63) / 64, N / 128);
   linear4_hilo<false><<<grid, 256, hilo_sb_bytes(K), st>>>(x, scratch, w, scales, biases, y,
-                                                          nullptr, nullptr, nullptr, nullptr, M,
-                                                          N, K);
+                                                          nullptr, nullptr, nullptr, nullptr, 0,
+                                                          M, N, K);
   return hipGetLastError();
 }
 
@@ -703,7 +705,7 @@ bool linear4_hilo_dual_fits(int M, int N, int K) {
 hipError_t launch_linear4_hilo_dual_f32(const float* x, const uint32_t* w, const uint16_t* scales,
                                         const uint16_t* biases, float* y, const uint32_t* uw,
                                         const uint16_t* uscales, const uint16_t* ubiases, float* u,
-                                        int M, int N, int K, float* scratch,
+                                        bool gated, int M, int N, int K, float* scratch,
                                         size_t scratch_floats, hipStream_t st) {
   if (M <= 0) return hipSuccess;
   if (!linear4_hilo_dual_fits(M, N, K) || !hilo_fits(M, N, K, x, scratch, scratch_floats))
@@ -711,7 +713,8 @@ hipError_t launch_linear4_hilo_dual_f32(const float* x, const uint32_t* w, const
   row_scales_f32<<<(M + 3) / 4, 256, 0, st>>>(x, M, K, scratch);
   dim3 grid((M + 63) / 64, N / 128);
   linear4_hilo<true><<<grid, 256, 2 * hilo_sb_bytes(K), st>>>(x, scratch, w, scales, biases, y,
-                                                             uw, uscales, ubiases, u, M, N, K);
+                                                             uw, uscales, ubiases, u,
+                                                             gated ? 1 : 0, M, N, K);
   return hipGetLastError();
 }
 

@@ -919,6 +919,9 @@ int mi_dispatch(void* runtime, const char* name, void** buffers, uint32_t count,
   return queue_op(rt, op) ? 0 : 1;
 }
 
+bool is_linear4(Route r);
+hipError_t launch_fused_dual(Runtime* rt, const Op& a, const Op& b, bool gated);
+
 // Pairs of queued launches that one kernel runs with the same bits (the second op of a pair is
 // then not launched on its own):
 //   a projection covering every row of its output, then gelu_f32 over exactly that output
@@ -928,10 +931,13 @@ int mi_dispatch(void* runtime, const char* name, void** buffers, uint32_t count,
 //   add(a, b -> a), then rms_norm(a -> y) -> one pass (add_rms_norm_f32);
 //   an in-place rms_norm, then rope on the same rows -> rms_norm_rope_f32;
 //   qkv4_f16, then norm_rope_f16 over its k output (D = 128) -> the projection with the k
-//     prologue in the k tiles' epilogue.
+//     prologue in the k tiles' epilogue;
+//   two uint4 projections of the same x with the same shape -> one fp16-MFMA launch
+//     (launch_fused_dual).
 // Returns the launch status, or hipErrorNotReady when ops[i], ops[i + 1] are not such a pair.
 hipError_t launch_fused_pair(Runtime* rt, const Op& a, const Op& b) {
   hipStream_t st = rt->stream;
+  if (is_linear4(a.route)) return launch_fused_dual(rt, a, b, false);
   const bool projection = a.route == R_MATMUL || a.route == R_MATMUL_TILED ||
                           a.route == R_MATMUL_CHUNK32 || a.route == R_MATMUL_BIAS ||
                           a.route == R_MATMUL_BIAS_CHUNK32;
@@ -1010,15 +1016,26 @@ bool is_linear4(Route r) {
 // of x and leaves the same bits in g and u. Returns the launch status, or hipErrorNotReady when
 // ops[i .. i + 2] are not such a triple.
 hipError_t launch_fused_gated(Runtime* rt, const Op& a, const Op& b, const Op& c) {
-  if (!is_linear4(a.route) || b.route != a.route || c.route != R_SILU_GATE) return hipErrorNotReady;
+  if (c.route != R_SILU_GATE || c.ptr[0] != a.ptr[4] || c.ptr[1] != b.ptr[4] ||
+      static_cast<uint64_t>(c.p.n) != static_cast<uint64_t>(a.p.rows) * a.p.cols)
+    return hipErrorNotReady;
+  return launch_fused_dual(rt, a, b, true);
+}
+
+// Two uint4 projections of the same x with the same shape (the k and v projections of a Qwen3
+// layer, or the gated MLP's gate and up) as one launch of the fp16-MFMA kernel, with the bits of
+// the two launches; with `gated` the first output receives silu(first) * second. Returns the
+// launch status, or hipErrorNotReady when the pair does not qualify.
+hipError_t launch_fused_dual(Runtime* rt, const Op& a, const Op& b, bool gated) {
+  if (!is_linear4(a.route) || b.route != a.route) return hipErrorNotReady;
   const Params &pa = a.p, &pb = b.p;
   if (pa.rows != pb.rows || pa.cols != pb.cols || pa.k != pb.k || a.ptr[0] != b.ptr[0])
     return hipErrorNotReady;
-  // outputs distinct from x and from each other: the second projection reads the same x
+  // outputs distinct from x, from each other and from the second projection's weights: the second
+  // projection reads them after the first has written its output
   if (a.ptr[4] == a.ptr[0] || b.ptr[4] == a.ptr[0] || a.ptr[4] == b.ptr[4]) return hipErrorNotReady;
-  if (c.ptr[0] != a.ptr[4] || c.ptr[1] != b.ptr[4] ||
-      static_cast<uint64_t>(c.p.n) != static_cast<uint64_t>(pa.rows) * pa.cols)
-    return hipErrorNotReady;
+  for (int i = 1; i < 4; ++i)
+    if (b.ptr[i] == a.ptr[4]) return hipErrorNotReady;
   RowRange ra, rb;
   if (!linear4_range(a.route, pa, a.threads, a.group, &ra) ||
       !linear4_range(b.route, pb, b.threads, b.group, &rb) || ra.r0 != 0 || ra.r1 != pa.rows ||
@@ -1032,9 +1049,9 @@ hipError_t launch_fused_gated(Runtime* rt, const Op& a, const Op& b, const Op& c
       static_cast<const uint16_t*>(a.ptr[2]), static_cast<const uint16_t*>(a.ptr[3]),
       static_cast<float*>(a.ptr[4]), static_cast<const uint32_t*>(b.ptr[1]),
       static_cast<const uint16_t*>(b.ptr[2]), static_cast<const uint16_t*>(b.ptr[3]),
-      static_cast<float*>(b.ptr[4]), M, N, K, rt->dense_scratch, kDenseScratchFloats,
+      static_cast<float*>(b.ptr[4]), gated, M, N, K, rt->dense_scratch, kDenseScratchFloats,
       rt->stream);
-  // hipErrorInvalidValue: nothing was launched (alignment or sizes); the three ops run as queued
+  // hipErrorInvalidValue: nothing was launched (alignment or sizes); the ops run as queued
   return e == hipErrorInvalidValue ? hipErrorNotReady : e;
 }
 

@@ -215,3 +215,43 @@ def test_qwen3_layer_tail_matches_oracle(runtime, tokens):
     expected = qwen_block.layer_tail(x, attended, w, bf16_values(gamma), eps=eps)
     scale = np.abs(expected).max()
     np.testing.assert_allclose(got, expected, atol=1e-5 * scale, rtol=1e-4)
+
+
+@pytest.mark.parametrize("rows,cols,k,fused", [(4096, 1024, 1024, True), (1040, 256, 512, True),
+                                               (1029, 256, 512, False)])
+def test_two_projections_of_one_x_run_as_one_kernel_with_the_same_bits(runtime, rows, cols, k,
+                                                                       fused):
+    """Two uint4 projections of the same x with the same shape queued back to back (a Qwen3
+    layer's k and v projections) run as one fp16-MFMA launch from 1024 rows, leaving the bits of
+    the two launches in separate commands in both outputs; at 1029 rows each projection is
+    several launches and nothing is fused."""
+    rng = np.random.default_rng(7 * rows + cols + k)
+    x = rng.normal(size=(rows, k)).astype(np.float32)
+    sets = [(ref.pack(rng.integers(0, 16, size=(cols, k), dtype=np.uint32)),
+             bf16_words(rng.uniform(0.01, 0.2, size=(cols, k // 64))),
+             bf16_words(rng.uniform(-1, 0.1, size=(cols, k // 64)))) for _ in range(2)]
+    buffers = [runtime.upload(a) for a in [x, *sets[0], *sets[1]]]
+    outs = [runtime.buffer(rows * cols * 4) for _ in range(4)]
+    try:
+        before = runtime.diagnostics()["fused_pairs"]
+        with runtime.command():
+            runtime._linear4([*buffers[:4], outs[0]], rows=rows, cols=cols, k=k)
+            runtime._linear4([buffers[0], *buffers[4:7], outs[1]], rows=rows, cols=cols, k=k)
+        assert runtime.diagnostics()["fused_pairs"] == before + int(fused)
+        with runtime.command():
+            runtime._linear4([*buffers[:4], outs[2]], rows=rows, cols=cols, k=k)
+        with runtime.command():
+            runtime._linear4([buffers[0], *buffers[4:7], outs[3]], rows=rows, cols=cols, k=k)
+        assert runtime.diagnostics()["fused_pairs"] == before + int(fused)
+        got = [runtime.read(b, (rows, cols)) for b in outs]
+        np.testing.assert_array_equal(got[0], got[2])
+        np.testing.assert_array_equal(got[1], got[3])
+        # and within the fp16 MFMA path's bound of float64 (2e-6 of sum_k |x| |w| per element)
+        xd = x.astype(np.float64)
+        for (packed, s, b), y in zip(sets, got[:2]):
+            w = ref.dequantize(packed, s, b, k, "bf16")
+            bound = 2e-6 * (np.abs(xd) @ np.abs(w).T) + 1e-30
+            assert np.all(np.abs(y - xd @ w.T) <= bound)
+    finally:
+        for b in buffers + outs:
+            b.close()
