@@ -17,6 +17,7 @@ length with fp16 output.
 
 --workload selects one of the other measured configurations instead (one JSON line each):
   qwen3_8x512       B=8, S=512, lengths U{64..512} (seed 3), same fused path, 8 layers
+  qwen3_32x512_full B=32, S=512, every length 512, the same fused path with fp16 output, 8 layers
   qwen3_8x512_f32   the same shape on the fp32 route (attention_tiled, D=128), 8 layers
   bge_32x512        BGE-small fp32 bidirectional attention, B=32, S=512, 12 heads x 32,
                     lengths U{2..512} (seed 2), 12 layers, route attention_tiled
@@ -135,13 +136,28 @@ def run_timed(rt: HipRuntime, step: Callable[[], None], steps: int, warmup: int,
             for _ in range(prof_steps):
                 step()
     kernels: dict[str, list[float]] = {}
+    fused: dict[str, str] = {}
     for r in records:
-        kernels.setdefault(r["kernel"], []).append(r["gpu_seconds"])
+        # a launch the runtime ran inside the previous op's kernel has no time of its own
+        if "fused_into" in r:
+            fused[r["kernel"]] = r["fused_into"]
+        else:
+            kernels.setdefault(r["kernel"], []).append(r["gpu_seconds"])
     return {
         "step": wall / steps,
         "gpu_step": gpu / steps if gpu >= 0 else None,
         "kernel_s": {k: float(np.mean(v)) for k, v in kernels.items()},
+        "kernel_step_s": {k: float(np.sum(v)) / prof_steps for k, v in kernels.items()},
+        "fused": {k: v for k, v in fused.items() if k not in kernels},
     }
+
+
+def kernel_us(t: dict[str, Any]) -> dict[str, Any]:
+    """Mean launch durations in microseconds; a route that only ran fused into another kernel is
+    listed with the kernel that carried it instead of a time."""
+    out: dict[str, Any] = {k: v * 1e6 for k, v in t["kernel_s"].items()}
+    out.update({k: {"fused_into": v} for k, v in t.get("fused", {}).items()})
+    return out
 
 
 def upload_qwen_layers(rt: HipRuntime, shape: workloads.Shape, layers: int, seed: int,
@@ -263,11 +279,21 @@ def bench_qwen(args, name: str, shape, lengths, seed: int, layers: int, lengths_
                 if not replayed:
                     direct()
 
+        odt = np.float16 if out_bytes == 2 else np.float32
         with rt._workspace():
             t = run_timed(rt, step, args.steps, args.warmup, 2 * layers)
+            # the parity check reads what a graph replay wrote: layer 0's output is poisoned with
+            # NaN, one step is replayed, and the result must also equal the direct launches' bits
+            rt.write(sets[0]["out"], np.full(host0["q"].shape, np.nan, odt))
+            replays = rt.diagnostics()["graph_launches"]
+            with rt.command():
+                step()
+            replayed = rt.diagnostics()["graph_launches"] > replays
+            out_graph = rt.read(sets[0]["out"], host0["q"].shape, odt)
         t_direct = run_timed(rt, direct, args.steps, 1, 2 * layers, profile=False)
-        out0 = rt.read(sets[0]["out"], host0["q"].shape, np.float16 if out_bytes == 2 else np.float32)
+        out0 = rt.read(sets[0]["out"], host0["q"].shape, odt)
         graphs = rt.diagnostics()
+        graph_bits_equal = bool(replayed and np.array_equal(out_graph, out0, equal_nan=False))
 
     step_s = t["step"]
     attn_avg = t["kernel_s"]["attention_f16_norm_rope"]
@@ -304,9 +330,9 @@ def bench_qwen(args, name: str, shape, lengths, seed: int, layers: int, lengths_
         "dense_convention_tflops": workloads.dense_flop(shape) * layers / step_s / 1e12,
         "gpu_event_ms_per_step": t["gpu_step"] * 1e3 if t["gpu_step"] is not None else None,
         "ms_per_step_direct_launches": t_direct["step"] * 1e3,
-        "plan_graph": {"builds": graphs["graph_builds"], "launches": graphs["graph_launches"]},
-        "kernel_us": {"attention_f16_norm_rope": attn_avg * 1e6,
-                      "norm_rope_f16": t["kernel_s"]["norm_rope_f16"] * 1e6},
+        "plan_graph": {"builds": graphs["graph_builds"], "launches": graphs["graph_launches"],
+                       "replay_equals_direct_launches": graph_bits_equal},
+        "kernel_us": kernel_us(t),
         "roofline": {
             "bound": "hbm",
             "achieved": achieved,
@@ -316,17 +342,22 @@ def bench_qwen(args, name: str, shape, lengths, seed: int, layers: int, lengths_
             "traffic": measured_traffic() if headline else None,
             "algorithmic_bytes": nbytes,
             "kernel": "attention_f16_norm_rope",
+            # the whole step (k prologue + attention per layer) against the attention's bytes
+            "step_achieved": nbytes * layers / step_s / 1e9,
+            "step_frac": nbytes * layers / step_s / 1e9 / PEAK_HBM_GBS,
             "mfma_tflops": flop / attn_avg / 1e12,
         },
     }
     if not args.no_cpu_baseline:
         log("cpu baseline")
         expected, result["cpu_baseline"] = qwen_cpu_baselines(shape, lengths, host0, layers)
-        err = float(np.max(np.abs(out0.astype(np.float64) - expected)))
+        # layer 0 as a graph replay wrote it (bit-equal to the direct launches, checked above)
+        err = float(np.max(np.abs(out_graph.astype(np.float64) - expected)))
         result["max_abs_err_layer0"] = err
         # the fused route carries q, k and P at ~22 bits: held to the fp32 bar with fp32 output
         bar = PARITY_F32_OUT if out_dtype == "f32" else PARITY_F16_OUT
-        result["parity"] = {"max_abs": err, "bar": bar, "ok": err <= bar}
+        result["parity"] = {"max_abs": err, "bar": bar, "graph_replay": graph_bits_equal,
+                            "ok": bool(err <= bar and graph_bits_equal)}
     else:
         result["cpu_baseline"] = None
     return result
@@ -374,7 +405,7 @@ def bench_bge(args, layers: int = 12) -> dict:
                    "dim": shape.dim, "layers": layers, "valid_tokens": int(lengths.sum()),
                    "lengths": "uniform [2,512], seed 2"},
         "tflops": flop * layers / step_s / 1e12,
-        "kernel_us": {kernel: avg * 1e6},
+        "kernel_us": kernel_us(t),
         "roofline": {
             "bound": "mfma",
             "achieved": tflops_kernel,
@@ -457,7 +488,7 @@ def bench_qwen_f32(args, layers: int = 8) -> dict:
                    "batch": shape.batch, "seq": shape.seq, "heads": shape.heads,
                    "kv_heads": shape.kv_heads, "dim": shape.dim, "layers": layers,
                    "valid_tokens": int(lengths.sum()), "lengths": "uniform [64,512], seed 3"},
-        "kernel_us": {kernel: avg * 1e6},
+        "kernel_us": kernel_us(t),
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_F32_TFLOPS,
                      "unit": "TFLOP/s", "frac": tflops / PEAK_F32_TFLOPS, "traffic": None,
                      "algorithmic_flop": flop, "algorithmic_bytes": nbytes,
@@ -526,7 +557,7 @@ def bench_qkv4_block(args, layers: int = 8) -> dict:
         "config": {"workload": "qwen_qkv4_16x256: qkv4 -> k norm+RoPE -> fused attention",
                    "rows": m, "k": k_in, "n": n_total, "layers": layers,
                    "valid_tokens": int(lengths.sum()), "lengths": "uniform [1,256], seed 5"},
-        "kernel_us": {k: v * 1e6 for k, v in ks.items()},
+        "kernel_us": kernel_us(t),
         "roofline": {
             "bound": "mfma",
             "achieved": gemm_flop / gemm / 1e12,
@@ -588,14 +619,11 @@ def bench_qwen_tail(args, tokens: int = 16 * 256) -> dict:
         out0 = rt.read(sets[0]["out"], (tokens, hidden))
     step_s = t["step"]
     ks = t["kernel_s"]
-    # the four projections run the linear4 kernel: route linear4_16x32_k64 at 4096 rows; at the
-    # measured Qwen3 heights linear4_32x32_k64 for o / down and the fused gated4 route
-    if "linear4_16x32_k64" in ks:
-        gemm_s = 4 * ks["linear4_16x32_k64"]
-        kernel = "linear4_16x32_k64"
-    else:
-        gemm_s = 2 * ks["linear4_32x32_k64"] + 2 * ks["gated4_16x32_k64"]
-        kernel = "linear4_32x32_k64 + gated4_16x32_k64"
+    # the four projections of a layer: every linear4 / gated4 launch of a step (the gated MLP's
+    # gate + up + SiLU run as one launch from 1024 rows, carried by the gate's record)
+    proj = sorted(k for k in t["kernel_step_s"] if k.startswith(("linear4", "gated4")))
+    gemm_s = sum(t["kernel_step_s"][k] for k in proj) / layers
+    kernel = " + ".join(proj)
     tflops = flop / gemm_s / 1e12
     # from 1024 rows linear4 runs on fp16 MFMA (row-scaled hi + lo halves of x, two MFMAs per
     # product): priced against the fp16 peak; below that on fp32 MFMA
@@ -620,7 +648,7 @@ def bench_qwen_tail(args, tokens: int = 16 * 256) -> dict:
                                "-> down -> residual", "tokens": tokens, "hidden": hidden,
                    "attention_width": width, "intermediate": inter, "layers": layers},
         "tflops": flop * layers / step_s / 1e12,
-        "kernel_us": {k: v * 1e6 for k, v in ks.items()},
+        "kernel_us": kernel_us(t),
         "roofline": {
             "bound": "mfma",
             "achieved": tflops,
@@ -741,7 +769,7 @@ def bench_bge_layer(args) -> dict:
                    "batch": batch, "seq": seq, "hidden": hidden, "intermediate": inter,
                    "layers": layers, "lengths": "uniform [2,512], seed 2"},
         "tflops": flop * layers / step_s / 1e12,
-        "kernel_us": {k: v * 1e6 for k, v in ks.items()},
+        "kernel_us": kernel_us(t),
         "roofline": {
             "bound": "mfma",
             "achieved": tflops,
@@ -1019,10 +1047,10 @@ def secondary_measurements(args) -> dict:
                    headline=False), PEAK_F16_TFLOPS)
     out["qwen3_8x512_f32"] = _kernel_summary(bench_qwen_f32(sub, layers=4), PEAK_F32_TFLOPS)
     out["qwen_qkv4_16x256"] = _kernel_summary(bench_qkv4_block(sub, layers=8), PEAK_F16_TFLOPS)
-    full = workloads.Shape(32, 512, 16, 8, 128, causal=True)
+    full, full_lengths = workloads.qwen3_32x512_full()
     out["qwen3_32x512_full_f16out"] = _kernel_summary(
-        bench_qwen(sub, "qwen3_32x512_full", full, np.full(32, 512, np.uint32), 4, 4,
-                   "all 512", headline=False, out_dtype="f16"), PEAK_F16_TFLOPS)
+        bench_qwen(sub, "qwen3_32x512_full", full, full_lengths, 4, 4, "all 512",
+                   headline=False, out_dtype="f16"), PEAK_F16_TFLOPS)
     return out
 
 
@@ -1034,7 +1062,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--layers", type=int, default=LAYERS, help="headline workload only")
     parser.add_argument("--workload", default="qwen3_32x512",
-                        choices=["qwen3_32x512", "qwen3_8x512", "qwen3_8x512_f32", "bge_32x512",
+                        choices=["qwen3_32x512", "qwen3_8x512", "qwen3_32x512_full",
+                                 "qwen3_8x512_f32", "bge_32x512",
                                  "qwen_qkv4_16x256",
                                  "qwen_tail_16x256", "qwen_tail_1x128", "bge_layer_32x512",
                                  "bge_plan_1x128", "qwen3_model_8x512", "bge_model_8x512"])
@@ -1063,6 +1092,10 @@ def main() -> int:
         shape, lengths = workloads.qwen3_8x512()
         result = bench_qwen(args, "qwen3_8x512", shape, lengths, 3, 8, "uniform [64,512], seed 3",
                             headline=False)
+    elif args.workload == "qwen3_32x512_full":
+        shape, lengths = workloads.qwen3_32x512_full()
+        result = bench_qwen(args, "qwen3_32x512_full", shape, lengths, 4, 8, "all 512",
+                            headline=False, out_dtype="f16")
     elif args.workload == "bge_32x512":
         result = bench_bge(args)
     elif args.workload == "qwen3_8x512_f32":

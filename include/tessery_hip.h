@@ -65,6 +65,11 @@ void mi_abort(void *runtime);
 int mi_profile_enable(void *runtime, int enabled);
 /* runtime.mm:278-283 */
 int mi_profile_read(void *runtime, double *seconds, uint32_t count);
+/* No counterpart in the reference (its runtime fuses nothing): for each dispatch of the last
+ * profiled command, 1 when it ran inside the kernel of the dispatch before it (a launch-time
+ * fusion; see mi_fusion_counts), so that its mi_profile_read seconds enclose no work of its own,
+ * else 0. `count` must equal mi_profile_read's. */
+int mi_profile_fused(void *runtime, uint8_t *fused, uint32_t count);
 
 /* runtime.mm:148-215. Prepared plans hold route ids, Params and binding slots, never buffers. */
 void *mi_plan_create(void *runtime, void **buffers, uint32_t count);
@@ -82,7 +87,8 @@ int mi_plan_run(void *runtime, void *plan, void **buffers, uint32_t count);
 int mi_graph_counts(void *runtime, uint64_t *launches, uint64_t *builds);
 /* No counterpart in the reference: the number of queued-launch pairs and gated-MLP triples
  * (linear4 gate, linear4 up, silu_gate) that ran as one kernel with the same bits, since
- * mi_create (diagnostics). */
+ * mi_create (diagnostics). A plan replayed as a HIP graph adds its fusions on every replay;
+ * capturing the graph adds nothing (captured launches do not run). */
 int mi_fusion_counts(void *runtime, uint64_t *pairs, uint64_t *gated);
 
 /* No counterpart in the reference (unified memory made it unnecessary there): copy `bytes`

@@ -747,16 +747,20 @@ __device__ __forceinline__ float dot_ones(half4 p, float acc) {
 }
 
 // The score accumulators of a QK^T chain are read by VALU (row max, masking) right after the last
-// v_mfma_f32_16x16x32_f16 of the chain, and the hardware does not interlock that read: it needs 8
-// wait states after the MFMA. The compiler counts them inside a basic block but not across the
-// branch that skips the causal masking, where the row max then read a partly accumulated score
-// (the softmax still came out right, being shift-invariant, but its rounding depended on timing).
-// The fence is 8 wait states after the chain, ordered after it through the operand.
+// MFMA of the chain, and the hardware does not interlock that read. AMD's CDNA3 ISA guide
+// ("Dependency Resolution: Required Independent Instructions") requires NumPasses + 3 wait states
+// between an XDL op writing a VGPR and a VALU read of it (11 for the 8-pass
+// v_mfma_f32_16x16x32_f16 / _bf16), and LLVM's gfx950 hazard recognizer adds one on gfx950: 12.
+// The compiler pads inside a basic block but not across the branch that skips the causal masking:
+// without this fence the gfx950 build reaches `v_max_f32` on the taken path one instruction after
+// the last MFMA, and the row max then read a partly accumulated score now and then (the softmax
+// still came out right, being shift-invariant, but its rounding depended on timing). The fence is
+// 12 wait states (s_nop 7 + s_nop 3) after the chain, ordered after it through the operand.
 __device__ __forceinline__ void mfma_result_fence(floatx4& acc) {
-  asm volatile("s_nop 7" : "+v"(acc));
+  asm volatile("s_nop 7\n\ts_nop 3" : "+v"(acc));
 }
 __device__ __forceinline__ void mfma_result_fence(floatx4& a, floatx4& b) {
-  asm volatile("s_nop 7" : "+v"(a), "+v"(b));
+  asm volatile("s_nop 7\n\ts_nop 3" : "+v"(a), "+v"(b));
 }
 
 // reduce over the four lanes r, r+16, r+32, r+48 that hold one query's scores

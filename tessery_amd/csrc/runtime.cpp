@@ -25,7 +25,7 @@ using tessery::Params;
 
 namespace {
 
-constexpr int kAbiVersion = 1;
+constexpr int kAbiVersion = 2;
 constexpr uint32_t kMaxBuffers = 8;
 constexpr size_t kMaxProfiled = 2048;  // runtime.mm:118 (4096 timestamp samples, 2 per dispatch)
 constexpr size_t kMaxPlanOps = 2048;   // runtime.mm:166
@@ -166,6 +166,9 @@ struct Runtime {
   bool profiling = false;
   std::vector<hipEvent_t> prof_events;
   std::vector<double> profile_seconds;
+  // per profiled op: 1 when it ran inside the kernel of the op before it (a launch-time fusion),
+  // so its events enclose no work of its own
+  std::vector<uint8_t> profile_fused;
   std::map<std::tuple<uint32_t, uint32_t, uint32_t>, RopeTable> rope;
   // Device allocations whose buffers were freed while a command was open: queued launches may
   // still name them, so they are released only after the command has finished or aborted.
@@ -181,10 +184,17 @@ struct PlanOp {
   std::array<uint32_t, kMaxBuffers> slots;
 };
 
-// An instantiated HIP graph of a plan's launches for one binding of its slots.
+// Launch-time fusions made while queuing a range of ops (see launch_range).
+struct FusionCount {
+  uint64_t pairs = 0, gated = 0;
+};
+
+// An instantiated HIP graph of a plan's launches for one binding of its slots, with the fusions
+// its captured launches made (added to the runtime's counts on every replay).
 struct CachedGraph {
   std::vector<void*> key;
   hipGraphExec_t exec;
+  FusionCount fused;
 };
 
 struct Plan {
@@ -1034,8 +1044,10 @@ hipError_t launch_fused_dual(Runtime* rt, const Op& a, const Op& b, bool gated) 
   // outputs distinct from x, from each other and from the second projection's weights: the second
   // projection reads them after the first has written its output
   if (a.ptr[4] == a.ptr[0] || b.ptr[4] == a.ptr[0] || a.ptr[4] == b.ptr[4]) return hipErrorNotReady;
+  // and the second output distinct from the first projection's weights, scales and biases: in one
+  // kernel the second projection's stores overlap the first projection's reads
   for (int i = 1; i < 4; ++i)
-    if (b.ptr[i] == a.ptr[4]) return hipErrorNotReady;
+    if (b.ptr[i] == a.ptr[4] || b.ptr[4] == a.ptr[i]) return hipErrorNotReady;
   RowRange ra, rb;
   if (!linear4_range(a.route, pa, a.threads, a.group, &ra) ||
       !linear4_range(b.route, pb, b.threads, b.group, &rb) || ra.r0 != 0 || ra.r1 != pa.rows ||
@@ -1056,14 +1068,16 @@ hipError_t launch_fused_dual(Runtime* rt, const Op& a, const Op& b, bool gated) 
 }
 
 // Launches ops [first, last) in order, running as one kernel the triples launch_fused_gated takes
-// and the pairs launch_fused_pair takes.
-hipError_t launch_range(Runtime* rt, size_t first, size_t last) {
+// and the pairs launch_fused_pair takes; the fusions made are added to *fc. Under stream capture
+// nothing runs yet, so the caller decides where the count goes (the runtime's totals for direct
+// launches, the cached graph for a capture).
+hipError_t launch_range(Runtime* rt, size_t first, size_t last, FusionCount* fc) {
   for (size_t i = first; i < last; ++i) {
     const hipError_t gated =
         i + 2 < last ? launch_fused_gated(rt, rt->ops[i], rt->ops[i + 1], rt->ops[i + 2])
                      : hipErrorNotReady;
     if (gated == hipSuccess) {
-      ++rt->fused_gated;
+      ++fc->gated;
       i += 2;
       continue;
     }
@@ -1071,7 +1085,7 @@ hipError_t launch_range(Runtime* rt, size_t first, size_t last) {
     const hipError_t fused =
         i + 1 < last ? launch_fused_pair(rt, rt->ops[i], rt->ops[i + 1]) : hipErrorNotReady;
     if (fused == hipSuccess) {
-      ++rt->fused_pairs;
+      ++fc->pairs;
       ++i;
       continue;
     }
@@ -1080,6 +1094,11 @@ hipError_t launch_range(Runtime* rt, size_t first, size_t last) {
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+void count_fusions(Runtime* rt, const FusionCount& fc) {
+  rt->fused_pairs += fc.pairs;
+  rt->fused_gated += fc.gated;
 }
 
 // A plan replay as one graph launch: the graph of this plan for this binding is instantiated the
@@ -1095,11 +1114,14 @@ hipError_t launch_segment_graph(Runtime* rt, const Segment& seg) {
       cache.erase(cache.begin() + static_cast<std::ptrdiff_t>(j));
       cache.push_back(hit);
       ++rt->graph_launches;
-      return hipGraphLaunch(hit.exec, rt->stream);
+      const hipError_t e = hipGraphLaunch(hit.exec, rt->stream);
+      if (e == hipSuccess) count_fusions(rt, hit.fused);
+      return e;
     }
   if (hipStreamBeginCapture(rt->stream, hipStreamCaptureModeThreadLocal) != hipSuccess)
     return hipErrorNotReady;
-  const hipError_t recorded = launch_range(rt, seg.first, seg.first + seg.count);
+  FusionCount fc;
+  const hipError_t recorded = launch_range(rt, seg.first, seg.first + seg.count, &fc);
   hipGraph_t graph = nullptr;
   const hipError_t ended = hipStreamEndCapture(rt->stream, &graph);
   if (recorded != hipSuccess || ended != hipSuccess || !graph) {
@@ -1118,10 +1140,20 @@ hipError_t launch_segment_graph(Runtime* rt, const Segment& seg) {
     (void)hipGraphExecDestroy(cache.front().exec);
     cache.erase(cache.begin());
   }
-  cache.push_back(CachedGraph{seg.key, exec});
+  cache.push_back(CachedGraph{seg.key, exec, fc});
   ++rt->graph_builds;
   ++rt->graph_launches;
-  return hipGraphLaunch(exec, rt->stream);
+  const hipError_t e = hipGraphLaunch(exec, rt->stream);
+  if (e == hipSuccess) count_fusions(rt, fc);
+  return e;
+}
+
+// Direct launches of ops [first, last), with their fusions counted.
+hipError_t launch_direct(Runtime* rt, size_t first, size_t last) {
+  FusionCount fc;
+  const hipError_t e = launch_range(rt, first, last, &fc);
+  if (e == hipSuccess) count_fusions(rt, fc);
+  return e;
 }
 
 int mi_finish(void* runtime) {
@@ -1144,18 +1176,19 @@ int mi_finish(void* runtime) {
     size_t i = 0;
     for (const Segment& seg : rt->segments) {
       if (failed) break;
-      if (launch_range(rt, i, seg.first) != hipSuccess) failed = 1;
+      if (launch_direct(rt, i, seg.first) != hipSuccess) failed = 1;
       if (failed) break;
       const hipError_t g = launch_segment_graph(rt, seg);
       if (g == hipErrorNotReady) {
-        if (launch_range(rt, seg.first, seg.first + seg.count) != hipSuccess) failed = 1;
+        if (launch_direct(rt, seg.first, seg.first + seg.count) != hipSuccess) failed = 1;
       } else if (g != hipSuccess) {
         failed = 1;
       }
       i = seg.first + seg.count;
     }
-    if (!failed && launch_range(rt, i, n) != hipSuccess) failed = 1;
+    if (!failed && launch_direct(rt, i, n) != hipSuccess) failed = 1;
   }
+  if (rt->profiling) rt->profile_fused.assign(n, 0);
   for (size_t i = 0; rt->profiling && i < n && !failed; ++i) {
     if (rt->profiling && hipEventRecord(rt->prof_events[2 * i], rt->stream) != hipSuccess) failed = 1;
     // a fused triple or pair runs inside the first op's events; the others' events enclose no
@@ -1178,8 +1211,10 @@ int mi_finish(void* runtime) {
     const size_t extra = !failed && gated == hipSuccess ? 2 : (!failed && fused == hipSuccess ? 1 : 0);
     rt->fused_gated += extra == 2;
     rt->fused_pairs += extra == 1;
+    rt->profile_fused[i] = 0;
     for (size_t e = 0; e < extra && !failed; ++e) {
       ++i;
+      rt->profile_fused[i] = 1;
       if (rt->profiling && (hipEventRecord(rt->prof_events[2 * i], rt->stream) != hipSuccess ||
                             hipEventRecord(rt->prof_events[2 * i + 1], rt->stream) != hipSuccess))
         failed = 1;
@@ -1204,6 +1239,7 @@ int mi_finish(void* runtime) {
     }
     if (failed) rt->profile_seconds.clear();
   }
+  if (rt->profile_seconds.empty()) rt->profile_fused.clear();
   rt->ops.clear();
   rt->segments.clear();
   rt->recording = false;
@@ -1230,6 +1266,7 @@ int mi_profile_enable(void* runtime, int enabled) {
   auto rt = static_cast<Runtime*>(runtime);
   if (!rt || rt->recording) return 1;
   rt->profile_seconds.clear();
+  rt->profile_fused.clear();
   rt->profiling = enabled != 0;
   if (!rt->profiling) release_profile_events(rt);
   return 0;
@@ -1239,6 +1276,13 @@ int mi_profile_read(void* runtime, double* seconds, uint32_t count) {
   auto rt = static_cast<Runtime*>(runtime);
   if (!rt || rt->recording || count != rt->profile_seconds.size()) return 1;
   if (count) std::memcpy(seconds, rt->profile_seconds.data(), count * sizeof(double));
+  return 0;
+}
+
+int mi_profile_fused(void* runtime, uint8_t* fused, uint32_t count) {
+  auto rt = static_cast<Runtime*>(runtime);
+  if (!rt || rt->recording || count != rt->profile_fused.size()) return 1;
+  if (count) std::memcpy(fused, rt->profile_fused.data(), count);
   return 0;
 }
 

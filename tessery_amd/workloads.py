@@ -124,6 +124,11 @@ def qwen3_32x512() -> tuple[Shape, NDArray[np.uint32]]:
     return Shape(32, execution_width(lengths), 16, 8, 128, causal=True), lengths
 
 
+def qwen3_32x512_full() -> tuple[Shape, NDArray[np.uint32]]:
+    """The Qwen3 32x512 shape with every length at 512 (the full-length form of the headline)."""
+    return Shape(32, 512, 16, 8, 128, causal=True), np.full(32, 512, np.uint32)
+
+
 def qwen_layer(shape: Shape, layer: int, seed: int) -> dict[str, NDArray]:
     """Pre-norm q/k and v in fp16 plus bf16 q/k norm weights for one layer."""
     rng = np.random.default_rng((seed, layer))

@@ -321,6 +321,20 @@ def test_qwen3_32x512(runtime, layer):
     assert err <= FUSED_F32_MAX, err
 
 
+def test_qwen3_32x512_full_length_f16_out(runtime):
+    """Every length 512 with fp16 output (the headline shape at full length): the whole batch runs
+    on the GPU, batch rows 0, 13 and 31 are checked against the float64 oracle at the fp16-output
+    bar."""
+    shape, lengths = workloads.qwen3_32x512_full()
+    t = workloads.qwen_layer(shape, 0, seed=4)
+    out, _ = norm_rope_attend(runtime, t, lengths, shape, "f16")
+    rows = [0, 13, 31]
+    sub = {name: (t[name][rows] if t[name].ndim == 4 else t[name]) for name in t}
+    _, expected = oracle_norm_rope(sub, lengths[rows])
+    err = np.max(np.abs(out[rows].astype(np.float64) - expected))
+    assert err <= fused_bar("f16"), err
+
+
 @pytest.mark.parametrize("aligned_first", [False, True])
 def test_fused_late_maximum_moves_the_running_max(runtime, aligned_first):
     """Fused route, causal: keys 40-55 line up with every query of head 0 (logit 128 / sqrt(128)

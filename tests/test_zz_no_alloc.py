@@ -140,3 +140,24 @@ def test_noalloc_rejects_shapes_beyond_its_scratch():
         status = lib.mi_attention_norm_rope_noalloc(*args, 1, 16, 16, 8, 96, 1e-6, 1e6, 0, 0,
                                                     None)
         assert status == 1
+
+
+def test_noalloc_under_graph_capture():
+    """The first call of the entry point in a fresh process made under hipStreamBeginCapture
+    (global mode), the graph replayed three times with eager calls of another shape in between:
+    every replay bit-equal to the route (tests/noalloc_capture_child.py)."""
+    import json
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    child = Path(__file__).resolve().parent / "noalloc_capture_child.py"
+    print("child: graph capture of mi_attention_norm_rope_noalloc", flush=True)
+    proc = subprocess.run([sys.executable, "-u", str(child)], capture_output=True, text=True,
+                          timeout=110)
+    lines = [line for line in proc.stdout.splitlines() if line.startswith("capture-result ")]
+    assert lines, proc.stdout[-2000:] + proc.stderr[-2000:]
+    result = json.loads(lines[-1][len("capture-result "):])
+    assert result["status_under_capture"] == 0 and result["end_capture"] == 0, result
+    assert result["replays_bit_equal"] == [True] * 6, result
+    assert proc.returncode == 0, proc.stderr[-2000:]
