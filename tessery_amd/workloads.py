@@ -352,7 +352,7 @@ def write_pack(directory: str, config: dict[str, Any], tensors: dict[str, tuple[
     import json
     import os
 
-    from .backends import ModelProfile
+    from .packs import ModelProfile
     from .weights import artifact_of, encode_safetensors
 
     config_bytes = json.dumps(config).encode()
