@@ -183,12 +183,15 @@ __device__ __forceinline__ void ranked_plane(uint32_t len, int B, int S, int KV,
 // therefore taken in reverse order (k -> k ^ 31 when the whole run exists), which deals every CU
 // a long and a short item from each pair of runs. serp = 0 (set by the launcher when k / wpp
 // would not be exact by Div) keeps the grid's order.
+// zoff / zcnt: the grid slices [zoff, zoff + zcnt) of z hold the attention items (a launch that
+// also runs another kernel's items in its other slices; zcnt < 0: every slice).
 __device__ __forceinline__ Sched schedule(const uint32_t* lengths, int B, int S, int KV, Div kvdiv,
-                                          Div wppdiv, int serp) {
+                                          Div wppdiv, int serp, int zoff = 0, int zcnt = -1) {
   Sched sc;
   if (sched_ranked(B, KV)) {
-    const int wpp = static_cast<int>(gridDim.y), n = wpp * static_cast<int>(gridDim.z);
-    int y = static_cast<int>(blockIdx.y), z = static_cast<int>(blockIdx.z);
+    const int zs = zcnt < 0 ? static_cast<int>(gridDim.z) : zcnt;
+    const int wpp = static_cast<int>(gridDim.y), n = wpp * zs;
+    int y = static_cast<int>(blockIdx.y), z = static_cast<int>(blockIdx.z) - zoff;
     if (serp) {
       int k = y + wpp * z;
       if (((k >> 5) & 1) && (k | 31) < n) k ^= 31;
@@ -833,6 +836,21 @@ struct F16Lds {
   static constexpr int HALVES = RING > 4 * 16 * RS / 2 ? RING : 4 * 16 * RS / 2;
 };
 
+// The k prologue of another layer (norm_rope_f16 with hi + lo planes, same B, S, KV, D = 128 and
+// lengths) carried by extra workgroups of a fused attention launch: grid slices [z0, z0 + zp) of z
+// hold its workgroups, z0 = 0 (lead) or after the attention slices.
+struct ProArgs {
+  const _Float16* x;      // pre-norm k [B,S,KV,D]
+  _Float16* y;            // hi plane; the lo plane follows at y + plane
+  const uint16_t* gamma;  // bf16 [D]
+  const float* cos;       // [S, D/2]
+  const float* sin;
+  float eps;
+  size_t plane;           // halves per plane, B*S*KV*D
+  int zp;                 // grid slices of prologue workgroups; 0: none
+  int lead;               // 1: the prologue slices come first in dispatch order
+};
+
 struct F16Args {
   const _Float16* q;
   const _Float16* k;
@@ -848,6 +866,7 @@ struct F16Args {
   float eps;
   size_t k_plane;
   F16Shape shp;
+  ProArgs pro;
 };
 
 // One block of one plane: 4 wavefronts x 16 query rows (geometry g), from the q load to the
@@ -1303,12 +1322,90 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
 }
 
 
+// A carried k prologue (ProArgs) is a list of items, each four passes of the norm_rope_f16 thread
+// layout over the valid positions of one batch row: row b holds ceil(L_b / (4 * ppp)) items
+// (ppp = positions per pass), in row order, so the list follows the lengths. The workgroups of
+// the prologue slice take items first, first + stride, ... Each thread runs norm_rope_piece on the
+// same (position, head, lane) data as the standalone kernel, so both planes get the same bits; the
+// loads of an item's four passes go out before the first is used.
+template <int D>
+__device__ __forceinline__ void k_prologue_items(const F16Args& a, int first, int stride) {
+  constexpr int T = D / 16;
+  constexpr int HALF = D / 2;
+  const ProArgs& pr = a.pro;
+  const int B = a.B, S = a.S, KV = a.KV;
+  const int lanes_per_pos = T * KV;  // <= 256, checked by the launcher
+  const int ppp = 256 / lanes_per_pos;
+  const int ppi = 4 * ppp;            // positions per item
+  const int lane = threadIdx.x & 63;
+  const uint32_t len = lane_length(a.lengths, B, S);
+  int incl = lane < B ? (static_cast<int>(len) + ppi - 1) / ppi : 0;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(incl, off);
+    if (lane >= off) incl += t;
+  }
+  const int total = __shfl(incl, 63);
+  const int tid = static_cast<int>(threadIdx.x);
+  const int slot = tid / lanes_per_pos, head = (tid % lanes_per_pos) / T, j = tid % T;
+  if (first >= total || slot >= ppp) return;  // idle threads when lanes_per_pos does not divide 256
+  const uint4v glo = *reinterpret_cast<const uint4v*>(pr.gamma + 8 * j);
+  const uint4v ghi = *reinterpret_cast<const uint4v*>(pr.gamma + HALF + 8 * j);
+  for (int item = first; item < total; item += stride) {  // workgroup-uniform
+    const int b = __popcll(__ballot(incl <= item));  // rows whose items all come before this one
+    const int before = b ? __shfl(incl, b - 1) : 0;
+    const int L = static_cast<int>(__builtin_amdgcn_readlane(len, b));
+    const int p0 = (item - before) * ppi;
+    half8 lo[4], hi[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int pos = p0 + slot + k * ppp;
+      if (pos < L) {
+        const size_t base = ((static_cast<size_t>(b) * S + pos) * KV + head) * D;
+        lo[k] = *reinterpret_cast<const half8*>(pr.x + base + 8 * j);
+        hi[k] = *reinterpret_cast<const half8*>(pr.x + base + HALF + 8 * j);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int pos = p0 + slot + k * ppp;
+      if (pos < L) {
+        const size_t base = ((static_cast<size_t>(b) * S + pos) * KV + head) * D;
+        half8 f1, f2, f1_lo, f2_lo;
+        norm_rope_piece<D>(lo[k], hi[k], glo, ghi, pr.cos + static_cast<size_t>(pos) * HALF + 8 * j,
+                           pr.sin + static_cast<size_t>(pos) * HALF + 8 * j, pr.eps, f1, f2, f1_lo,
+                           f2_lo);
+        *reinterpret_cast<half8*>(pr.y + base + 8 * j) = f1;
+        *reinterpret_cast<half8*>(pr.y + base + HALF + 8 * j) = f2;
+        *reinterpret_cast<half8*>(pr.y + pr.plane + base + 8 * j) = f1_lo;
+        *reinterpret_cast<half8*>(pr.y + pr.plane + base + HALF + 8 * j) = f2_lo;
+      }
+    }
+  }
+}
+
 template <int D, typename TOut, bool FUSED>
 __global__ __launch_bounds__(256, 2) void attn_f16_mfma(F16Args a) {
   __shared__ __attribute__((aligned(1024))) _Float16 ring[F16Lds<D, TOut, FUSED>::HALVES];
   // the wavefront index is uniform; readfirstlane lets the compiler branch on it with scalars
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const Sched sc = schedule(a.lengths, a.B, a.S, a.KV, a.shp.kv, a.shp.wpp, a.shp.serp);
+  int zoff = 0, zcnt = -1;
+  if constexpr (FUSED && D == 128) {
+    if (a.pro.zp) {  // some grid slices carry another layer's k prologue
+      const int z = static_cast<int>(blockIdx.z);
+      zcnt = static_cast<int>(gridDim.z) - a.pro.zp;
+      const int z0 = a.pro.lead ? 0 : zcnt;
+      if (z >= z0 && z < z0 + a.pro.zp) {
+        const int per_slice = 8 * static_cast<int>(gridDim.y);
+        k_prologue_items<D>(a, ((z - z0) * static_cast<int>(gridDim.y) +
+                                static_cast<int>(blockIdx.y)) * 8 + static_cast<int>(blockIdx.x),
+                            a.pro.zp * per_slice);
+        return;
+      }
+      zoff = a.pro.lead ? a.pro.zp : 0;
+    }
+  }
+  const Sched sc = schedule(a.lengths, a.B, a.S, a.KV, a.shp.kv, a.shp.wpp, a.shp.serp, zoff, zcnt);
   f16_block<D, TOut, FUSED>(a, geom16_of(sc, a.bidi, wave, a.shp), ring, wave);
 }
 
@@ -1658,6 +1755,10 @@ __global__ __launch_bounds__(256, 2) void attn_f32x3(X3Args a) {
 // ---------------------------------------------------------------------------------------------
 // Host launchers.
 // ---------------------------------------------------------------------------------------------
+// Where a carried k prologue's items go in dispatch order (see ProArgs): 1 = before the attention
+// items.
+constexpr int kProloguesLead = 1;
+
 static dim3 mfma_grid(int B, int S, int H, int KV) {
   const int G = H / KV;
   const int nrb = G * ((S + 31) / 32);
@@ -1814,8 +1915,15 @@ hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st) {
 
 template <int D, typename TOut, bool FUSED>
 static void launch_f16_kernel(const F16Args& f, hipStream_t st) {
-  attn_f16_mfma<D, TOut, FUSED><<<sched_grid(f.B, f.KV, (f.shp.nwb + 3) / 4), 256, 0, st>>>(f);
+  dim3 grid = sched_grid(f.B, f.KV, (f.shp.nwb + 3) / 4);
+  grid.z += static_cast<unsigned>(f.pro.zp);
+  attn_f16_mfma<D, TOut, FUSED><<<grid, 256, 0, st>>>(f);
 }
+
+// Grid slices of a carried k prologue: each slice is 8 * wpp workgroups (120-128 at S = 464-512)
+// that stride over the items, enough loads in flight to stream the prologue beside the attention
+// items without taking many of their slots.
+constexpr int kPrologueSlices = 1;
 
 template <int D, bool FUSED>
 static void launch_f16_d(const AttnArgs& a, F16Shape shp, float sl2, hipStream_t st) {
@@ -1837,6 +1945,17 @@ static void launch_f16_d(const AttnArgs& a, F16Shape shp, float sl2, hipStream_t
   f.eps = a.eps;
   f.k_plane = static_cast<size_t>(a.B) * a.S * a.KV * a.D;
   f.shp = shp;
+  if (a.pro_x) {
+    f.pro.x = a.pro_x;
+    f.pro.y = a.pro_y;
+    f.pro.gamma = a.pro_gamma;
+    f.pro.cos = a.pro_cos;
+    f.pro.sin = a.pro_sin;
+    f.pro.eps = a.pro_eps;
+    f.pro.plane = f.k_plane;
+    f.pro.zp = kPrologueSlices;
+    f.pro.lead = kProloguesLead;
+  }
   if (a.out_f16)
     launch_f16_kernel<D, _Float16, FUSED>(f, st);
   else
@@ -1859,9 +1978,18 @@ bool attention_f16_fits(int B, int S, int H, int KV, int D) {
          static_cast<uint64_t>(H) * D * 4 * 16 < (1ull << 31);
 }
 
+bool attention_f16_carries_prologue(int B, int S, int H, int KV, int D) {
+  if (!attention_f16_fits(B, S, H, KV, D) || D != 128 || !sched_ranked(B, KV) || 8 * KV > 256)
+    return false;
+  return static_cast<int64_t>(B) * KV / 8 + kPrologueSlices <= 65535;
+}
+
 hipError_t launch_attention_f16(const AttnArgs& a, hipStream_t st) {
   if (!a.B || !a.S || !a.H) return hipSuccess;
   if (!attention_f16_fits(a.B, a.S, a.H, a.KV, a.D)) return hipErrorInvalidValue;
+  if (a.pro_x && (!a.gamma_q || !a.pro_y || !a.pro_gamma || !a.pro_cos || !a.pro_sin ||
+                  !attention_f16_carries_prologue(a.B, a.S, a.H, a.KV, a.D)))
+    return hipErrorInvalidValue;
   F16Shape shp;
   shp.G = a.H / a.KV;
   shp.hsh = __builtin_ctz(static_cast<unsigned>(f16_heads_per_wave(shp.G)));

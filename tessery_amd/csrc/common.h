@@ -42,11 +42,17 @@ __device__ __forceinline__ float silu_times(float g, float u) { return g / (1.0f
 // the row's position, gw_lo / gw_hi hold the bf16 gamma words of its channels. fp32 math; out
 // receives the rotated values rounded to fp16 (first: channels 8j.., second: D/2 + 8j..) and
 // out_lo what that rounding left (hi + lo carry the fp32 value to ~22 bits).
+// Three kernels in three translation units (norm_rope_f16, the qkv4 k-tile epilogue and the
+// attention launch that carries a k prologue) run this function and must give the same bits, so
+// every fused multiply-add is written out, the compiler may contract nothing else, and the rotated
+// values are fp32 before their fp16 rounding: its contraction and fp16-conversion choices
+// otherwise follow the surrounding code and the unit's flags.
 template <int D>
 __device__ __forceinline__ void norm_rope_piece(const half8& lo, const half8& hi, const uint4v& gw_lo,
                                                 const uint4v& gw_hi, const float* cs,
                                                 const float* sn, float eps, half8& first,
                                                 half8& second, half8& first_lo, half8& second_lo) {
+#pragma clang fp contract(off)
   constexpr int T = D / 16;
   const floatx4 c0 = *reinterpret_cast<const floatx4*>(cs);
   const floatx4 c1 = *reinterpret_cast<const floatx4*>(cs + 4);
@@ -58,11 +64,13 @@ __device__ __forceinline__ void norm_rope_piece(const half8& lo, const half8& hi
   for (int m = 0; m < 8; ++m) {
     a[m] = static_cast<float>(lo[m]);
     c[m] = static_cast<float>(hi[m]);
-    ss += a[m] * a[m] + c[m] * c[m];
+    ss = __builtin_fmaf(a[m], a[m], ss);
+    ss = __builtin_fmaf(c[m], c[m], ss);
   }
 #pragma unroll
   for (int off = T / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-  const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+  // 1 / D is exact (D a power of two), so this is ss / D + eps with one rounding
+  const float inv = 1.0f / sqrtf(__builtin_fmaf(ss, 1.0f / static_cast<float>(D), eps));
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
     const int sh = 16 * (m & 1);
@@ -70,7 +78,11 @@ __device__ __forceinline__ void norm_rope_piece(const half8& lo, const half8& hi
     const float wh = bf16_to_float(static_cast<uint16_t>((gw_hi[m >> 1] >> sh) & 0xffffu));
     const float p = a[m] * inv * wl, q = c[m] * inv * wh;
     const float cv = m < 4 ? c0[m] : c1[m - 4], sv = m < 4 ? s0[m] : s1[m - 4];
-    const float r0 = p * cv - q * sv, r1 = p * sv + q * cv;
+    float r0 = __builtin_fmaf(p, cv, -(q * sv)), r1 = __builtin_fmaf(p, sv, q * cv);
+    // r0 and r1 are fp32 values before the fp16 rounding: the compiler would otherwise fold some
+    // of the fma + convert pairs into one v_fma_mix (a single rounding to fp16, a different
+    // result in rare cases), depending on the surrounding code
+    asm("" : "+v"(r0), "+v"(r1));
     first[m] = static_cast<_Float16>(r0);
     second[m] = static_cast<_Float16>(r1);
     first_lo[m] = static_cast<_Float16>(r0 - static_cast<float>(first[m]));

@@ -27,6 +27,15 @@ struct AttnArgs {
   const float* rope_cos;    // [S, D/2]
   const float* rope_sin;    // [S, D/2]
   float eps;
+  // Optional (fused route, D = 128, ranked schedule): the k prologue of another layer, the
+  // norm_rope_f16 that writes hi + lo planes of normalized, rotated keys, with the same B, S, KV
+  // and lengths, run by extra workgroups of the same launch; null when unused.
+  const _Float16* pro_x;      // pre-norm k [B,S,KV,D] fp16
+  _Float16* pro_y;            // hi plane; the lo plane follows (B*S*KV*D halves)
+  const uint16_t* pro_gamma;  // bf16 [D]
+  const float* pro_cos;       // [S, D/2]
+  const float* pro_sin;
+  float pro_eps;
 };
 
 // Shape limits of the attention launchers (grid sizes, 32-bit offsets, exact reciprocal
@@ -34,6 +43,8 @@ struct AttnArgs {
 bool attention_scalar_fits(uint64_t B, uint64_t S, uint64_t H);
 bool attention_f32_fits(int B, int S, int H, int KV);
 bool attention_f16_fits(int B, int S, int H, int KV, int D);
+// Whether a fused-route launch of this shape can carry another layer's k prologue (AttnArgs pro_*).
+bool attention_f16_carries_prologue(int B, int S, int H, int KV, int D);
 
 hipError_t launch_attention_scalar(const AttnArgs& a, hipStream_t st);
 hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st);

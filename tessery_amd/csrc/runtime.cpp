@@ -621,6 +621,38 @@ tessery::Qkv4Args qkv4_args(const Op& op) {
   return a;
 }
 
+// Kernel arguments of an attention-family op (buffers q, k, v, lengths, out [, q_norm]).
+bool attention_args(Runtime* rt, const Op& op, tessery::AttnArgs* out) {
+  const Params& p = op.p;
+  AttnShape s;
+  if (!attn_shape(op.route, p, op.threads, op.group, &s)) return false;
+  tessery::AttnArgs a{};
+  a.q = op.ptr[0];
+  a.k = op.ptr[1];
+  a.v = op.ptr[2];
+  a.lengths = static_cast<const uint32_t*>(op.ptr[3]);
+  a.out = op.ptr[4];
+  a.B = static_cast<int>(s.B);
+  a.S = static_cast<int>(s.S);
+  a.H = static_cast<int>(s.H);
+  a.KV = static_cast<int>(s.KV);
+  a.D = static_cast<int>(s.D);
+  a.scale = p.scale;
+  a.bidi = p.u0 ? 1 : 0;
+  a.in_f16 = s.in_f16;
+  a.out_f16 = s.out_f16;
+  a.eps = p.eps;
+  if (op.route == R_ATTENTION_F16_NORM_ROPE) {
+    const RopeTable* t = rope_of(rt, p);
+    if (!t) return false;
+    a.gamma_q = static_cast<const uint16_t*>(op.ptr[5]);
+    a.rope_cos = t->cos;
+    a.rope_sin = t->sin;
+  }
+  *out = a;
+  return true;
+}
+
 hipError_t launch(Runtime* rt, const Op& op) {
   hipStream_t st = rt->stream;
   const Params& p = op.p;
@@ -632,31 +664,8 @@ hipError_t launch(Runtime* rt, const Op& op) {
     case R_ATTENTION_F16:
     case R_ATTENTION_F16_SCALAR:
     case R_ATTENTION_F16_NORM_ROPE: {
-      AttnShape s;
-      if (!attn_shape(op.route, p, op.threads, op.group, &s)) return hipErrorInvalidValue;
       tessery::AttnArgs a{};
-      a.q = op.ptr[0];
-      a.k = op.ptr[1];
-      a.v = op.ptr[2];
-      a.lengths = static_cast<const uint32_t*>(op.ptr[3]);
-      a.out = op.ptr[4];
-      a.B = static_cast<int>(s.B);
-      a.S = static_cast<int>(s.S);
-      a.H = static_cast<int>(s.H);
-      a.KV = static_cast<int>(s.KV);
-      a.D = static_cast<int>(s.D);
-      a.scale = p.scale;
-      a.bidi = p.u0 ? 1 : 0;
-      a.in_f16 = s.in_f16;
-      a.out_f16 = s.out_f16;
-      a.eps = p.eps;
-      if (op.route == R_ATTENTION_F16_NORM_ROPE) {
-        const RopeTable* t = rope_of(rt, p);
-        if (!t) return hipErrorInvalidValue;
-        a.gamma_q = static_cast<const uint16_t*>(op.ptr[5]);
-        a.rope_cos = t->cos;
-        a.rope_sin = t->sin;
-      }
+      if (!attention_args(rt, op, &a)) return hipErrorInvalidValue;
       if (op.route == R_ATTENTION || op.route == R_ATTENTION_F16_SCALAR)
         return tessery::launch_attention_scalar(a, st);
       if (op.route == R_ATTENTION_F16 || op.route == R_ATTENTION_F16_NORM_ROPE)
@@ -943,7 +952,10 @@ hipError_t launch_fused_dual(Runtime* rt, const Op& a, const Op& b, bool gated);
 //   qkv4_f16, then norm_rope_f16 over its k output (D = 128) -> the projection with the k
 //     prologue in the k tiles' epilogue;
 //   two uint4 projections of the same x with the same shape -> one fp16-MFMA launch
-//     (launch_fused_dual).
+//     (launch_fused_dual);
+//   attention_f16_norm_rope of one layer, then norm_rope_f16 (hi + lo planes) of another over the
+//     same shape and lengths, neither writing a buffer of the other -> the attention launch with
+//     the prologue in extra workgroups.
 // Returns the launch status, or hipErrorNotReady when ops[i], ops[i + 1] are not such a pair.
 hipError_t launch_fused_pair(Runtime* rt, const Op& a, const Op& b) {
   hipStream_t st = rt->stream;
@@ -1001,6 +1013,31 @@ hipError_t launch_fused_pair(Runtime* rt, const Op& a, const Op& b) {
     q.kn_S = static_cast<int>(b.p.seq);
     q.kn_eps = b.p.eps;
     return tessery::launch_qkv4_f16(q, st);
+  }
+  if (a.route == R_ATTENTION_F16_NORM_ROPE && b.route == R_NORM_ROPE_F16 && (b.p.u1 & 1u) &&
+      b.ptr[2] == a.ptr[3]) {
+    // the fused attention of one layer, then the k prologue of another (the next layer's, queued
+    // right after it) over the same lengths and shape, with no buffer of one written by the
+    // other: extra workgroups of the attention launch run the prologue, with its bits
+    tessery::AttnArgs args;
+    if (!attention_args(rt, a, &args) || b.p.dim != static_cast<uint32_t>(args.D) ||
+        b.p.heads != static_cast<uint32_t>(args.KV) || b.p.seq != static_cast<uint32_t>(args.S) ||
+        b.threads != static_cast<uint64_t>(args.B) * args.S ||
+        !tessery::attention_f16_carries_prologue(args.B, args.S, args.H, args.KV, args.D))
+      return hipErrorNotReady;
+    for (int i = 0; i < 6; ++i)
+      if (b.ptr[3] == a.ptr[i]) return hipErrorNotReady;
+    for (int i = 0; i < 3; ++i)
+      if (a.ptr[4] == b.ptr[i]) return hipErrorNotReady;
+    const RopeTable* t = rope_of(rt, b.p);
+    if (!t) return hipErrorNotReady;
+    args.pro_x = static_cast<const _Float16*>(b.ptr[0]);
+    args.pro_y = static_cast<_Float16*>(b.ptr[3]);
+    args.pro_gamma = static_cast<const uint16_t*>(b.ptr[1]);
+    args.pro_cos = t->cos;
+    args.pro_sin = t->sin;
+    args.pro_eps = b.p.eps;
+    return tessery::launch_attention_f16(args, st);
   }
   if (a.route == R_RMS_NORM && b.route == R_ROPE && a.ptr[2] == a.ptr[0] &&
       b.ptr[0] == a.ptr[0] && b.p.dim == a.p.cols &&

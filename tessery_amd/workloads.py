@@ -248,6 +248,13 @@ def attention_bytes(
     return q + kv + o + 4 * shape.batch
 
 
+def k_prologue_bytes(shape: Shape, lengths: NDArray[np.uint32]) -> int:
+    """Compulsory HBM traffic of the fused route's k prologue (norm_rope_f16 with hi + lo planes):
+    valid k rows in as fp16, two fp16 planes out."""
+    valid = int(np.minimum(lengths.astype(np.int64), shape.seq).sum())
+    return valid * shape.kv_heads * shape.dim * (2 + 4)
+
+
 # ---- synthetic weight packs (model.safetensors + config.json of the real model shapes) --------
 
 QWEN3_0P6B = {"hidden": 1024, "intermediate": 3072, "layers": 28, "heads": 16, "kv_heads": 8,

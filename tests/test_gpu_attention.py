@@ -335,6 +335,70 @@ def test_qwen3_32x512_full_length_f16_out(runtime):
     assert err <= fused_bar("f16"), err
 
 
+def layers_in_one_command(engine, layers, lengths, shape, out_dtype, shared_k_work):
+    """Layers queued back to back in one command, each the fused route's k prologue then its
+    attention; k planes per layer (the attention of layer i may then carry layer i + 1's
+    prologue) or one shared k buffer (it may not). Returns outputs, k planes and the number of
+    launch-time pairs that ran."""
+    odt = np.float16 if out_dtype == "f16" else np.float32
+    lens = engine.upload(lengths.astype(np.uint32))
+    sets = []
+    shared = engine.buffer(2 * layers[0]["k"].nbytes)
+    for t in layers:
+        s = {n: engine.upload(t[n]) for n in ("q", "k", "v", "q_norm", "k_norm")}
+        s["out"] = engine.buffer(t["q"].size * np.dtype(odt).itemsize)
+        s["kw"] = shared if shared_k_work else engine.buffer(2 * t["k"].nbytes)
+        sets.append(s)
+    before = engine.diagnostics()["fused_pairs"]
+    b, sq, h, kv, d = shape.batch, shape.seq, shape.heads, shape.kv_heads, shape.dim
+    with engine.command():
+        for s in sets:
+            engine._attention_norm_rope(
+                [s["q"], s["k"], s["v"], lens, s["out"], s["q_norm"], s["k_norm"], s["kw"]],
+                tokens=b * sq, seq=sq, heads=h, kv_heads=kv, dim=d, eps=workloads.EPS,
+                theta=workloads.THETA, out_dtype=out_dtype)
+    fused = engine.diagnostics()["fused_pairs"] - before
+    outs = [engine.read(s["out"], t["q"].shape, odt) for s, t in zip(sets, layers)]
+    planes = [engine.read(s["kw"], (2,) + t["k"].shape, np.float16) for s, t in zip(sets, layers)]
+    return outs, planes, fused
+
+
+@pytest.mark.parametrize("shape,lengths,out_dtype", [
+    (workloads.Shape(8, 464, 16, 8, 128, causal=True), (464, 1, 300, 17, 464, 129, 64, 2), "f32"),
+    (workloads.Shape(8, 256, 16, 8, 128, causal=True), (256, 256, 200, 3, 77, 128, 255, 1), "f16"),
+    (workloads.Shape(16, 72, 8, 2, 128, causal=True), tuple(range(72, 56, -1)), "f32"),
+])
+def test_attention_carries_next_layers_k_prologue(runtime, shape, lengths, out_dtype):
+    """Three layers in one command with a k buffer per layer: attention of layers 0 and 1 carry
+    the k prologues of layers 1 and 2 in extra workgroups of their launches. Outputs and k
+    planes equal those of each layer run in a command of its own, bit for bit, and layer 0 is
+    within the fused route's bar of the float64 oracle."""
+    lengths = np.array(lengths, np.uint32)
+    layers = [workloads.qwen_layer(shape, i, seed=70) for i in range(3)]
+    outs, planes, fused = layers_in_one_command(runtime, layers, lengths, shape, out_dtype, False)
+    assert fused == 2
+    for i, t in enumerate(layers):
+        alone, alone_planes = norm_rope_attend(runtime, t, lengths, shape, out_dtype)
+        np.testing.assert_array_equal(outs[i], alone)
+        for bi, length in enumerate(lengths):  # the prologue writes valid rows only
+            np.testing.assert_array_equal(planes[i][:, bi, :length], alone_planes[:, bi, :length])
+    _, expected = oracle_norm_rope(layers[0], lengths)
+    assert np.max(np.abs(outs[0].astype(np.float64) - expected)) <= fused_bar(out_dtype)
+
+
+def test_shared_k_buffer_is_not_carried(runtime):
+    """With one k buffer for every layer, the next layer's prologue would overwrite the planes
+    the attention still reads: no pair runs, and each layer's result equals its own command's."""
+    shape = workloads.Shape(8, 128, 16, 8, 128, causal=True)
+    lengths = np.array([128, 5, 64, 100, 1, 128, 33, 90], np.uint32)
+    layers = [workloads.qwen_layer(shape, i, seed=71) for i in range(2)]
+    outs, _, fused = layers_in_one_command(runtime, layers, lengths, shape, "f32", True)
+    assert fused == 0
+    for i, t in enumerate(layers):
+        alone, _ = norm_rope_attend(runtime, t, lengths, shape, "f32")
+        np.testing.assert_array_equal(outs[i], alone)
+
+
 @pytest.mark.parametrize("aligned_first", [False, True])
 def test_fused_late_maximum_moves_the_running_max(runtime, aligned_first):
     """Fused route, causal: keys 40-55 line up with every query of head 0 (logit 128 / sqrt(128)
