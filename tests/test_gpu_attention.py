@@ -367,6 +367,9 @@ def layers_in_one_command(engine, layers, lengths, shape, out_dtype, shared_k_wo
     (workloads.Shape(8, 464, 16, 8, 128, causal=True), (464, 1, 300, 17, 464, 129, 64, 2), "f32"),
     (workloads.Shape(8, 256, 16, 8, 128, causal=True), (256, 256, 200, 3, 77, 128, 255, 1), "f16"),
     (workloads.Shape(16, 72, 8, 2, 128, causal=True), tuple(range(72, 56, -1)), "f32"),
+    # the headline shape: blocks run in pairs (more than two rounds of workgroups)
+    (workloads.Shape(32, 464, 16, 8, 128, causal=True),
+     tuple(int(x) for x in workloads.lengths_loguniform(4, 32)), "f32"),
 ])
 def test_attention_carries_next_layers_k_prologue(runtime, shape, lengths, out_dtype):
     """Three layers in one command with a k buffer per layer: attention of layers 0 and 1 carry
