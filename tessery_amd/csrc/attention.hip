@@ -183,15 +183,16 @@ __device__ __forceinline__ void ranked_plane(uint32_t len, int B, int S, int KV,
 // therefore taken in reverse order (k -> k ^ 31 when the whole run exists), which deals every CU
 // a long and a short item from each pair of runs. serp = 0 (set by the launcher when k / wpp
 // would not be exact by Div) keeps the grid's order.
-// zoff / zcnt: the grid slices [zoff, zoff + zcnt) of z hold the attention items (a launch that
-// also runs another kernel's items in its other slices; zcnt < 0: every slice).
+// zat / zcnt: this workgroup's slice among the zcnt slices of z that hold attention items (a
+// launch that also runs another kernel's workgroups in its other slices); zat < 0: blockIdx.z of
+// all gridDim.z slices.
 __device__ __forceinline__ Sched schedule(const uint32_t* lengths, int B, int S, int KV, Div kvdiv,
-                                          Div wppdiv, int serp, int zoff = 0, int zcnt = -1) {
+                                          Div wppdiv, int serp, int zat = -1, int zcnt = -1) {
   Sched sc;
   if (sched_ranked(B, KV)) {
     const int zs = zcnt < 0 ? static_cast<int>(gridDim.z) : zcnt;
     const int wpp = static_cast<int>(gridDim.y), n = wpp * zs;
-    int y = static_cast<int>(blockIdx.y), z = static_cast<int>(blockIdx.z) - zoff;
+    int y = static_cast<int>(blockIdx.y), z = zat < 0 ? static_cast<int>(blockIdx.z) : zat;
     if (serp) {
       int k = y + wpp * z;
       if (((k >> 5) & 1) && (k | 31) < n) k ^= 31;
@@ -838,7 +839,7 @@ struct F16Lds {
 
 // The k prologue of another layer (norm_rope_f16 with hi + lo planes, same B, S, KV, D = 128 and
 // lengths) carried by extra workgroups of a fused attention launch: grid slices [z0, z0 + zp) of z
-// hold its workgroups, z0 = 0 (lead) or after the attention slices.
+// hold its workgroups, the attention items the slices before and after them.
 struct ProArgs {
   const _Float16* x;      // pre-norm k [B,S,KV,D]
   _Float16* y;            // hi plane; the lo plane follows at y + plane
@@ -848,7 +849,7 @@ struct ProArgs {
   float eps;
   size_t plane;           // halves per plane, B*S*KV*D
   int zp;                 // grid slices of prologue workgroups; 0: none
-  int lead;               // 1: the prologue slices come first in dispatch order
+  int z0;                 // first grid slice of the prologue workgroups (dispatch position)
 };
 
 struct F16Args {
@@ -1389,12 +1390,11 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(F16Args a) {
   __shared__ __attribute__((aligned(1024))) _Float16 ring[F16Lds<D, TOut, FUSED>::HALVES];
   // the wavefront index is uniform; readfirstlane lets the compiler branch on it with scalars
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  int zoff = 0, zcnt = -1;
+  int zat = -1, zcnt = -1;
   if constexpr (FUSED && D == 128) {
     if (a.pro.zp) {  // some grid slices carry another layer's k prologue
-      const int z = static_cast<int>(blockIdx.z);
+      const int z = static_cast<int>(blockIdx.z), z0 = a.pro.z0;
       zcnt = static_cast<int>(gridDim.z) - a.pro.zp;
-      const int z0 = a.pro.lead ? 0 : zcnt;
       if (z >= z0 && z < z0 + a.pro.zp) {
         const int per_slice = 8 * static_cast<int>(gridDim.y);
         k_prologue_items<D>(a, ((z - z0) * static_cast<int>(gridDim.y) +
@@ -1402,10 +1402,10 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(F16Args a) {
                             a.pro.zp * per_slice);
         return;
       }
-      zoff = a.pro.lead ? a.pro.zp : 0;
+      zat = z < z0 ? z : z - a.pro.zp;
     }
   }
-  const Sched sc = schedule(a.lengths, a.B, a.S, a.KV, a.shp.kv, a.shp.wpp, a.shp.serp, zoff, zcnt);
+  const Sched sc = schedule(a.lengths, a.B, a.S, a.KV, a.shp.kv, a.shp.wpp, a.shp.serp, zat, zcnt);
   f16_block<D, TOut, FUSED>(a, geom16_of(sc, a.bidi, wave, a.shp), ring, wave);
 }
 
@@ -1755,9 +1755,9 @@ __global__ __launch_bounds__(256, 2) void attn_f32x3(X3Args a) {
 // ---------------------------------------------------------------------------------------------
 // Host launchers.
 // ---------------------------------------------------------------------------------------------
-// Where a carried k prologue's items go in dispatch order (see ProArgs): 1 = before the attention
-// items.
-constexpr int kProloguesLead = 1;
+// Where a carried k prologue's workgroups go in dispatch order (see ProArgs): after this fraction
+// (in 1/8) of the attention slices.
+constexpr int kPrologueAt8 = 0;
 
 static dim3 mfma_grid(int B, int S, int H, int KV) {
   const int G = H / KV;
@@ -1954,7 +1954,7 @@ static void launch_f16_d(const AttnArgs& a, F16Shape shp, float sl2, hipStream_t
     f.pro.eps = a.pro_eps;
     f.pro.plane = f.k_plane;
     f.pro.zp = kPrologueSlices;
-    f.pro.lead = kProloguesLead;
+    f.pro.z0 = a.B * a.KV / 8 * kPrologueAt8 / 8;
   }
   if (a.out_f16)
     launch_f16_kernel<D, _Float16, FUSED>(f, st);
