@@ -313,33 +313,36 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
   stage_barrier();
   flush_bias(groups - (groups - 1) % kBiasChunk - 1, (groups - 1) % kBiasChunk + 1);
 
-  // ---- store y[m][n] = acc as fp16 ----
-  const int n = tile * 128 + col;
+  // ---- y = acc as fp16: the tile goes row-major into the x stages (free since the last group:
+  // the barrier before flush_bias), then every thread stores whole 16-byte pieces of rows ----
+  constexpr int KD = 128, KSTR = KD + 8;  // staged row stride in halves (16 bytes of padding)
+  _Float16* const kst = &xs[0][0];
 #pragma unroll
   for (int k = 0; k < 4; ++k)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int m = m0 + 32 * rtile(k) + 8 * (e >> 2) + 4 * hh + (e & 3);
-      if (m < M) y[static_cast<size_t>(m) * N + n] = static_cast<_Float16>(acc[k][e]);
+      const int row = 32 * rtile(k) + 8 * (e >> 2) + 4 * hh + (e & 3);
+      kst[row * KSTR + col] = static_cast<_Float16>(acc[k][e]);
     }
+  wait_lgkmcnt<0>();
+  stage_barrier();
+  {
+    // thread t stores chunk t % 16 of rows t / 16 + 16 i (i < 8)
+    const int chunk = tid & 15, r0 = tid >> 4;
+    _Float16* const ytile = y + static_cast<size_t>(tile) * KD + 8 * chunk;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = r0 + 16 * i, m = m0 + row;
+      const uint4v v = *reinterpret_cast<const uint4v*>(kst + row * KSTR + 8 * chunk);
+      if (m < M) *reinterpret_cast<uint4v*>(ytile + static_cast<size_t>(m) * N) = v;
+    }
+  }
 
   // ---- k prologue of the attention (k tiles, when asked): the tile is one head of 128
-  // channels. Its fp16 values go row-major into the x stages (free since the last group: the
-  // barrier before flush_bias), then norm_rope_piece runs in norm_rope_f16's lane layout (eight
-  // consecutive lanes per row, 32 rows per pass) on the same fp16 values, so both planes hold the
-  // bits of the separate launch.
+  // channels. norm_rope_piece runs on the staged fp16 values in norm_rope_f16's lane layout
+  // (eight consecutive lanes per row, 32 rows per pass), so both planes hold the bits of the
+  // separate launch.
   if (proj == 1 && a.kn) {  // workgroup-uniform
-    constexpr int KD = 128, KSTR = KD + 8;  // staged row stride in halves (16 bytes of padding)
-    _Float16* const kst = &xs[0][0];
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = 32 * rtile(k) + 8 * (e >> 2) + 4 * hh + (e & 3);
-        kst[row * KSTR + col] = static_cast<_Float16>(acc[k][e]);
-      }
-    wait_lgkmcnt<0>();
-    stage_barrier();
     const int S = a.kn_S, j = tid & 7;
     const size_t plane = static_cast<size_t>(M) * N;
     const uint4v glo = *reinterpret_cast<const uint4v*>(a.kn_gamma + 8 * j);
