@@ -196,8 +196,11 @@ hipError_t launch_l4(const float* x, const uint32_t* w, const uint16_t* scales,
   if constexpr (!GATED) {
     // large batches: fp16 MFMA on row-scaled hi + lo activations (fp32-grade, several times the
     // fp32 MFMA rate)
+    const float* xr = x + static_cast<size_t>(row0) * k;
+    const float* yr = out + static_cast<size_t>(row0) * cols;
     if (rows >= kLinear4HiloRows && cols % 128 == 0 && scratch &&
-        static_cast<size_t>(rows) <= scratch_floats)
+        static_cast<size_t>(rows) <= scratch_floats &&
+        ((reinterpret_cast<uintptr_t>(xr) | reinterpret_cast<uintptr_t>(yr)) & 15) == 0)
       return launch_linear4_hilo_f32(x + static_cast<size_t>(row0) * k, w, scales, biases,
                                      out + static_cast<size_t>(row0) * cols, rows, cols, k,
                                      scratch, scratch_floats, st);

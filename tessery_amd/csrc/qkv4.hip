@@ -649,24 +649,48 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
     flush_bias(last, groups - last);
   }
 
-  // ---- y = acc / 2^e_m, fp32, row-major ----
+  // ---- y = acc / 2^e_m, fp32, row-major: each output tile goes into the x stages (free since
+  // the barrier before the last flush; 64 rows x 128 floats = their 32 KiB), then every thread
+  // stores whole 16-byte pieces of rows. 16-byte chunk c of row r sits at chunk
+  // c ^ 8 ((r >> 2) & 1): the rows r and r + 4 that the two lane halves write together fall in
+  // opposite halves of a bank line. ----
+  float* const ost = reinterpret_cast<float*>(&xs[0][0][0]);
+  auto ochunk = [](int row, int chunk) { return row * 128 + 4 * (chunk ^ (8 * ((row >> 2) & 1))); };
+  float inv[16];  // 1 / rs[m], exact: rs[m] = 2^e_m with |e_m| <= 126, frexp gives e_m + 1
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
-    const int m = m0 + wrow + 8 * (e >> 2) + 4 * hh + (e & 3);
-    if (m < M) {
-      // 1 / rs[m], exact: rs[m] = 2^e_m with |e_m| <= 126, frexp gives e_m + 1
-      const float inv = __builtin_amdgcn_ldexpf(1.0f, 1 - __builtin_amdgcn_frexp_expf(rs[m]));
+    const int m = min(m0 + wrow + 8 * (e >> 2) + 4 * hh + (e & 3), M - 1);
+    inv[e] = __builtin_amdgcn_ldexpf(1.0f, 1 - __builtin_amdgcn_frexp_expf(rs[m]));
+  }
+#pragma unroll
+  for (int out = 0; out < NW; ++out) {
+    if (out) stage_barrier();  // the first output's pieces have been read back
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int row = wrow + 8 * (e >> 2) + 4 * hh + (e & 3);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const size_t at = static_cast<size_t>(m) * N + nw + 32 * j + l32;
+        const int c = wn * 64 + 32 * j + l32;
+        float v;
         if constexpr (DUAL) {
-          const float gate = acc[0][j][e] * inv, up = acc[1][j][e] * inv;
-          y2[at] = up;
-          y[at] = gated ? silu_times(gate, up) : gate;
+          const float gate = acc[0][j][e] * inv[e], up = acc[1][j][e] * inv[e];
+          v = out ? up : (gated ? silu_times(gate, up) : gate);
         } else {
-          y[at] = acc[0][j][e] * inv;
+          v = acc[0][j][e] * inv[e];
         }
+        ost[ochunk(row, c >> 2) + (c & 3)] = v;
       }
+    }
+    wait_lgkmcnt<0>();
+    stage_barrier();
+    float* const dst = out ? y2 : y;
+    const int chunk = tid & 31;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = (tid >> 5) + 8 * i, m = m0 + row;
+      const floatx4 v = *reinterpret_cast<const floatx4*>(ost + ochunk(row, chunk));
+      if (m < M)
+        *reinterpret_cast<floatx4*>(dst + static_cast<size_t>(m) * N + tile * 128 + 4 * chunk) = v;
     }
   }
 }
@@ -677,18 +701,20 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
 // 48 KiB of x / weight stages and row sums two workgroups fit a CU up to K = 4096)
 static size_t hilo_sb_bytes(int K) { return static_cast<size_t>(2 * 128 * 2) * (K / 64); }
 
-static bool hilo_fits(int M, int N, int K, const float* x, const float* scratch,
+// x is read and y written in 16-byte pieces
+static bool hilo_fits(int M, int N, int K, const float* x, const float* y, const float* scratch,
                       size_t scratch_floats) {
   return K > 0 && K % 64 == 0 && N > 0 && N % 128 == 0 && scratch &&
          static_cast<uint64_t>(M) * static_cast<uint64_t>(K) * 4 < (1ull << 32) &&
-         static_cast<size_t>(M) <= scratch_floats && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+         static_cast<size_t>(M) <= scratch_floats &&
+         ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15) == 0;
 }
 
 hipError_t launch_linear4_hilo_f32(const float* x, const uint32_t* w, const uint16_t* scales,
                                    const uint16_t* biases, float* y, int M, int N, int K,
                                    float* scratch, size_t scratch_floats, hipStream_t st) {
   if (M <= 0) return hipSuccess;
-  if (!hilo_fits(M, N, K, x, scratch, scratch_floats) || hilo_sb_bytes(K) > 64 * 1024)
+  if (!hilo_fits(M, N, K, x, y, scratch, scratch_floats) || hilo_sb_bytes(K) > 64 * 1024)
     return hipErrorInvalidValue;
   row_scales_f32<<<(M + 3) / 4, 256, 0, st>>>(x, M, K, scratch);
   dim3 grid((M + 63) / 64, N / 128);
@@ -711,7 +737,8 @@ hipError_t launch_linear4_hilo_dual_f32(const float* x, const uint32_t* w, const
                                         bool gated, int M, int N, int K, float* scratch,
                                         size_t scratch_floats, hipStream_t st) {
   if (M <= 0) return hipSuccess;
-  if (!linear4_hilo_dual_fits(M, N, K) || !hilo_fits(M, N, K, x, scratch, scratch_floats))
+  if (!linear4_hilo_dual_fits(M, N, K) || !hilo_fits(M, N, K, x, y, scratch, scratch_floats) ||
+      (reinterpret_cast<uintptr_t>(u) & 15))
     return hipErrorInvalidValue;
   row_scales_f32<<<(M + 3) / 4, 256, 0, st>>>(x, M, K, scratch);
   dim3 grid((M + 63) / 64, N / 128);
