@@ -407,9 +407,9 @@ __global__ __launch_bounds__(256) void row_scales_f32(const float* __restrict__ 
 // ring).
 constexpr int kHiloChunk = 16;
 
-// 64 x 128 output tile per workgroup, 4 wavefronts in a 2 x 2 grid of 32 x 64 (1 x 2 MFMA tiles
-// of 32 x 32, v_mfma_f32_32x32x16_f16), the A / B k-mapping of qkv4_f16. Per group g, after one
-// barrier:
+// 64 x 128 output tile per workgroup, 4 wavefronts of 64 x 32 (2 x 1 MFMA tiles of 32 x 32,
+// v_mfma_f32_32x32x16_f16; each weight word is decoded once per workgroup), the A / B k-mapping of
+// qkv4_f16. Per group g, after one barrier:
 //   * the MFMAs of group g (hi and lo planes of x from LDS stage g % 2) interleave with the
 //     staging of group g + 1 into the other stage: x * 2^e_m split into hi / lo halves
 //     (hi = fp16(x 2^e), lo = fp16(x 2^e - hi)), stored in the k order of
@@ -450,12 +450,12 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
   extern __shared__ __attribute__((aligned(1024))) uint16_t sbuf[];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  const int wm = wave >> 1, wn = wave & 1;
   const int groups = K / 64;
   const int m0 = blockIdx.x * TM;
   const int tile = blockIdx.y;
-  const int nw = tile * 128 + wn * 64;
-  const int wrow = wm * 32;  // wavefront's rows in the tile
+  // wavefront w owns the tile's columns 32 w .. 32 w + 31 and all 64 rows (two 32-row MFMA
+  // tiles): each weight word is decoded once per workgroup
+  const int col = 32 * wave + l32;  // the lane's column in the tile
 
   // ---- scales and biases of the tile's columns, all groups, transposed into LDS once (before
   // any of this kernel's asm loads: the memory-wait counts below assume none older) ----
@@ -524,39 +524,37 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[set][j][e] = 0.0f;
 
-  // acc[j] += sum_{g in [g0, g0 + count)} bias[n][g] X_g[m] (v_mfma_f32_32x32x2_f32: k-slot
-  // kk = l / 32 of lane l is group g0 + 2 q + kk); operands first, then the MFMAs
+  // acc[i] += sum_{g in [g0, g0 + count)} bias[n][g] X_g[m] for row tile i (v_mfma_f32_32x32x2_f32:
+  // k-slot kk = l / 32 of lane l is group g0 + 2 q + kk); operands first, then the MFMAs
   auto flush_bias = [&](int g0, int count) {
-    float av[kHiloChunk / 2];
+    float av[kHiloChunk / 2][2];
 #pragma unroll
     for (int q2 = 0; q2 < kHiloChunk / 2; ++q2) {
       const int q = 2 * q2 + hh;
       const bool live = q < count;
       const int qc = live ? q : 0;
-      av[q2] = live ? xg_lds[(g0 + qc) % kHiloChunk][wrow + l32] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        av[q2][i] = live ? xg_lds[(g0 + qc) % kHiloChunk][32 * i + l32] : 0.0f;
     }
 #pragma unroll
     for (int set = 0; set < NW; ++set) {
-      float bw[kHiloChunk / 2][2];
+      float bw[kHiloChunk / 2];
       const uint16_t* sb = sbuf + set * 2 * 128 * groups;
 #pragma unroll
       for (int q2 = 0; q2 < kHiloChunk / 2; ++q2) {
         const int q = 2 * q2 + hh;
         const bool live = q < count;
         const int qc = live ? q : 0;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int col = wn * 64 + 32 * j + l32;
-          bw[q2][j] = live ? bf16_to_float(sb[128 * groups + (g0 + qc) * 128 + col]) : 0.0f;
-        }
+        bw[q2] = live ? bf16_to_float(sb[128 * groups + (g0 + qc) * 128 + col]) : 0.0f;
       }
 #pragma unroll
       for (int q2 = 0; q2 < kHiloChunk / 2; ++q2) {
         if (2 * q2 >= count) break;  // wavefront-uniform
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[set][j] =
-              __builtin_amdgcn_mfma_f32_32x32x2f32(av[q2], bw[q2][j], acc[set][j], 0, 0, 0);
+        for (int i = 0; i < 2; ++i)
+          acc[set][i] =
+              __builtin_amdgcn_mfma_f32_32x32x2f32(av[q2][i], bw[q2], acc[set][i], 0, 0, 0);
       }
     }
   };
@@ -592,17 +590,13 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
     rsum += __shfl_xor(rsum, 2);
     if (spart == 0) xg_lds[g % kHiloChunk][srow] = rsum;
 
-    uint4v wd[NW][2];
-    float gs[NW][2];
+    uint4v wd[NW];
+    float gs[NW];
 #pragma unroll
-    for (int set = 0; set < NW; ++set)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int col = wn * 64 + 32 * j + l32;
-        wd[set][j] = *reinterpret_cast<const uint4v*>(
-            &ws[set][st][256 * (2 * wn + j) + 128 * hh + 4 * l32]);
-        gs[set][j] = bf16_to_float(sbuf[set * 2 * 128 * groups + g * 128 + col]);
-      }
+    for (int set = 0; set < NW; ++set) {
+      wd[set] = *reinterpret_cast<const uint4v*>(&ws[set][st][256 * wave + 128 * hh + 4 * l32]);
+      gs[set] = bf16_to_float(sbuf[set * 2 * 128 * groups + g * 128 + col]);
+    }
     // stage group g + 1 from its register set, refill that set with group g + 3, then the
     // weights of group g + 2 into the ring stage group g - 1 used
     xsum = stage_x(par ^ 1, par ^ 1);
@@ -614,21 +608,21 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
       floatx16 p[2];
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
-        const int row = wrow + l32;
-        const int off = row * 64 + 8 * ((4 * hh + s4) ^ xsw(row));
-        const half8 ah = *reinterpret_cast<const half8*>(&xs[par][0][off]);
-        const half8 al = *reinterpret_cast<const half8*>(&xs[par][1][off]);
+        const half8 bq = decode_codes_evenodd(wd[set][s4]);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const half8 bq = decode_codes_evenodd(wd[set][j][s4]);
-          p[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bq, s4 ? p[j] : floatx16{}, 0, 0, 0);
-          p[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bq, p[j], 0, 0, 0);
+        for (int i = 0; i < 2; ++i) {
+          const int row = 32 * i + l32;
+          const int off = row * 64 + 8 * ((4 * hh + s4) ^ xsw(row));
+          const half8 ah = *reinterpret_cast<const half8*>(&xs[par][0][off]);
+          const half8 al = *reinterpret_cast<const half8*>(&xs[par][1][off]);
+          p[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bq, s4 ? p[i] : floatx16{}, 0, 0, 0);
+          p[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bq, p[i], 0, 0, 0);
         }
       }
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[set][j][e] = fmaf(gs[set][j], p[j][e], acc[set][j][e]);
+        for (int e = 0; e < 16; ++e) acc[set][i][e] = fmaf(gs[set], p[i][e], acc[set][i][e]);
     }
   };
   int st = 0;  // g % 3
@@ -656,31 +650,26 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
   // opposite halves of a bank line. ----
   float* const ost = reinterpret_cast<float*>(&xs[0][0][0]);
   auto ochunk = [](int row, int chunk) { return row * 128 + 4 * (chunk ^ (8 * ((row >> 2) & 1))); };
-  float inv[16];  // 1 / rs[m], exact: rs[m] = 2^e_m with |e_m| <= 126, frexp gives e_m + 1
-#pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const int m = min(m0 + wrow + 8 * (e >> 2) + 4 * hh + (e & 3), M - 1);
-    inv[e] = __builtin_amdgcn_ldexpf(1.0f, 1 - __builtin_amdgcn_frexp_expf(rs[m]));
-  }
 #pragma unroll
   for (int out = 0; out < NW; ++out) {
     if (out) stage_barrier();  // the first output's pieces have been read back
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int row = wrow + 8 * (e >> 2) + 4 * hh + (e & 3);
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int c = wn * 64 + 32 * j + l32;
+      for (int e = 0; e < 16; ++e) {
+        const int row = 32 * i + 8 * (e >> 2) + 4 * hh + (e & 3);
+        // 1 / rs[m], exact: rs[m] = 2^e_m with |e_m| <= 126, frexp gives e_m + 1
+        const float inv = __builtin_amdgcn_ldexpf(
+            1.0f, 1 - __builtin_amdgcn_frexp_expf(rs[min(m0 + row, M - 1)]));
         float v;
         if constexpr (DUAL) {
-          const float gate = acc[0][j][e] * inv[e], up = acc[1][j][e] * inv[e];
+          const float gate = acc[0][i][e] * inv, up = acc[1][i][e] * inv;
           v = out ? up : (gated ? silu_times(gate, up) : gate);
         } else {
-          v = acc[0][j][e] * inv[e];
+          v = acc[0][i][e] * inv;
         }
-        ost[ochunk(row, c >> 2) + (c & 3)] = v;
+        ost[ochunk(row, col >> 2) + (col & 3)] = v;
       }
-    }
     wait_lgkmcnt<0>();
     stage_barrier();
     float* const dst = out ? y2 : y;
