@@ -695,6 +695,7 @@ struct F16Shape {
   int G, hsh, nwb;
   Div kv, hbn, wpp;  // KV, G >> hsh (head blocks per position block), workgroups per plane
   int serp;          // serpentine item order on (see schedule)
+  int nwpp;          // workgroups per plane
 };
 
 __device__ __forceinline__ Geom16 geom16_of(const Sched& sc, int bidi, int wave, F16Shape sh) {
@@ -770,6 +771,25 @@ __device__ __forceinline__ void mfma_result_fence(floatx4& a, floatx4& b) {
 // reduce over the four lanes r, r+16, r+32, r+48 that hold one query's scores
 __device__ __forceinline__ float rowmax4(float x) { return pair32(pair16(x, true), true); }
 __device__ __forceinline__ float rowsum4(float x) { return pair32(pair16(x, false), false); }
+
+// lane N of every row of 16 lanes, to each lane of that row (DPP row_newbcast, gfx90a and later)
+template <int N>
+__device__ __forceinline__ float row_bcast(float x) {
+  static_assert(N >= 0 && N < 16, "row lane");
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x150 + N, 0xf, 0xf, false));
+}
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+// f(IntC<0>{}), ..., f(IntC<N - 1>{}): loop indexes usable as DPP controls
+template <int N, typename F>
+__device__ __forceinline__ void for_ct(F&& f) {
+  if constexpr (N > 0) {
+    for_ct<N - 1>(f);
+    f(IntC<N - 1>{});
+  }
+}
 
 // K/V ring geometry. A tile holds KT = 2048 / D keys, so every plane tile (K hi, K lo when fused,
 // V) is 4 KiB: four 1 KiB DMA blocks, one per wavefront. D = 128 runs 16-key tiles, D = 64 runs
@@ -945,19 +965,19 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
   // takes the registers as operands (wait_vmcnt_pin6).
   // tab: gamma [0, NS) (bf16 words, channels 32s + 8g..+7), cos [NS, 2NS), sin [2NS, 3NS) with
   // entry NS + 2s + h holding channels 32s + 8g + 4h..+3.
+  // The 16 lanes of row g need the same 4NS gamma words: lane j of the row loads word j of them
+  // (one dword) and the words reach the row by row broadcasts after the wait.
   floatx4 tab[FUSED ? 3 * NS : 1];
+  float gw = 0.0f;
   if constexpr (FUSED) {
-    const uint32_t goff = static_cast<uint32_t>(16 * gq);
+    const int j = lane & (4 * NS - 1);
+    load4_at<0>(gw, gamma, static_cast<uint32_t>(4 * (16 * (j >> 2) + 4 * gq + (j & 3))));
     const uint32_t toff = static_cast<uint32_t>((qpos_c * (D / 2) + 8 * gq) * 4);
-    load16_at<0>(tab[0], gamma, goff);
-    load16_at<64>(tab[1], gamma, goff);
     load16_at<0>(tab[NS], rope_cos, toff);
     load16_at<16>(tab[NS + 1], rope_cos, toff);
     load16_at<0>(tab[2 * NS], rope_sin, toff);
     load16_at<16>(tab[2 * NS + 1], rope_sin, toff);
     if constexpr (NS == 4) {
-      load16_at<128>(tab[2], gamma, goff);
-      load16_at<192>(tab[3], gamma, goff);
       load16_at<128>(tab[NS + 2], rope_cos, toff);
       load16_at<144>(tab[NS + 3], rope_cos, toff);
       load16_at<128>(tab[2 * NS + 2], rope_sin, toff);
@@ -994,8 +1014,14 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
     float inv = __builtin_amdgcn_rsqf(ss * (1.0f / static_cast<float>(D)) + eps);
     // D = 128: q is carried pre-multiplied by the softmax scale in log2 units (see PRE below)
     if constexpr (KT == 16) inv *= scale_log2;
-    wait_vmcnt_pin6<0>(tab);
-    if constexpr (NS == 4) wait_vmcnt_pin6<0>(tab + 6);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    pin_reg(gw);
+#pragma unroll
+    for (int i = NS; i < 3 * NS; ++i) pin_reg(tab[i]);
+    for_ct<4 * NS>([&](auto wi) {
+      constexpr int w = decltype(wi)::value;
+      tab[w >> 2][w & 3] = row_bcast<w>(gw);
+    });
     uint32_t hv[NS][4], lv[NS][4];  // word m / 2 of step s: channels (m, m + 1) packed
 #pragma unroll
     for (int s = 0; s < NS / 2; ++s)
@@ -1404,6 +1430,11 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(F16Args a) {
       }
       zat = z < z0 ? z : z - a.pro.zp;
     }
+    // The two branches join in the compiled code, and the compiler's wait placement carries the
+    // prologue loop's last loads over into this path as if still in flight: the first asm load
+    // below would get a vmcnt(0) that stalls the q loads behind the K/V DMA. Nothing is in flight
+    // here, so this wait costs nothing and clears that record.
+    wait_vmcnt<0>();
   }
   const Sched sc = schedule(a.lengths, a.B, a.S, a.KV, a.shp.kv, a.shp.wpp, a.shp.serp, zat, zcnt);
   f16_block<D, TOut, FUSED>(a, geom16_of(sc, a.bidi, wave, a.shp), ring, wave);
@@ -1840,8 +1871,9 @@ static F16Shape f16_shape(int B, int S, int H, int KV) {
   shp.nwb = f16_wave_blocks(S, shp.G);
   shp.kv = make_div(static_cast<uint32_t>(KV));
   shp.hbn = make_div(static_cast<uint32_t>(shp.G >> shp.hsh));
-  shp.wpp = make_div(static_cast<uint32_t>((shp.nwb + 3) / 4));
-  shp.serp = serpentine_exact((shp.nwb + 3) / 4, B * KV / 8);
+  shp.nwpp = (shp.nwb + 3) / 4;
+  shp.wpp = make_div(static_cast<uint32_t>(shp.nwpp));
+  shp.serp = serpentine_exact(shp.nwpp, B * KV / 8);
   return shp;
 }
 
@@ -1915,7 +1947,7 @@ hipError_t launch_attention_f32(const AttnArgs& a, hipStream_t st) {
 
 template <int D, typename TOut, bool FUSED>
 static void launch_f16_kernel(const F16Args& f, hipStream_t st) {
-  dim3 grid = sched_grid(f.B, f.KV, (f.shp.nwb + 3) / 4);
+  dim3 grid = sched_grid(f.B, f.KV, f.shp.nwpp);
   grid.z += static_cast<unsigned>(f.pro.zp);
   attn_f16_mfma<D, TOut, FUSED><<<grid, 256, 0, st>>>(f);
 }
@@ -1990,14 +2022,7 @@ hipError_t launch_attention_f16(const AttnArgs& a, hipStream_t st) {
   if (a.pro_x && (!a.gamma_q || !a.pro_y || !a.pro_gamma || !a.pro_cos || !a.pro_sin ||
                   !attention_f16_carries_prologue(a.B, a.S, a.H, a.KV, a.D)))
     return hipErrorInvalidValue;
-  F16Shape shp;
-  shp.G = a.H / a.KV;
-  shp.hsh = __builtin_ctz(static_cast<unsigned>(f16_heads_per_wave(shp.G)));
-  shp.nwb = f16_wave_blocks(a.S, shp.G);
-  shp.kv = make_div(static_cast<uint32_t>(a.KV));
-  shp.hbn = make_div(static_cast<uint32_t>(shp.G >> shp.hsh));
-  shp.wpp = make_div(static_cast<uint32_t>((shp.nwb + 3) / 4));
-  shp.serp = serpentine_exact((shp.nwb + 3) / 4, a.B * a.KV / 8);
+  const F16Shape shp = f16_shape(a.B, a.S, a.H, a.KV);
   const float sl2 = a.scale * kLog2e;
   const bool fused = a.gamma_q != nullptr;
   if (fused && (!a.rope_cos || !a.rope_sin)) return hipErrorInvalidValue;

@@ -93,10 +93,13 @@ __device__ __forceinline__ void norm_rope_piece(const half8& lo, const half8& hi
 // x0 * sc and x1 * sc rounded to fp16 and packed (hi), and the fp16 of what hi leaves of each
 // (lo = fp16(x * sc - hi), the product exact inside the fma): four v_fma_mix instructions. The
 // lo/hi forms write one half of the destination and keep the other, so each packed pair is built
-// in place; hi's halves enter the lo fmas as fp16 operands (op_sel picks the upper half).
+// in place; hi's halves enter the lo fmas as fp16 operands (op_sel picks the upper half). The
+// leading s_nop is the one wait state gfx940 and later require between a transcendental (sc may be
+// a v_rsq result) and a VALU reading its result, which the compiler does not add before inline asm.
 __device__ __forceinline__ void scaled_split2(float x0, float x1, float sc, uint32_t& hi,
                                               uint32_t& lo) {
-  asm("v_fma_mixlo_f16 %0, %2, %4, 0\n\t"
+  asm("s_nop 0\n\t"
+      "v_fma_mixlo_f16 %0, %2, %4, 0\n\t"
       "v_fma_mixhi_f16 %0, %3, %4, 0\n\t"
       "v_fma_mixlo_f16 %1, %2, %4, -%0 op_sel_hi:[0,0,1]\n\t"
       "v_fma_mixhi_f16 %1, %3, %4, -%0 op_sel:[0,0,1] op_sel_hi:[0,0,1]"

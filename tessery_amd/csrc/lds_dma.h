@@ -11,6 +11,14 @@ namespace tessery {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// Wait states inside these asm statements. The compiler's hazard padding does not look into
+// inline asm, and CDNA3/gfx950 require (AMD's CDNA3 ISA guide, "Manually Inserted Wait States"):
+// 5 wait states between a VALU write of an SGPR (v_readlane restoring a spilled SGPR,
+// v_readfirstlane) and a vector memory instruction that reads that SGPR as its base address, and
+// 1 between an SALU write of M0 and an LDS DMA that reads it. Every asm vector memory instruction
+// below is therefore preceded, inside its own statement, by at least 5 wait states (s_nop 4, plus
+// the s_mov to M0 where there is one), whatever the compiler placed before the statement.
+//
 // 16 bytes per lane, global -> LDS (global_load_lds_dwordx4): lane l's bytes land at the
 // wave-uniform LDS address + 16*l. Issued as inline asm so the compiler's wait insertion does not
 // treat the in-flight DMA as aliasing every later LDS read (it would wait for the whole ring);
@@ -18,7 +26,7 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 __device__ __forceinline__ void dma16(const void* src, _Float16* lds) {
   const unsigned addr = __builtin_amdgcn_readfirstlane(
       static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_ptr_t)(lds))));
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, off"
                :
                : "v"(src), "s"(addr)
                : "memory", "m0");
@@ -29,7 +37,7 @@ __device__ __forceinline__ void dma16(const void* src, _Float16* lds) {
 __device__ __forceinline__ void dma16_at(const void* base, uint32_t off, _Float16* lds) {
   const unsigned addr = __builtin_amdgcn_readfirstlane(
       static_cast<unsigned>(reinterpret_cast<uintptr_t>((lds_ptr_t)(lds))));
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1"
                :
                : "v"(off), "s"(base), "s"(addr)
                : "memory", "m0");
@@ -42,10 +50,26 @@ __device__ __forceinline__ void dma16_at(const void* base, uint32_t off, _Float1
 // read of its previous value is ordered before the load (or reads a copy made before it).
 template <int OFF>
 __device__ __forceinline__ void load16_at(floatx4& dst, const void* base, uint32_t off) {
-  asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3"
+  asm volatile("s_nop 4\n\tglobal_load_dwordx4 %0, %1, %2 offset:%3"
                : "+v"(dst)
                : "v"(off), "s"(base), "i"(OFF)
                : "memory");
+}
+
+// 4 bytes per lane, global -> a VGPR, addressed like load16_at.
+template <int OFF>
+__device__ __forceinline__ void load4_at(float& dst, const void* base, uint32_t off) {
+  asm volatile("s_nop 4\n\tglobal_load_dword %0, %1, %2 offset:%3"
+               : "+v"(dst)
+               : "v"(off), "s"(base), "i"(OFF)
+               : "memory");
+}
+
+// The register counts as written here: placed after an s_waitcnt (volatile asm keeps its order
+// with the wait), it orders every later read of an asm-loaded register after that wait.
+template <typename T>
+__device__ __forceinline__ void pin_reg(T& x) {
+  asm volatile("" : "+v"(x));
 }
 
 // s_waitcnt vmcnt(N); the four registers count as written here, so nothing reads them earlier.

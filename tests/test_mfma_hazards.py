@@ -18,15 +18,22 @@ from tessery_amd import _build
 
 CSRC = _build.PACKAGE / "csrc"
 MFMA_SOURCES = ("attention.hip", "qkv4.hip", "linear4.hip", "dense.hip")
+ALL_SOURCES = MFMA_SOURCES + ("norm_rope.hip", "model.hip", "util.hip", "noalloc.hip")
 
 pytestmark = pytest.mark.skipif(shutil.which("hipcc") is None and
                                 not Path("/opt/rocm/bin/hipcc").exists(),
                                 reason="hipcc is needed to build the device assembly")
 
 
-def test_no_mfma_result_read_early_through_a_branch(tmp_path):
-    listings = [mfma_hazards.device_assembly(CSRC / s, tmp_path / (s + ".s")) for s in MFMA_SOURCES]
-    rule, cross, short = mfma_hazards.scan(listings)
+@pytest.fixture(scope="module")
+def assembly(tmp_path_factory):
+    """gfx950 assembly of every device source, built once for the scans below."""
+    out = tmp_path_factory.mktemp("asm")
+    return {s: mfma_hazards.device_assembly(CSRC / s, out / (s + ".s")) for s in ALL_SOURCES}
+
+
+def test_no_mfma_result_read_early_through_a_branch(assembly):
+    rule, cross, short = mfma_hazards.scan([assembly[s] for s in MFMA_SOURCES])
     assert "v_mfma_f32_16x16x32_f16" in rule and "v_mfma_f32_16x16x32_bf16" in rule
     assert len(cross) > 50  # the attention kernels' score reads behind the masking branch
     assert short == [], short[:5]
@@ -44,3 +51,60 @@ def test_scan_finds_the_score_read_without_the_fence(tmp_path):
     _, _, short = mfma_hazards.scan([asm])
     assert any(op == "v_mfma_f32_16x16x32_f16" and t.startswith("v_max_f32")
                for op, _, _, _, _, t in short)
+
+
+def test_inline_asm_reads_no_fresh_valu_result(assembly):
+    """Every inline asm vector memory instruction comes at least 5 wait states after any VALU
+    write of its SGPR base (the persistent attention loop restores spilled SGPRs with v_readlane
+    right before the table loads), and every inline asm VALU instruction at least one after a
+    transcendental whose result it reads, on every path."""
+    assert mfma_hazards.inline_asm_hazards(list(assembly.values())) == []
+
+
+def test_inline_asm_scan_sees_short_distances():
+    """A v_readlane restoring a spilled SGPR base right before an asm table load (the pattern of
+    the memory fault that made the wait states in the asm helpers necessary: the load took a stale
+    base address), and a v_rsq result read by the asm split with no wait state between; with the
+    helpers' wait states in the asm statements, neither is reported."""
+    def listing(nop_vmem, nop_valu):
+        return "\n".join([
+            "_Zk:",
+            "\tv_readlane_b32 s8, v127, 4",
+            "\tv_readlane_b32 s9, v127, 5",
+            "\t;;#ASMSTART",
+            *(["\ts_nop 4"] if nop_vmem else []),
+            "\tglobal_load_dwordx4 v[2:5], v11, s[8:9] offset:0",
+            "\t;;#ASMEND",
+            "\tv_rsq_f32_e32 v6, v6",
+            "\t;;#ASMSTART",
+            *(["\ts_nop 0"] if nop_valu else []),
+            "\tv_fma_mixlo_f16 v7, v8, v6, 0",
+            "\t;;#ASMEND",
+            "\ts_endpgm",
+            ".Lfunc_end0:"])
+    found = mfma_hazards.inline_asm_hazards([listing(False, False)])
+    assert [(t.split()[0], waited, w.split()[0]) for _, t, waited, w in found] == [
+        ("global_load_dwordx4", 0, "v_readlane_b32"), ("v_fma_mixlo_f16", 0, "v_rsq_f32_e32")]
+    assert mfma_hazards.inline_asm_hazards([listing(True, True)]) == []
+
+
+def test_no_instruction_touches_a_register_an_asm_load_is_filling(assembly):
+    """The table, q and activation loads issued as inline asm are invisible to the compiler's wait
+    placement: no instruction may read or overwrite their destination registers (as a spill, a
+    copy or a reuse for another value) before a vmcnt wait has retired them, on any path."""
+    assert mfma_hazards.asm_load_reuse(list(assembly.values())) == []
+
+
+def test_asm_load_scan_sees_an_early_read():
+    listing = "\n".join([
+        "_Zk:",
+        "\t;;#ASMSTART",
+        "\tglobal_load_dwordx4 v[6:9], v1, s[2:3] offset:0",
+        "\t;;#ASMEND",
+        "\tglobal_load_dword v20, v[2:3], off",
+        "\ts_waitcnt vmcnt({n})",
+        "\tv_add_f32_e32 v10, v6, v7",
+        "\ts_endpgm",
+        ".Lfunc_end0:"])
+    assert mfma_hazards.asm_load_reuse([listing.format(n=1)]) == []
+    assert mfma_hazards.asm_load_reuse([listing.format(n=2)]) == [("_Zk", "v_add_f32_e32 v10, v6, v7")]
