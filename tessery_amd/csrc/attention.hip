@@ -778,6 +778,12 @@ __device__ __forceinline__ float row_bcast(float x) {
   static_assert(N >= 0 && N < 16, "row lane");
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x150 + N, 0xf, 0xf, false));
 }
+// the even (ODD = false) or odd lane of every lane pair, to both lanes of the pair (DPP quad_perm
+// [0, 0, 2, 2] / [1, 1, 3, 3])
+template <bool ODD>
+__device__ __forceinline__ float pair_bcast(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), ODD ? 0xF5 : 0xA0, 0xf, 0xf, false));
+}
 template <int V>
 struct IntC {
   static constexpr int value = V;
@@ -961,27 +967,43 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
   // per position; channel c < D/2 of step s is 32s + 8g + j, j < 8: two 16-byte chunks) go out
   // first, as asm loads: the compiler would otherwise sink them past the q-dependent row sum into
   // the tile loop's entry block, putting an L2 round trip behind the q load. The compiler does
-  // not know they are in flight, so their first use is ordered after an explicit vmcnt(0) that
-  // takes the registers as operands (wait_vmcnt_pin6).
+  // not know they are in flight, so their first use is ordered after an explicit vmcnt(0), and
+  // each register counts as written after it (pin_reg).
   // tab: gamma [0, NS) (bf16 words, channels 32s + 8g..+7), cos [NS, 2NS), sin [2NS, 3NS) with
-  // entry NS + 2s + h holding channels 32s + 8g + 4h..+3.
+  // entry NS + c, c = 2s + h, holding channels 32s + 8g + 4h..+3 (chunk c, 16 bytes at 128s + 16h
+  // into the lane's row of the table).
   // The 16 lanes of row g need the same 4NS gamma words: lane j of the row loads word j of them
-  // (one dword) and the words reach the row by row broadcasts after the wait.
+  // (one dword) and the words reach the row by row broadcasts after the wait. With two or more
+  // heads per wavefront the two lanes of a pair (rows 2p, 2p + 1) hold one position: the even lane
+  // loads chunks 0..NS/2 - 1 of cos and sin, the odd lane the rest, and pair broadcasts hand them
+  // round (half the table loads); otherwise every lane loads its own NS chunks of each table.
   floatx4 tab[FUSED ? 3 * NS : 1];
   float gw = 0.0f;
+  floatx4 pc[FUSED ? NS / 2 : 1], ps[FUSED ? NS / 2 : 1];
+  const bool pair = g.hsh >= 1;
   if constexpr (FUSED) {
     const int j = lane & (4 * NS - 1);
     load4_at<0>(gw, gamma, static_cast<uint32_t>(4 * (16 * (j >> 2) + 4 * gq + (j & 3))));
     const uint32_t toff = static_cast<uint32_t>((qpos_c * (D / 2) + 8 * gq) * 4);
-    load16_at<0>(tab[NS], rope_cos, toff);
-    load16_at<16>(tab[NS + 1], rope_cos, toff);
-    load16_at<0>(tab[2 * NS], rope_sin, toff);
-    load16_at<16>(tab[2 * NS + 1], rope_sin, toff);
-    if constexpr (NS == 4) {
-      load16_at<128>(tab[NS + 2], rope_cos, toff);
-      load16_at<144>(tab[NS + 3], rope_cos, toff);
-      load16_at<128>(tab[2 * NS + 2], rope_sin, toff);
-      load16_at<144>(tab[2 * NS + 3], rope_sin, toff);
+    if (pair) {
+      const uint32_t poff = toff + static_cast<uint32_t>((NS == 4 ? 128 : 16) * (lane & 1));
+      load16_at<0>(pc[0], rope_cos, poff);
+      load16_at<0>(ps[0], rope_sin, poff);
+      if constexpr (NS == 4) {
+        load16_at<16>(pc[1], rope_cos, poff);
+        load16_at<16>(ps[1], rope_sin, poff);
+      }
+    } else {
+      load16_at<0>(tab[NS], rope_cos, toff);
+      load16_at<16>(tab[NS + 1], rope_cos, toff);
+      load16_at<0>(tab[2 * NS], rope_sin, toff);
+      load16_at<16>(tab[2 * NS + 1], rope_sin, toff);
+      if constexpr (NS == 4) {
+        load16_at<128>(tab[NS + 2], rope_cos, toff);
+        load16_at<144>(tab[NS + 3], rope_cos, toff);
+        load16_at<128>(tab[2 * NS + 2], rope_sin, toff);
+        load16_at<144>(tab[2 * NS + 3], rope_sin, toff);
+      }
     }
   }
   // q rows of one batch row lie within S * H * D halves (below 2^31 bytes, checked by the
@@ -1016,8 +1038,24 @@ __device__ __forceinline__ void f16_block(const F16Args& a, const Geom16& g, _Fl
     if constexpr (KT == 16) inv *= scale_log2;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     pin_reg(gw);
+    if (pair) {
 #pragma unroll
-    for (int i = NS; i < 3 * NS; ++i) pin_reg(tab[i]);
+      for (int i = 0; i < NS / 2; ++i) {
+        pin_reg(pc[i]);
+        pin_reg(ps[i]);
+      }
+#pragma unroll
+      for (int c = 0; c < NS; ++c)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const int i = c % (NS / 2);
+          tab[NS + c][d] = c < NS / 2 ? pair_bcast<false>(pc[i][d]) : pair_bcast<true>(pc[i][d]);
+          tab[2 * NS + c][d] = c < NS / 2 ? pair_bcast<false>(ps[i][d]) : pair_bcast<true>(ps[i][d]);
+        }
+    } else {
+#pragma unroll
+      for (int i = NS; i < 3 * NS; ++i) pin_reg(tab[i]);
+    }
     for_ct<4 * NS>([&](auto wi) {
       constexpr int w = decltype(wi)::value;
       tab[w >> 2][w & 3] = row_bcast<w>(gw);
