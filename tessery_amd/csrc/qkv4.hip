@@ -90,6 +90,14 @@ __device__ __forceinline__ float word_value(uint16_t w) {
 
 __device__ __forceinline__ int xsw(int row) { return (row >> 1) & 7; }
 
+// The x-stage chunk swizzle of linear4_hilo, whose threads write the stage themselves (ds_write_b128)
+// where qkv4_f16's DMA writes whole rows. Measured on gfx950: ds_read_b128 serves 16 lanes per
+// cycle over 64 banks (256 bytes), ds_write_b128 8 lanes per cycle over a 128-byte bank window.
+// A write instruction covers rows 2k and 2k + 1 (four lanes each, chunks 2p + c) in one 8-lane
+// group, and both rows start on the same 128-byte bank window: the odd row takes the other chunk
+// parity (^ (row & 1)). The 16 rows of a read group keep distinct chunks per row parity.
+__device__ __forceinline__ int xsw_pair(int row) { return ((row >> 1) & 7) ^ (row & 1); }
+
 // Scale and bias words of a 128-column tile, all groups, into LDS transposed to
 // [part][group][column] (part 0 scales, 1 biases): the lanes of a column block then read one
 // group's words from consecutive addresses (in the global [N, groups] layout they are `groups`
@@ -498,7 +506,7 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
         for (int t = 0; t < 2; ++t)
           scaled_split2(xr[set][2 * c + h][t], xr[set][2 * c + h][t + 2], rscale, hw[2 * t + h],
                         lw[2 * t + h]);
-      const int pos = srow * 64 + 8 * ((2 * spart + c) ^ xsw(srow));
+      const int pos = srow * 64 + 8 * ((2 * spart + c) ^ xsw_pair(srow));
       *reinterpret_cast<uint4v*>(&xs[st][0][pos]) = uint4v{hw[0], hw[1], hw[2], hw[3]};
       *reinterpret_cast<uint4v*>(&xs[st][1][pos]) = uint4v{lw[0], lw[1], lw[2], lw[3]};
     }
@@ -612,7 +620,7 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const int row = 32 * i + l32;
-          const int off = row * 64 + 8 * ((4 * hh + s4) ^ xsw(row));
+          const int off = row * 64 + 8 * ((4 * hh + s4) ^ xsw_pair(row));
           const half8 ah = *reinterpret_cast<const half8*>(&xs[par][0][off]);
           const half8 al = *reinterpret_cast<const half8*>(&xs[par][1][off]);
           p[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bq, s4 ? p[i] : floatx16{}, 0, 0, 0);

@@ -191,7 +191,7 @@ def _writer_within(ins, preds, i, need, is_writer):
             stack.extend((p, waited) for p in preds[k])
             continue
         op, _, operands = t.partition(" ")
-        if is_writer(op, operands):
+        if is_writer(op, operands, ins[k][1]):
             found.append((waited, t))
             continue
         step = int(operands) + 1 if op == "s_nop" else 1
@@ -200,23 +200,34 @@ def _writer_within(ins, preds, i, need, is_writer):
 
 
 def inline_asm_hazards(listings: list[str]):
-    """(kernel, asm instruction, wait states, writer) for every asm vector memory instruction
-    whose SGPR operands a VALU wrote fewer than 5 wait states before, and every asm VALU
-    instruction reading a transcendental's result with no wait state between."""
+    """(kernel, instruction, wait states, writer) for every asm vector memory instruction whose
+    SGPR operands a VALU wrote fewer than 5 wait states before, every asm VALU instruction reading
+    a transcendental's result with no wait state between, and every MFMA reading a VGPR that an
+    asm VALU instruction wrote fewer than 2 wait states before (the compiler pads neither the
+    asm's reads nor the reads of what the asm wrote)."""
     out = []
     for asm in listings:
         for name, ins in functions_with_asm(asm).items():
             preds = _predecessors(ins)
             for i, (t, inside) in enumerate(ins):
-                if not inside:
-                    continue
                 op, _, operands = t.partition(" ")
+                if not inside:
+                    if op.startswith("v_mfma"):
+                        msrc = regs(operands.partition(",")[2])
+
+                        def asm_valu_writer(wop, wops, winside, msrc=msrc):
+                            return (winside and wop.startswith("v_") and
+                                    bool(regs(wops.split(",")[0]) & msrc))
+
+                        for waited, w in _writer_within(ins, preds, i, 2, asm_valu_writer):
+                            out.append((name, t, waited, w))
+                    continue
                 if op.startswith(_VMEM):
                     srcs = sregs(operands)
                     if not srcs:
                         continue
 
-                    def sgpr_writer(wop, wops, srcs=srcs):
+                    def sgpr_writer(wop, wops, _winside, srcs=srcs):
                         if not wop.startswith("v_"):
                             return False
                         return bool(sregs(wops.split(",")[0]) & srcs)
@@ -226,7 +237,7 @@ def inline_asm_hazards(listings: list[str]):
                 elif op.startswith("v_"):
                     vsrc = regs(operands.partition(",")[2])
 
-                    def trans_writer(wop, wops, vsrc=vsrc):
+                    def trans_writer(wop, wops, _winside, vsrc=vsrc):
                         return wop.startswith(_TRANS) and bool(regs(wops.split(",")[0]) & vsrc)
 
                     for waited, w in _writer_within(ins, preds, i, 1, trans_writer):

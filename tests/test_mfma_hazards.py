@@ -88,6 +88,25 @@ def test_inline_asm_scan_sees_short_distances():
     assert mfma_hazards.inline_asm_hazards([listing(True, True)]) == []
 
 
+def test_inline_asm_scan_sees_an_mfma_reading_an_asm_result():
+    """An MFMA reading a V fragment that an asm v_mov_b64 copied the instruction before: the
+    compiler adds no wait state after an asm statement, so the statement carries its own two."""
+    def listing(nop):
+        return "\n".join([
+            "_Zk:",
+            "\t;;#ASMSTART",
+            "\tv_mov_b64 v[100:101], v[98:99]",
+            *(["\ts_nop 1"] if nop else []),
+            "\t;;#ASMEND",
+            "\tv_mfma_f32_16x16x32_f16 v[62:65], v[98:101], v[72:75], v[62:65]",
+            "\ts_endpgm",
+            ".Lfunc_end0:"])
+    found = mfma_hazards.inline_asm_hazards([listing(False)])
+    assert [(t.split()[0], waited, w.split()[0]) for _, t, waited, w in found] == [
+        ("v_mfma_f32_16x16x32_f16", 0, "v_mov_b64")]
+    assert mfma_hazards.inline_asm_hazards([listing(True)]) == []
+
+
 def test_no_instruction_touches_a_register_an_asm_load_is_filling(assembly):
     """The table, q and activation loads issued as inline asm are invisible to the compiler's wait
     placement: no instruction may read or overwrite their destination registers (as a spill, a
