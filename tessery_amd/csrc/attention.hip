@@ -1540,9 +1540,13 @@ __device__ __forceinline__ shortx4 lds_read_tr_s(const uint16_t* p) {
 // lanes at a time) take 32 bytes from each of 8 consecutive rows, which must land in the eight
 // 32-byte bank groups: the 32-byte unit is XORed with the row's position among the rows that
 // share its bank-line offset.
+// D = 32 (64-byte rows): the line-index XOR, (row / 4) & 3, still cost a 2-way conflict per
+// score read on gfx950 (measured with the bank counter on this exact pattern); pairs of rows
+// sharing a chunk, (row / 2) & 3, are conflict-free for these reads and for the split writes.
 template <int D>
 __device__ __forceinline__ int ksw_x3(int row) {
   constexpr int CPR = D / 8, RPL = 16 / CPR;
+  if constexpr (D == 32) return (row >> 1) & 3;
   return (row / RPL) & (CPR - 1);
 }
 template <int D>
