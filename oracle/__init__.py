@@ -1,7 +1,7 @@
 """CPU oracle of tessery's prefill-attention path (float64 NumPy).
 
 TEST INFRASTRUCTURE ONLY. It is imported by tests/, by __graft_entry__.smoke() and by bench.py's
-CPU-baseline leg, and only as the checker or the timed CPU baseline. The product path
+CPU-baseline leg, and only as the reference results or the timed CPU baseline. The product path
 (tessery_amd) never imports, calls or falls back to it.
 
 Modules and what pins each one (the tests under tests/test_oracle_*.py run these checks):
