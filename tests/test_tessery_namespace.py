@@ -1,4 +1,4 @@
-"""The `tessery` namespace re-exports this build's implementation under tessery's names
+"""The `tessery` namespace re-exports tessery_amd's implementation under tessery's names
 (src/tessery/__init__.py:1-42, src/metal_inference module names), with no device touched."""
 
 import tessery
