@@ -533,7 +533,8 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
       for (int e = 0; e < 16; ++e) acc[set][j][e] = 0.0f;
 
   // acc[i] += sum_{g in [g0, g0 + count)} bias[n][g] X_g[m] for row tile i (v_mfma_f32_32x32x2_f32:
-  // k-slot kk = l / 32 of lane l is group g0 + 2 q + kk); operands first, then the MFMAs
+  // k-slot kk = l / 32 of lane l is group g0 + 2 q + kk); operands first, then the MFMAs. g0 is a
+  // multiple of kHiloChunk, so group g0 + q sits in row q of the row-sum ring.
   auto flush_bias = [&](int g0, int count) {
     float av[kHiloChunk / 2][2];
 #pragma unroll
@@ -543,7 +544,7 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
       const int qc = live ? q : 0;
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        av[q2][i] = live ? xg_lds[(g0 + qc) % kHiloChunk][32 * i + l32] : 0.0f;
+        av[q2][i] = live ? xg_lds[qc][32 * i + l32] : 0.0f;
     }
 #pragma unroll
     for (int set = 0; set < NW; ++set) {
