@@ -1502,30 +1502,8 @@ __global__ __launch_bounds__(256, 2) void attn_f16_mfma(F16Args a) {
 // same four keys:
 // [p1,p1]x[v1,v2], [p2,p2]x[v1,v2], [p1,p3]x[v3,v1].
 // ---------------------------------------------------------------------------------------------
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short shortx4 __attribute__((ext_vector_type(4)));
 typedef short shortx8 __attribute__((ext_vector_type(8)));
-
-// x[0..7] -> three packed bf16x8 words (channel pairs (2m, 2m + 1) in word m)
-__device__ __forceinline__ void split3x8(const floatx4& x0, const floatx4& x1, uint4v& p1,
-                                         uint4v& p2, uint4v& p3) {
-  uint32_t u0[8], u1[8], u2[8];
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    const float x = m < 4 ? x0[m] : x1[m - 4];
-    u0[m] = __float_as_uint(x);
-    const float r1 = x - __uint_as_float(u0[m] & 0xffff0000u);
-    u1[m] = __float_as_uint(r1);
-    u2[m] = __float_as_uint(r1 - __uint_as_float(u1[m] & 0xffff0000u));
-  }
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    // upper halves of words 2w (result bits 0-15) and 2w + 1 (bits 16-31)
-    p1[w] = __builtin_amdgcn_perm(u0[2 * w + 1], u0[2 * w], 0x07060302u);
-    p2[w] = __builtin_amdgcn_perm(u1[2 * w + 1], u1[2 * w], 0x07060302u);
-    p3[w] = __builtin_amdgcn_perm(u2[2 * w + 1], u2[2 * w], 0x07060302u);
-  }
-}
 
 // 8 bytes of a row-major bf16 V plane, transposed across each 16-lane group (as lds_read_tr)
 __device__ __forceinline__ shortx4 lds_read_tr_s(const uint16_t* p) {

@@ -25,6 +25,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float float2v __attribute__((ext_vector_type(2)));
 typedef uint32_t uint4v __attribute__((ext_vector_type(4)));
 typedef uint32_t uint2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 // BF16 storage word -> float (exact): tessery stores norm weights and uint4 scales/biases
 // as bfloat16 words (kernels.metal:10).
@@ -124,5 +125,32 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 // log2(e) for exp2-based softmax.
 constexpr float kLog2e = 1.4426950408889634f;
+
+// An fp32 value splits exactly into three bf16 terms by truncation: b1 = the upper half of x's
+// bits, r1 = x - b1 (exact), b2 = the upper half of r1, b3 = r1 - b2 (at most 8 significant bits,
+// so exactly a bf16). bf16 keeps fp32's exponent range, so no scaling is needed; a product x * y
+// is taken as the six terms b_i c_j with i + j <= 4 (the three dropped ones are below 2^-24 |x y|)
+// and every bf16 product is exact in fp32.
+// x[0..7] -> three packed bf16x8 words (channel pairs (2m, 2m + 1) in word m)
+__device__ __forceinline__ void split3x8(const floatx4& x0, const floatx4& x1, uint4v& p1,
+                                         uint4v& p2, uint4v& p3) {
+  uint32_t u0[8], u1[8], u2[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const float x = m < 4 ? x0[m] : x1[m - 4];
+    u0[m] = __float_as_uint(x);
+    const float r1 = x - __uint_as_float(u0[m] & 0xffff0000u);
+    u1[m] = __float_as_uint(r1);
+    u2[m] = __float_as_uint(r1 - __uint_as_float(u1[m] & 0xffff0000u));
+  }
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    // upper halves of words 2w (result bits 0-15) and 2w + 1 (bits 16-31)
+    p1[w] = __builtin_amdgcn_perm(u0[2 * w + 1], u0[2 * w], 0x07060302u);
+    p2[w] = __builtin_amdgcn_perm(u1[2 * w + 1], u1[2 * w], 0x07060302u);
+    p3[w] = __builtin_amdgcn_perm(u2[2 * w + 1], u2[2 * w], 0x07060302u);
+  }
+}
+
 
 }  // namespace tessery

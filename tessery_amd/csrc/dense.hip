@@ -150,6 +150,135 @@ __global__ __launch_bounds__(256) void matmul_f32(const float* __restrict__ a,
     }
 }
 
+// matmul_x3<BIAS, GELU>: the same product on bf16 MFMA for large shapes (K % 32 == 0, N % 128
+// == 0, at least 256 tiles): a and bt are split exactly into three bf16 planes each (split3x8)
+// and every fp32 product is taken as the six terms b_i c_j with i + j <= 4 on
+// v_mfma_f32_32x32x16_bf16 in fp32 (the bf16 rate is 16x the fp32 one, so six products cost well
+// under half the fp32 instructions). Tile 64 rows x 128 columns; wavefront w
+// owns rows 32 (w >> 1) .. +31 and columns 64 (w & 1) .. +63 (two 32x32 tiles). Per 32-wide K
+// chunk every thread loads 8 floats of one x row and 16 of one weight row into registers (one
+// chunk ahead), splits them after the barrier that retires the previous chunk's reads, and
+// stores the three planes to LDS as rows of 64 bytes (four 16-byte chunks, chunk c of row r at
+// c ^ ((r >> 1) & 3): conflict-free for the 16-lane reads and the 8-lane writes on gfx950). As in
+// matmul_f32, each 32-wide chunk's products form a partial sum added to the total (the chunk32
+// order), and the bias and GELU are applied the same way. Rows past row1 read row0 and are never
+// stored.
+constexpr int kX3Rows = 64;
+
+__device__ __forceinline__ int x3sw(int row) { return (row >> 1) & 3; }
+
+// PARTIAL: as in matmul_f32, workgroup z sums K chunks [z * per, (z + 1) * per) (of 32 here) and
+// stores its raw sums for dense_reduce.
+template <bool BIAS, bool GELU, bool PARTIAL>
+__global__ __launch_bounds__(256, 3) void matmul_x3(const float* __restrict__ a,
+                                                   const float* __restrict__ bt,
+                                                   const float* __restrict__ bias,
+                                                   float* __restrict__ out, int row0, int row1,
+                                                   int cols, int k, int per) {
+  __shared__ __attribute__((aligned(16))) uint16_t as[3][kX3Rows * 32];
+  __shared__ __attribute__((aligned(16))) uint16_t bs[3][128 * 32];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int wr = wave >> 1, wc = wave & 1;
+  const int rbase = row0 + blockIdx.x * kX3Rows;
+  const int nbase = blockIdx.y * 128;
+  // load roles: x row tid / 4, floats 8 (tid % 4) .. +7 of the chunk; weight row tid / 2,
+  // floats 16 (tid % 2) .. +15
+  const int arow = tid >> 2, apart = tid & 3;
+  const int brow = tid >> 1, bpart = tid & 1;
+  const int agrow = rbase + arow < row1 ? rbase + arow : row0;
+  const float* const asrc = a + static_cast<size_t>(agrow) * k + 8 * apart;
+  const float* const bsrc = bt + static_cast<size_t>(nbase + brow) * k + 16 * bpart;
+  floatx4 ar[2], br[4];
+  auto load = [&](int k0) {
+    ar[0] = *reinterpret_cast<const floatx4*>(asrc + k0);
+    ar[1] = *reinterpret_cast<const floatx4*>(asrc + k0 + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) br[j] = *reinterpret_cast<const floatx4*>(bsrc + k0 + 4 * j);
+  };
+  const int aslot = arow * 32 + 8 * (apart ^ x3sw(arow));
+  const int bslot0 = brow * 32 + 8 * ((2 * bpart) ^ x3sw(brow));
+  const int bslot1 = brow * 32 + 8 * ((2 * bpart + 1) ^ x3sw(brow));
+  // operand rows of this lane: x row 32 wr + l32, weight rows 64 wc + 32 j + l32
+  const int orow = 32 * wr + l32;
+  floatx16 acc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[j][e] = 0.0f;
+  const int k_begin = PARTIAL ? static_cast<int>(blockIdx.z) * per * 32 : 0;
+  const int k_end = PARTIAL ? min(k_begin + per * 32, k) : k;
+  load(k_begin);
+  for (int k0 = k_begin; k0 < k_end; k0 += 32) {
+    {
+      uint4v p1, p2, p3;
+      split3x8(ar[0], ar[1], p1, p2, p3);
+      *reinterpret_cast<uint4v*>(&as[0][aslot]) = p1;
+      *reinterpret_cast<uint4v*>(&as[1][aslot]) = p2;
+      *reinterpret_cast<uint4v*>(&as[2][aslot]) = p3;
+      split3x8(br[0], br[1], p1, p2, p3);
+      *reinterpret_cast<uint4v*>(&bs[0][bslot0]) = p1;
+      *reinterpret_cast<uint4v*>(&bs[1][bslot0]) = p2;
+      *reinterpret_cast<uint4v*>(&bs[2][bslot0]) = p3;
+      split3x8(br[2], br[3], p1, p2, p3);
+      *reinterpret_cast<uint4v*>(&bs[0][bslot1]) = p1;
+      *reinterpret_cast<uint4v*>(&bs[1][bslot1]) = p2;
+      *reinterpret_cast<uint4v*>(&bs[2][bslot1]) = p3;
+    }
+    __syncthreads();  // this chunk's planes are in LDS
+    if (k0 + 32 < k_end) load(k0 + 32);
+    // the chunk's 32-wide partial sum of each tile, then added to its total (the chunk32 order)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int wrow = 64 * wc + 32 * j + l32;
+      floatx16 c;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) c[e] = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int chunk = 2 * ks + hh;
+        const int ao = orow * 32 + 8 * (chunk ^ x3sw(orow));
+        const int bo = wrow * 32 + 8 * (chunk ^ x3sw(wrow));
+        const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(&as[0][ao]);
+        const bf16x8 a2 = *reinterpret_cast<const bf16x8*>(&as[1][ao]);
+        const bf16x8 a3 = *reinterpret_cast<const bf16x8*>(&as[2][ao]);
+        const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(&bs[0][bo]);
+        const bf16x8 b2 = *reinterpret_cast<const bf16x8*>(&bs[1][bo]);
+        const bf16x8 b3 = *reinterpret_cast<const bf16x8*>(&bs[2][bo]);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a3, b1, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b2, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b3, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b1, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b2, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, c, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[j][e] += c[e];
+    }
+    __syncthreads();  // every wavefront has read this chunk's planes
+  }
+  // rows of a partial are counted from row0
+  float* const dst = PARTIAL ? out + static_cast<size_t>(blockIdx.z) * (row1 - row0) * cols : out;
+  const int rfirst = PARTIAL ? row0 : 0;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = nbase + 64 * wc + 32 * j + l32;
+    const float b = BIAS ? bias[n] : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int r = rbase + 32 * wr + 8 * (e >> 2) + 4 * hh + (e & 3);
+      if (r < row1) {
+        const size_t at = static_cast<size_t>(r - rfirst) * cols + n;
+        if constexpr (PARTIAL) {
+          dst[at] = acc[j][e];
+        } else {
+          const float y = BIAS ? acc[j][e] + b : acc[j][e];
+          dst[at] = GELU ? gelu_value(y) : y;
+        }
+      }
+    }
+  }
+}
+
 // Split-K epilogue: out[r][n] = sum over z in order of part[z][r - row0][n] (+ bias, GELU).
 template <bool BIAS, bool GELU>
 __global__ __launch_bounds__(256) void dense_reduce(const float* __restrict__ part,
@@ -225,12 +354,68 @@ int dense_splits(int rows, int cols, int k, size_t scratch_floats) {
   return splits;
 }
 
+// Workgroups along K for the split-bf16 kernel: 1 from 512 tiles of 64 x 128; from 64 tiles, enough
+// splits of at least two 32-wide chunks for about 768 workgroups when the partial sums fit the
+// scratch; 0 (the fp32 kernel) otherwise. Every split holds at least one chunk.
+static int x3_split_count(int rows, int cols, int k, int tiles, size_t scratch_floats) {
+  if (tiles >= 512) return 1;
+  const int chunks32 = k / 32;
+  if (tiles < 64 || chunks32 < 4) return 0;
+  int splits = std::min(chunks32 / 2, (768 + tiles - 1) / tiles);
+  const int per = (chunks32 + splits - 1) / splits;
+  splits = (chunks32 + per - 1) / per;
+  if (splits < 2 || static_cast<size_t>(splits) * rows * cols > scratch_floats) return 0;
+  return splits;
+}
+
 hipError_t launch_matmul_f32(const float* a, const float* bt, const float* bias, float* out,
                              int row0, int row1, int cols, int k, bool gelu, float* scratch,
                              size_t scratch_floats, hipStream_t st) {
   if (row1 <= row0 || cols <= 0) return hipSuccess;
   if (k <= 0) return hipErrorInvalidValue;
   const int rows = row1 - row0, chunks = (k + 63) / 64;
+  // large shapes on bf16 MFMA (split x3), with 16-byte rows: at least two tiles per CU, or K
+  // split over workgroups into partial sums (about 768 workgroups) from 64 tiles
+  const int x3_tiles = ((rows + kX3Rows - 1) / kX3Rows) * (cols / 128);
+  const int x3_splits = k % 32 == 0 && cols % 128 == 0 &&
+                                ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(bt)) &
+                                 15) == 0
+                            ? x3_split_count(rows, cols, k, x3_tiles, scratch ? scratch_floats : 0)
+                            : 0;
+  if (x3_splits == 1) {
+    dim3 grid((rows + kX3Rows - 1) / kX3Rows, cols / 128);
+    if (bias && gelu)
+      matmul_x3<true, true, false><<<grid, 256, 0, st>>>(a, bt, bias, out, row0, row1, cols, k, 0);
+    else if (bias)
+      matmul_x3<true, false, false><<<grid, 256, 0, st>>>(a, bt, bias, out, row0, row1, cols, k, 0);
+    else if (gelu)
+      matmul_x3<false, true, false><<<grid, 256, 0, st>>>(a, bt, nullptr, out, row0, row1, cols, k,
+                                                          0);
+    else
+      matmul_x3<false, false, false><<<grid, 256, 0, st>>>(a, bt, nullptr, out, row0, row1, cols,
+                                                           k, 0);
+    return hipGetLastError();
+  }
+  if (x3_splits > 1) {
+    const int chunks32 = k / 32, per = (chunks32 + x3_splits - 1) / x3_splits;
+    dim3 grid((rows + kX3Rows - 1) / kX3Rows, cols / 128, x3_splits);
+    matmul_x3<false, false, true><<<grid, 256, 0, st>>>(a, bt, nullptr, scratch, row0, row1, cols,
+                                                        k, per);
+    const unsigned blocks = static_cast<unsigned>((static_cast<size_t>(rows) * cols + 255) / 256);
+    if (bias && gelu)
+      dense_reduce<true, true><<<blocks, 256, 0, st>>>(scratch, bias, out, row0, rows, cols,
+                                                       x3_splits);
+    else if (bias)
+      dense_reduce<true, false><<<blocks, 256, 0, st>>>(scratch, bias, out, row0, rows, cols,
+                                                        x3_splits);
+    else if (gelu)
+      dense_reduce<false, true><<<blocks, 256, 0, st>>>(scratch, nullptr, out, row0, rows, cols,
+                                                        x3_splits);
+    else
+      dense_reduce<false, false><<<blocks, 256, 0, st>>>(scratch, nullptr, out, row0, rows, cols,
+                                                         x3_splits);
+    return hipGetLastError();
+  }
   const int splits = scratch ? dense_splits(rows, cols, k, scratch_floats) : 1;
   if (splits > 1) {
     // few output tiles (small batches): K split over workgroups, partial sums added in order

@@ -94,6 +94,66 @@ def test_f32_chunked_projections_and_bounded_tail(runtime, m, n, k, pattern):
                                rtol=5e-5)
 
 
+@pytest.mark.parametrize("rows,cols,k", [(11000, 384, 1536), (2800, 1536, 384), (10944, 384, 384),
+                                         (4000, 384, 384), (4096, 384, 1536)])
+@pytest.mark.parametrize("pattern", ["random", "cancellation", "wide range"])
+def test_large_projections_on_split_bf16_mfma(runtime, rows, cols, k, pattern):
+    """Shapes with at least 64 tiles of 64 x 128 (K % 32 == 0, N % 128 == 0) run on bf16 MFMA with
+    both operands split exactly into three bf16 terms and six products per fp32 product (below 512
+    tiles with K split into partial sums added in order); the result keeps fp32 accuracy against a
+    float64 product, through cancellation (pairs of columns that nearly cancel) and over a wide
+    exponent range (bf16 keeps fp32's exponent)."""
+    rng = np.random.default_rng(rows + cols + k)
+    x = rng.normal(size=(rows, k)).astype(np.float32)
+    w = rng.normal(scale=k ** -0.5, size=(cols, k)).astype(np.float32)
+    if pattern == "cancellation":
+        x[:, 1::2] = -x[:, ::2]
+        w[:, 1::2] = w[:, ::2] + np.float32(2**-16)
+    elif pattern == "wide range":
+        x *= np.exp2(rng.integers(-40, 40, size=(rows, 1))).astype(np.float32)
+        w *= np.exp2(rng.integers(-20, 20, size=(1, k))).astype(np.float32)
+    expected = x.astype(np.float64) @ w.astype(np.float64).T
+    got = runtime.matmul(x, np.ascontiguousarray(w.T))
+    scale = np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T
+    # fp32-grade: within a few units of 2^-24 of the sum of |products|
+    assert np.max(np.abs(got - expected) / np.maximum(scale, 1e-300)) < 2e-6
+    if pattern == "random":
+        np.testing.assert_allclose(got, expected, atol=5e-5, rtol=5e-5)
+
+
+@pytest.mark.parametrize("rows,cols,k", [(2800, 1536, 384), (11000, 384, 1536), (4000, 384, 1536)])
+def test_large_fused_projection_gelu_matches_split(runtime, rows, cols, k):
+    """The bias + GELU epilogue of the split-bf16 projection gives the bits of the projection
+    followed by the gelu_f32 launch, and both match a float64 reference."""
+    rng = np.random.default_rng(rows * 5 + k)
+    x = rng.normal(size=(rows, k)).astype(np.float32)
+    w = rng.normal(scale=k ** -0.5, size=(cols, k)).astype(np.float32)
+    bias = rng.normal(size=cols).astype(np.float32)
+
+    def run(split):
+        bufs = [runtime.upload(a) for a in (x, w, np.zeros((rows, cols), np.float32), bias)]
+        try:
+            steps = [lambda: runtime._matmul_bias_f32(bufs, rows=rows, cols=cols, k=k),
+                     lambda: runtime._dispatch("gelu_f32", [bufs[2]], threads=rows * cols,
+                                               n=rows * cols)]
+            if split:
+                for step in steps:
+                    with runtime.command():
+                        step()
+            else:
+                with runtime.command():
+                    for step in steps:
+                        step()
+            return runtime.read(bufs[2], (rows, cols))
+        finally:
+            for b in bufs:
+                b.close()
+
+    fused, split = run(False), run(True)
+    np.testing.assert_array_equal(fused, split)
+    np.testing.assert_allclose(fused, ref.gelu(ref.linear(x, w, bias)), atol=5e-5, rtol=5e-5)
+
+
 def test_f32_scalar_tail_does_not_touch_complete_rows(runtime):
     rng = np.random.default_rng(33)
     x = rng.normal(size=(15, 1536)).astype(np.float32)
@@ -199,6 +259,20 @@ def test_bge_layer_matches_oracle(runtime, batch, seq, lengths):
     got = bge_layer(runtime, x, lengths, w, heads, eps)
     expected = ref.layer(x, lengths, w, heads=heads, eps=eps)
     np.testing.assert_allclose(got, expected, atol=5e-5, rtol=5e-5)
+
+
+def test_bge_layer_at_32x512_matches_oracle_on_sampled_rows(runtime):
+    """The layer at the bge_layer_32x512 size (16,384 tokens: every projection on the split-bf16
+    kernel) against the float64 oracle on batch rows 0, 1 and 31 (rows are independent)."""
+    rng = np.random.default_rng(3232)
+    batch, seq, hidden, heads, inter, eps = 32, 512, 384, 12, 1536, 1e-12
+    x = rng.normal(size=(batch, seq, hidden)).astype(np.float32)
+    lengths = rng.integers(2, seq + 1, size=batch).astype(np.uint32)
+    w = bge_weights(rng, hidden, inter)
+    got = bge_layer(runtime, x, lengths, w, heads, eps)
+    rows = [0, 1, 31]
+    expected = ref.layer(x[rows], lengths[rows], w, heads=heads, eps=eps)
+    np.testing.assert_allclose(got[rows], expected, atol=5e-5, rtol=5e-5)
 
 
 @pytest.mark.parametrize("rows,cols,k", [(64, 1536, 384), (200, 384, 1536), (13, 96, 40)])
