@@ -318,6 +318,46 @@ __global__ __launch_bounds__(256) void layer_norm_f32(float* x, const float* r,
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= rows) return;
   float* xr = x + static_cast<size_t>(row) * cols;
+  if (cols % 64 == 0 && cols <= 512 && (!RESIDUAL || out == x)) {
+    // the row in registers (one load of x and r): the sums below add the same values in the
+    // same order as the loop further down, so both give the same bits
+    const int nv = cols / 64;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i < nv) {
+        v[i] = xr[lane + 64 * i];
+        if constexpr (RESIDUAL) v[i] = v[i] + r[static_cast<size_t>(row) * cols + lane + 64 * i];
+      }
+    }
+    float total = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (i < nv) total += v[i];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) total += __shfl_xor(total, off);
+    const float mean = total / static_cast<float>(cols);
+    float squares = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i < nv) {
+        const float d = v[i] - mean;
+        squares += d * d;
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) squares += __shfl_xor(squares, off);
+    const float inv = __frsqrt_rn(squares / static_cast<float>(cols) + eps);
+    float* orow = out + static_cast<size_t>(row) * cols;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i < nv) {
+        const int c = lane + 64 * i;
+        orow[c] = (v[i] - mean) * inv * w[c] + bias[c];
+      }
+    }
+    return;
+  }
   if constexpr (RESIDUAL) {
     const float* rr = r + static_cast<size_t>(row) * cols;
     for (int c = lane; c < cols; c += 64) xr[c] = xr[c] + rr[c];
