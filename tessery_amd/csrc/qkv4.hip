@@ -12,8 +12,9 @@
 // so the dequantized weight is never rounded to fp16: the only rounding beyond fp32
 // accumulation is the final fp16 store of y.
 // qkv4_f16 folds only acc += scale * A_g in the loop; the bias term acc += sum_g bias_g X_g is
-// one fp32 GEMM of depth K/64 on v_mfma_f32_32x32x2_f32 (row sums of 16 groups kept in LDS,
-// flushed every 16 groups).
+// one GEMM of depth K/64 (row sums of 16 groups kept in LDS, flushed every 16 groups) on bf16
+// MFMA with X_g split exactly into three bf16 terms and the bias word into one or two, so its
+// products are exact and its sums fp32.
 // The codes enter the MFMA as normal fp16 integers (1024 + c, less 1024, both exact). fp16
 // subnormal codes (c * 2^-24, one v_perm per code pair) would save half the decode, but the MFMA
 // does not sum products of subnormal operands exactly: measured against float64 they leave a
@@ -208,28 +209,47 @@ __global__ __launch_bounds__(256, 2) void qkv4_f16(Qkv4Args a) {
     for (int e = 0; e < 16; ++e) acc[k][e] = 0.0f;
   auto rtile = [&](int k) { return (wave + k) & 3; };
 
-  // bias term of groups [g0, g0 + count): acc[k][m][n] += sum_g X_g[m] * bias[n][g] on fp32 MFMA
-  // (v_mfma_f32_32x32x2_f32: k-slot kk of lane l is group g0 + 2 q + kk, kk = l / 32; its output
-  // layout is the one of the 32x32x16 tiles). Called with every wavefront past the barrier that
-  // follows the last of those groups' row sums.
-  auto flush_bias = [&](int g0, int count) {
-    // every operand first (one LDS round trip), then the MFMAs of the live pairs
-    float av[kBiasChunk / 2][4], bv[kBiasChunk / 2];
+  // bias term of groups [g0, g0 + count): acc[k][m][n] += sum_g X_g[m] * bias[n][g] on
+  // v_mfma_f32_32x32x16_bf16 (its output layout is the one of the 32x32x16 f16 tiles; k-slot j of
+  // lane l is group g0 + 8 (l / 32) + j, dead slots zero). X_g (fp32) is split exactly into three
+  // bf16 terms (split3x8) and the bias word into one (bf16 words) or two (fp16: 11 bits = 8 + 3),
+  // so every product is exact and the sums run in fp32, as on fp32 MFMA, at three or six bf16
+  // MFMAs of 32 cycles per tile where fp32 MFMA takes eight of 64. Called with every wavefront
+  // past the barrier that follows the last of those groups' row sums.
+  auto flush_bias = [&](int g0, int count) __attribute__((always_inline)) {
+    floatx4 bv[2];
 #pragma unroll
-    for (int q2 = 0; q2 < kBiasChunk / 2; ++q2) {
-      const int q = 2 * q2 + hh;  // this lane's k-slot: group g0 + q
+    for (int j = 0; j < 8; ++j) {
+      const int q = 8 * hh + j;  // this lane's k-slot j: group g0 + q
       const bool live = q < count;
       const int qc = live ? q : 0;  // a dead slot reads a live one and uses zeros
-#pragma unroll
-      for (int k = 0; k < 4; ++k) av[q2][k] = live ? xg_lds[qc][32 * rtile(k) + l32] : 0.0f;
-      bv[q2] = live ? word_value<BF16>(sbuf[128 * groups + (g0 + qc) * 128 + col]) : 0.0f;
+      bv[j >> 2][j & 3] = live ? word_value<BF16>(sbuf[128 * groups + (g0 + qc) * 128 + col]) : 0.0f;
     }
+    uint4v b1, b2, b3;
+    split3x8(bv[0], bv[1], b1, b2, b3);  // b3 is zero: a bias word has at most 11 bits
 #pragma unroll
-    for (int q2 = 0; q2 < kBiasChunk / 2; ++q2) {
-      if (2 * q2 >= count) break;  // wavefront-uniform
+    for (int k = 0; k < 4; ++k) {
+      floatx4 av[2];
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
-        acc[k] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q2][k], bv[q2], acc[k], 0, 0, 0);
+      for (int j = 0; j < 8; ++j) {
+        const int q = 8 * hh + j;
+        const bool live = q < count;
+        const int qc = live ? q : 0;
+        av[j >> 2][j & 3] = live ? xg_lds[qc][32 * rtile(k) + l32] : 0.0f;
+      }
+      uint4v x1, x2, x3;
+      split3x8(av[0], av[1], x1, x2, x3);
+      const bf16x8 a1 = __builtin_bit_cast(bf16x8, x1), a2 = __builtin_bit_cast(bf16x8, x2),
+                   a3 = __builtin_bit_cast(bf16x8, x3), c1 = __builtin_bit_cast(bf16x8, b1);
+      if constexpr (!BF16) {
+        const bf16x8 c2 = __builtin_bit_cast(bf16x8, b2);
+        acc[k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a3, c2, acc[k], 0, 0, 0);
+        acc[k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, c2, acc[k], 0, 0, 0);
+        acc[k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, c2, acc[k], 0, 0, 0);
+      }
+      acc[k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a3, c1, acc[k], 0, 0, 0);
+      acc[k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, c1, acc[k], 0, 0, 0);
+      acc[k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, c1, acc[k], 0, 0, 0);
     }
   };
 
@@ -423,8 +443,8 @@ constexpr int kHiloChunk = 16;
 //     (hi = fp16(x 2^e), lo = fp16(x 2^e - hi)), stored in the k order of
 //     decode_codes_evenodd within each 8-element chunk, and its row sums;
 //   * the fold acc += scale * A_g follows the MFMAs;
-//   * the bias term acc += sum_g bias_g X_g runs on v_mfma_f32_32x32x2_f32 over a ring of
-//     kHiloChunk row sums in LDS, flushed every kHiloChunk groups.
+//   * the bias term acc += sum_g bias_g X_g runs on bf16 MFMA (X_g split exactly into three
+//     bf16 terms) over a ring of kHiloChunk row sums in LDS, flushed every kHiloChunk groups.
 // Memory: the tile's packed weight words ride a three-stage LDS ring (global_load_lds_dwordx4,
 // group g + 2 issued during group g, the qkv4_f16 layout); the scales and biases of all groups
 // arrive in LDS once, up front, transposed to [group][column]; fp32 x is prefetched two groups
@@ -532,38 +552,52 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[set][j][e] = 0.0f;
 
-  // acc[i] += sum_{g in [g0, g0 + count)} bias[n][g] X_g[m] for row tile i (v_mfma_f32_32x32x2_f32:
-  // k-slot kk = l / 32 of lane l is group g0 + 2 q + kk); operands first, then the MFMAs. g0 is a
-  // multiple of kHiloChunk, so group g0 + q sits in row q of the row-sum ring.
-  auto flush_bias = [&](int g0, int count) {
-    float av[kHiloChunk / 2][2];
+  // acc[i] += sum_{g in [g0, g0 + count)} bias[n][g] X_g[m] for row tile i on
+  // v_mfma_f32_32x32x16_bf16 (k-slot j of lane l is group g0 + 8 (l / 32) + j, dead slots zero):
+  // X_g split exactly into three bf16 terms (split3x8) against the bias word as it is (bf16), so
+  // every product is exact and the sums run in fp32, three MFMAs of 32 cycles per tile where fp32
+  // MFMA takes eight of 64. g0 is a multiple of kHiloChunk, so group g0 + q sits in row q of the
+  // row-sum ring.
+  auto flush_bias = [&](int g0, int count) __attribute__((always_inline)) {
+    bf16x8 xa[2][3];
 #pragma unroll
-    for (int q2 = 0; q2 < kHiloChunk / 2; ++q2) {
-      const int q = 2 * q2 + hh;
-      const bool live = q < count;
-      const int qc = live ? q : 0;
+    for (int i = 0; i < 2; ++i) {
+      floatx4 av[2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        av[q2][i] = live ? xg_lds[qc][32 * i + l32] : 0.0f;
+      for (int j = 0; j < 8; ++j) {
+        const int q = 8 * hh + j;
+        const bool live = q < count;
+        const int qc = live ? q : 0;  // a dead slot reads a live one and uses zeros
+        av[j >> 2][j & 3] = live ? xg_lds[qc][32 * i + l32] : 0.0f;
+      }
+      uint4v x1, x2, x3;
+      split3x8(av[0], av[1], x1, x2, x3);
+      xa[i][0] = __builtin_bit_cast(bf16x8, x1);
+      xa[i][1] = __builtin_bit_cast(bf16x8, x2);
+      xa[i][2] = __builtin_bit_cast(bf16x8, x3);
     }
 #pragma unroll
     for (int set = 0; set < NW; ++set) {
-      float bw[kHiloChunk / 2];
       const uint16_t* sb = sbuf + set * 2 * 128 * groups;
+      uint32_t bw[4];
 #pragma unroll
-      for (int q2 = 0; q2 < kHiloChunk / 2; ++q2) {
-        const int q = 2 * q2 + hh;
-        const bool live = q < count;
-        const int qc = live ? q : 0;
-        bw[q2] = live ? bf16_to_float(sb[128 * groups + (g0 + qc) * 128 + col]) : 0.0f;
+      for (int j2 = 0; j2 < 4; ++j2) {
+        uint32_t h[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int q = 8 * hh + 2 * j2 + t;
+          const bool live = q < count;
+          const int qc = live ? q : 0;
+          h[t] = live ? sb[128 * groups + (g0 + qc) * 128 + col] : 0u;
+        }
+        bw[j2] = h[0] | (h[1] << 16);
       }
+      const bf16x8 bb = __builtin_bit_cast(bf16x8, uint4v{bw[0], bw[1], bw[2], bw[3]});
 #pragma unroll
-      for (int q2 = 0; q2 < kHiloChunk / 2; ++q2) {
-        if (2 * q2 >= count) break;  // wavefront-uniform
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-          acc[set][i] =
-              __builtin_amdgcn_mfma_f32_32x32x2f32(av[q2][i], bw[q2], acc[set][i], 0, 0, 0);
+      for (int i = 0; i < 2; ++i) {
+        acc[set][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[i][2], bb, acc[set][i], 0, 0, 0);
+        acc[set][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[i][1], bb, acc[set][i], 0, 0, 0);
+        acc[set][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[i][0], bb, acc[set][i], 0, 0, 0);
       }
     }
   };

@@ -127,3 +127,15 @@ def test_asm_load_scan_sees_an_early_read():
         ".Lfunc_end0:"])
     assert mfma_hazards.asm_load_reuse([listing.format(n=1)]) == []
     assert mfma_hazards.asm_load_reuse([listing.format(n=2)]) == [("_Zk", "v_add_f32_e32 v10, v6, v7")]
+
+
+def test_no_kernel_uses_scratch(assembly):
+    """Every kernel keeps its arrays in registers: a helper lambda that the compiler does not
+    inline takes the accumulator arrays it captures by reference into scratch memory (qkv4_f16
+    ran six times slower so, with no spill reported)."""
+    import re
+
+    sizes = {s: [int(n) for n in re.findall(r"^\s*\.amdhsa_private_segment_fixed_size (\d+)",
+                                            assembly[s], re.M)] for s in ALL_SOURCES}
+    assert sum(map(len, sizes.values())) > 40  # every kernel of the library
+    assert {s: v for s, v in sizes.items() if any(v)} == {}
