@@ -472,12 +472,7 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
   constexpr int NW = DUAL ? 2 : 1;  // weight sets
   __shared__ __attribute__((aligned(1024))) _Float16 xs[2][2][TM * 64];  // [stage][hi, lo]
   __shared__ __attribute__((aligned(1024))) uint32_t ws[NW][3][128 * 8];  // qkv4_f16 layout
-  // row sums of the last kHiloChunk groups, [row][group] in 16-byte chunks of four groups, chunk c
-  // of row r at c ^ ((r >> 2) & 3): the flush reads a row's eight groups as two 16-byte reads,
-  // and the 16 rows of a read group cover the 64 banks
-  __shared__ __attribute__((aligned(16))) float xg_lds[TM][kHiloChunk];
-  static_assert(kHiloChunk == 16, "ring rows of four 16-byte chunks");
-  auto xg_at = [](int row, int q) { return row * kHiloChunk + 4 * ((q >> 2) ^ ((row >> 2) & 3)) + (q & 3); };
+  __shared__ __attribute__((aligned(16))) float xg_lds[kHiloChunk][TM];
   // scale and bias words of the tile's 128 columns, all groups, per weight set:
   // [set][2][groups][128] (dynamic size)
   extern __shared__ __attribute__((aligned(1024))) uint16_t sbuf[];
@@ -571,14 +566,13 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
     bf16x8 xa[2][3];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int row = 32 * i + l32;
       floatx4 av[2];
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        av[c] = *reinterpret_cast<const floatx4*>(&xg_lds[0][0] + xg_at(row, 8 * hh + 4 * c));
-#pragma unroll
-        for (int t = 0; t < 4; ++t)  // dead slots (groups past the chunk) use zeros
-          if (8 * hh + 4 * c + t >= count) av[c][t] = 0.0f;
+      for (int j = 0; j < 8; ++j) {
+        const int q = 8 * hh + j;
+        const bool live = q < count;
+        const int qc = live ? q : 0;  // a dead slot reads a live one and uses zeros
+        av[j >> 2][j & 3] = live ? xg_lds[qc][32 * i + l32] : 0.0f;
       }
       uint4v x1, x2, x3;
       split3x8(av[0], av[1], x1, x2, x3);
@@ -646,7 +640,7 @@ __global__ __launch_bounds__(256, 2) void linear4_hilo(const float* __restrict__
     rsum += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(rsum), 0x4E, 0xf, 0xf, false));
     // all four threads of the row hold the same total (the sums above commute) and store it to the
     // same word: no branch around the store
-    (&xg_lds[0][0])[xg_at(srow, g % kHiloChunk)] = rsum;
+    xg_lds[g % kHiloChunk][srow] = rsum;
 
     uint4v wd[NW];
     float gs[NW];
