@@ -23,8 +23,10 @@ SOURCES = ("attention.hip", "norm_rope.hip", "linear4.hip", "qkv4.hip", "dense.h
            "util.hip", "noalloc.hip", "runtime.cpp")
 
 # Per-source flags. The attention kernels never produce NaN from finite inputs (masked scores are
-# -inf, every row has a finite maximum), so max() needs no NaN quieting.
-SOURCE_FLAGS = {"attention.hip": ("-fno-honor-nans",)}
+# -inf, every row has a finite maximum), so max() needs no NaN quieting. The max-memory-clause
+# scheduling strategy ran the fused fp16 attention 0.4-0.6 us faster per headline layer in two
+# A/B orders (the fp32 attention kernels unchanged within the spread).
+SOURCE_FLAGS = {"attention.hip": ("-fno-honor-nans", "-mllvm", "--amdgpu-sched-strategy=max-memory-clause")}
 
 # -packed-fp32-ops keeps the device compiler from emitting packed fp32 VALU instructions.
 FLAGS = (
